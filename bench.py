@@ -1,0 +1,365 @@
+#!/usr/bin/env python3
+"""Benchmark of the int8 / int8-dyn quantized-linear path on one MI355X.
+
+Headline (``value``): int8 weight-only decode at M=1 - one step is one pass
+over the fused-QKV [6144x4096], gate+up [24576x4096] and down [4096x12288]
+projections (int8 per-channel weights, fp16 activations, fp16 outputs), with
+inputs resident in HBM.  ``value`` = algorithmic bytes per step (N*K weights +
+4N scales + M*K*2 activations + M*N*2 outputs) x steps / time, in GB/s.
+Weights rotate over enough distinct copies (>= 512 MB) that the 256 MB
+Infinity Cache cannot serve them.  Each step is one HIP graph replay.
+
+Also reported (``extra``): M=4/16 decode, the 4096x4096 single GEMV (fp32 and
+fp16 activations), the prefill GEMM at M=512/2048/8192 (N=12288, K=4096,
+TFLOP/s vs the 2.5 PFLOP/s dense fp16 peak), int8-dyn at M=1/128/2048, and
+one decode step through all 539 linears of a random-init 36-layer hybrid
+model (hidden 4096, FFN 12288, vocab 151936) at M=1 and M=8.
+
+``roofline`` covers the dominant kernel (the gate+up GEMV launch): its average
+duration is measured with HIP events around a graph of back-to-back launches
+on the stream the kernel runs on.  ``cpu_baseline`` times the reference's CPU
+path (the int8 block loop of quant.py:46-53, restated with torch CPU ops) on
+the host cores for the same decode step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "spikingbrain-cpu_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "int8 W-only GEMV GB/s (%HBM peak) at M=1; prefill GEMM TFLOPS (%MFMA) M=2048"
+HBM_PEAK_GBS = 8000.0
+F16_PEAK_TFLOPS = 2500.0
+I8_PEAK_TOPS = 5000.0
+DECODE_SHAPES = [(6144, 4096), (24576, 4096), (4096, 12288)]  # fused QKV, gate+up, down
+DOMINANT = (24576, 4096)
+ROTATE_BYTES = 512 << 20
+SOFTMAX_LAYERS = (0, 1, 2, 3, 6, 12, 17, 21, 24, 35)
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(M, N, K, xbytes=2, ybytes=2):
+    return N * K + 4 * N + M * K * xbytes + M * N * ybytes
+
+
+class Ctx:
+    def __init__(self):
+        import torch
+
+        from sbq import quant
+
+        self.torch = torch
+        self.quant = quant
+        self.dev = torch.device("cuda", 0)
+        torch.cuda.set_device(self.dev)
+
+    def weights(self, N, K, seed, colsum=False):
+        """Random N(0, 0.02) weights quantized and packed on the GPU."""
+        torch = self.torch
+        g = torch.Generator(device=self.dev).manual_seed(seed)
+        w = torch.randn(N, K, generator=g, device=self.dev) * 0.02
+        q, s = self.quant.quantize_per_channel_gpu(w)
+        del w
+        packed, cs = self.quant.repack(q, with_colsum=colsum)
+        del q
+        return packed, s, cs
+
+    def act(self, M, K, seed, dtype=None, outliers=False):
+        torch = self.torch
+        g = torch.Generator(device=self.dev).manual_seed(seed)
+        x = torch.randn(M, K, generator=g, device=self.dev)
+        if outliers:
+            idx = torch.randperm(K, generator=g, device=self.dev)[: max(1, K // 100)]
+            x[:, idx] *= 20
+        return x.to(dtype or torch.float16)
+
+    def graph(self, fn):
+        torch = self.torch
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()  # warm the launch path outside capture
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return g
+
+    def time_graphs(self, graphs, steps, warmup):
+        """Replay graphs round-robin; return ms per replay (events on the
+        stream the graphs are launched on, synchronize on both sides)."""
+        torch = self.torch
+        for i in range(warmup):
+            graphs[i % len(graphs)].replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            graphs[i % len(graphs)].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+
+# ---------------------------------------------------------------------------
+# decode (weight-only GEMV)
+# ---------------------------------------------------------------------------
+def decode_setup(ctx, M, shapes, xdtype=None, seed=0):
+    torch = ctx.torch
+    step_bytes = sum(gemv_bytes(M, N, K, 4 if xdtype == torch.float32 else 2) for N, K in shapes)
+    weight_bytes = sum(N * K for N, K in shapes)
+    copies = max(1, math.ceil(ROTATE_BYTES / weight_bytes)) + (1 if weight_bytes < ROTATE_BYTES else 0)
+    layers = [[ctx.weights(N, K, seed + 17 * c + i) for i, (N, K) in enumerate(shapes)] for c in range(copies)]
+    xs = [ctx.act(M, K, 100 + i, xdtype) for i, (N, K) in enumerate(shapes)]
+    ys = [torch.empty((M, N), dtype=torch.float16, device=ctx.dev) for N, K in shapes]
+    return layers, xs, ys, step_bytes, copies
+
+
+def decode_bench(ctx, M, steps, warmup, shapes=DECODE_SHAPES, xdtype=None):
+    quant = ctx.quant
+    layers, xs, ys, step_bytes, copies = decode_setup(ctx, M, shapes, xdtype)
+
+    def step(c):
+        for (packed, s, _), x, y, (N, K) in zip(layers[c], xs, ys, shapes):
+            quant.linear_w8(x, packed, s, None, N, out=y)
+
+    graphs = [ctx.graph(lambda c=c: step(c)) for c in range(copies)]
+    ms = ctx.time_graphs(graphs, steps, warmup)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    out = {"ms_per_step": ms, "GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "bytes_per_step": step_bytes,
+           "weight_copies": copies}
+    del graphs, layers
+    return out
+
+
+def dominant_kernel(ctx, M=1, launches_per_copy=8, reps=5):
+    """Average duration of the gate+up GEMV launch: a graph of back-to-back
+    launches (rotating weight copies), HIP events around the replays."""
+    quant = ctx.quant
+    N, K = DOMINANT
+    wbytes = N * K
+    copies = math.ceil(ROTATE_BYTES / wbytes) + 1
+    layers = [ctx.weights(N, K, 500 + c) for c in range(copies)]
+    x = ctx.act(M, K, 7)
+    y = ctx.torch.empty((M, N), dtype=ctx.torch.float16, device=ctx.dev)
+
+    def run():
+        for _ in range(launches_per_copy):
+            for packed, s, _ in layers:
+                quant.linear_w8(x, packed, s, None, N, out=y)
+
+    g = ctx.graph(run)
+    n = launches_per_copy * copies
+    ms = ctx.time_graphs([g], reps, 1)
+    us = ms * 1e3 / n
+    bytes_per_launch = gemv_bytes(M, N, K)
+    return {"kernel": "sbq::gemv_w8_kernel (gate+up 24576x4096, M=1, fp16 x, fp16 y)", "avg_us": us,
+            "bytes_per_launch": bytes_per_launch, "GBps": bytes_per_launch / (us * 1e-6) / 1e9,
+            "launches": n * reps}
+
+
+# ---------------------------------------------------------------------------
+# prefill GEMM and int8-dyn
+# ---------------------------------------------------------------------------
+def prefill_bench(ctx, M, N=12288, K=4096, steps=10, warmup=3):
+    quant = ctx.quant
+    packed, s, _ = ctx.weights(N, K, 900)
+    x = ctx.act(M, K, 901)
+    y = ctx.torch.empty((M, N), dtype=ctx.torch.float16, device=ctx.dev)
+    g = ctx.graph(lambda: quant.linear_w8(x, packed, s, None, N, out=y))
+    ms = ctx.time_graphs([g], steps, warmup)
+    tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    return {"M": M, "N": N, "K": K, "ms": ms, "TFLOPs": tflops, "mfma_frac": tflops / F16_PEAK_TFLOPS}
+
+
+def w8a8_bench(ctx, M, N, K=4096, steps=10, warmup=3):
+    torch, quant = ctx.torch, ctx.quant
+    wbytes = N * K
+    copies = 1 if M >= 128 else math.ceil(ROTATE_BYTES / wbytes) + 1
+    layers = [ctx.weights(N, K, 950 + c, colsum=True) for c in range(copies)]
+    x = ctx.act(M, K, 951, outliers=True)
+    y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
+    ws = quant.w8a8_workspace(M, K, ctx.dev)
+    graphs = [ctx.graph(lambda L=L: quant.linear_w8a8(x, L[0], L[1], L[2], None, N, torch.float16,
+                                                       workspace=ws, out=y)) for L in layers]
+    ms = ctx.time_graphs(graphs, steps, warmup)
+    res = {"M": M, "N": N, "K": K, "ms": ms}
+    tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    res["TOPs"] = tops
+    res["i8_frac"] = tops / I8_PEAK_TOPS
+    res["GBps"] = gemv_bytes(M, N, K) / (ms * 1e-3) / 1e9
+    return res
+
+
+# ---------------------------------------------------------------------------
+# one decode step through every quantized linear of the 36-layer hybrid model
+# ---------------------------------------------------------------------------
+def hybrid_stack_shapes(H=4096, F=12288, heads=32, kv_heads=8, d=128, routers=4, vocab=151936, layers=36):
+    shapes = []
+    for i in range(layers):
+        if i in SOFTMAX_LAYERS:
+            shapes += [(heads * d, H), (kv_heads * d, H), (kv_heads * d, H), (H, heads * d)]
+        else:
+            shapes += [(heads * d, H)] * 3                      # sse_q, sse_k, sse_v
+            shapes += [(d, H), (d, H), (heads * d, d), (heads * d, d)]  # lora_q/k [0], [1]
+            shapes += [(2 * heads, H), (2 * heads, H), (routers, H)]   # sse_a, sse_b, sse_e
+            shapes += [(H, heads * d)]                          # sse_o
+            shapes += [(heads * d, H), (kv_heads * d, H), (kv_heads * d, H), (H, heads * d)]  # swa q,k,v,o
+        shapes += [(F, H), (F, H), (H, F)]                      # gate, up, down
+    shapes.append((vocab, H))                                   # lm_head
+    return shapes
+
+
+def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3):
+    torch, quant = ctx.torch, ctx.quant
+    shapes = hybrid_stack_shapes()
+    layers = [ctx.weights(N, K, 2000 + i) for i, (N, K) in enumerate(shapes)]
+    wbytes = sum(N * K for N, K in shapes)
+    res = {"linears": len(shapes), "weight_bytes": wbytes}
+    for M in Ms:
+        xs = {}
+        for N, K in shapes:
+            if K not in xs:
+                xs[K] = ctx.act(M, K, 3000 + K)
+        ys = [torch.empty((M, N), dtype=torch.float16, device=ctx.dev) for N, K in shapes]
+
+        def step():
+            for (packed, s, _), y, (N, K) in zip(layers, ys, shapes):
+                quant.linear_w8(xs[K], packed, s, None, N, out=y)
+
+        g = ctx.graph(step)
+        ms = ctx.time_graphs([g], steps, warmup)
+        nbytes = sum(gemv_bytes(M, N, K) for N, K in shapes)
+        res[f"M{M}"] = {"ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3), "GBps": nbytes / (ms * 1e-3) / 1e9}
+        del g, ys
+    del layers
+    return res
+
+
+# ---------------------------------------------------------------------------
+def traffic_from_profiles():
+    """HBM bytes per launch of the dominant kernel from the committed PMC
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy-kernel calibration)."""
+    p = ROOT / "profiles" / "gemv_w8_gateup_m1_traffic.json"
+    try:
+        return float(json.loads(p.read_text())["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(budget_s):
+    import torch
+
+    import oracle.cpu_baseline as cb
+
+    info = cb.cpu_info()
+    threads = info["host_threads"]
+    r_all = cb.decode_step_baseline(DECODE_SHAPES, 1, threads, budget_s)
+    r_4 = cb.decode_step_baseline(DECODE_SHAPES, 1, min(4, threads), budget_s / 2)
+    gbs = r_all["bytes_per_step"] / r_all["seconds_per_step"] / 1e9
+    torch.set_num_threads(threads)
+    return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": (f"int8 block loop of quant.py:46-53 (torch CPU restatement) over the same M=1 decode step "
+                       f"(QKV, gate+up, down), median of repetitions over ~{budget_s:.0f} s"),
+            "ms_per_step": r_all["seconds_per_step"] * 1e3,
+            "GBps_4_threads": r_4["bytes_per_step"] / r_4["seconds_per_step"] / 1e9, **info}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported in this build "
+              "(the sharding design is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs one process on one GPU; WORLD_SIZE > 1 is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    ctx = Ctx()
+    torch = ctx.torch
+    log("decode M=1 (headline)")
+    head = decode_bench(ctx, 1, args.steps, args.warmup)
+    log(f"  {head['GBps']:.0f} GB/s, {head['ms_per_step'] * 1e3:.1f} us/step")
+    dom = dominant_kernel(ctx)
+    log(f"  dominant kernel {dom['avg_us']:.2f} us, {dom['GBps']:.0f} GB/s")
+    extra = {}
+    if not args.no_extra:
+        for M in (4, 16):
+            log(f"decode M={M}")
+            extra[f"decode_M{M}"] = decode_bench(ctx, M, args.steps, args.warmup)
+        log("single 4096x4096 GEMV")
+        extra["gemv_4096_f16x"] = decode_bench(ctx, 1, args.steps, args.warmup, shapes=[(4096, 4096)])
+        extra["gemv_4096_f32x"] = decode_bench(ctx, 1, args.steps, args.warmup, shapes=[(4096, 4096)],
+                                               xdtype=torch.float32)
+        log("prefill GEMM")
+        extra["prefill"] = [prefill_bench(ctx, M) for M in (512, 2048, 8192)]
+        log("int8-dyn")
+        extra["w8a8"] = [w8a8_bench(ctx, M, N) for M in (1, 128, 2048) for N in (4096, 12288)]
+        log("36-layer linear stack")
+        extra["stack"] = stack_bench(ctx)
+        torch.cuda.empty_cache()
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
+
+    pre2048 = next((p for p in extra.get("prefill", []) if p["M"] == 2048), None)
+    line = {
+        "metric": METRIC,
+        "value": round(head["GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (random N(0,0.02) weights quantized per channel, N(0,1) activations)",
+        "config": {
+            "workload": "int8 weight-only decode step at M=1: fused QKV 6144x4096 + gate+up 24576x4096 + "
+                        "down 4096x12288, fp16 activations and outputs, weights rotating over "
+                        f"{head['weight_copies']} copies",
+            "hbm_frac": round(head["hbm_frac"], 4),
+            "prefill_M2048_TFLOPs": None if pre2048 is None else round(pre2048["TFLOPs"], 1),
+            "prefill_M2048_mfma_frac": None if pre2048 is None else round(pre2048["mfma_frac"], 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(dom["GBps"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles(),
+            "kernel": dom["kernel"],
+            "avg_us": round(dom["avg_us"], 3),
+            "bytes_per_launch": dom["bytes_per_launch"],
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,148 @@
+/*
+ * sbq.h - C ABI of the MI355X (gfx950) quantized-linear library (libsbq.so).
+ *
+ * This is the drop-in boundary for the quantized-linear hot path of
+ * spikingbrain-cpu: the `int8` (weight-only, symmetric per-output-channel
+ * int8, fp32 scales) and `int8-dyn` (W8A8 with dynamic per-tensor asymmetric
+ * uint8 activations, fbgemm semantics) formats of spikingbrain_cpu/quant.py.
+ *
+ * Conventions (all entry points):
+ *   - plain pointers and sizes only; every pointer named `d_*` or documented as
+ *     "device" is HIP device memory owned by the caller.  The library never
+ *     allocates device memory: scratch space is passed in as `workspace`.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Every call is asynchronous on that stream and reentrant: the library
+ *     keeps no mutable state between calls.
+ *   - matrices are row-major; `ld*` is the row stride in elements.
+ *   - return value: SBQ_OK (0) or a negative SBQ_ERR_* code; nothing throws.
+ *     sbq_status_string() names a code.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   sbq_quantize_per_channel  <- spikingbrain_cpu/quant.py:25-29 quantize_per_channel
+ *   sbq_repack_w8             <- spikingbrain_cpu/quant.py:33-39 Int8Linear.__init__ buffers
+ *                                and quant.py:57-61 DynamicInt8Linear.__init__ (linear_prepack)
+ *   sbq_linear_w8             <- spikingbrain_cpu/quant.py:41-53 Int8Linear.forward
+ *   sbq_act_qparams           <- spikingbrain_cpu/quant.py:65 (the per-tensor activation
+ *                                quantization parameters chosen inside
+ *                                torch.ops.quantized.linear_dynamic)
+ *   sbq_linear_w8a8           <- spikingbrain_cpu/quant.py:63-66 DynamicInt8Linear.forward
+ */
+#ifndef SBQ_H_
+#define SBQ_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define SBQ_OK 0
+#define SBQ_ERR_ARG (-1)        /* bad size / stride / null pointer           */
+#define SBQ_ERR_DTYPE (-2)      /* unsupported dtype code                      */
+#define SBQ_ERR_ALIGN (-3)      /* pointer not aligned as the entry requires   */
+#define SBQ_ERR_WORKSPACE (-4)  /* workspace missing or too small              */
+#define SBQ_ERR_LAUNCH (-5)     /* hipLaunchKernel / HIP runtime error         */
+#define SBQ_ERR_DEVICE (-6)     /* current device is not a gfx950 GPU          */
+
+/* ---- dtype codes -------------------------------------------------------- */
+#define SBQ_F32 0
+#define SBQ_F16 1
+#define SBQ_BF16 2
+
+/* Library version string, e.g. "sbq 0.1.0 gfx950". */
+const char* sbq_version(void);
+
+/* Human-readable name of a status code. */
+const char* sbq_status_string(int status);
+
+/* Checks that the current HIP device is a gfx950 part the kernels were built
+ * for.  Returns SBQ_OK or SBQ_ERR_DEVICE.  Optional: every compute entry point
+ * reports a launch failure on its own. */
+int sbq_check_device(void);
+
+/* ---- weight quantization and packing ------------------------------------ */
+
+/* quantize_per_channel (spikingbrain_cpu/quant.py:25-29):
+ *   scale[n] = max(max_k |w[n,k]|, 1e-8f) / 127.0f      (IEEE fp32 division)
+ *   q[n,k]   = clamp(rint(w[n,k] / scale[n]), -127, 127) (IEEE fp32 division,
+ *                                                         round-half-even)
+ * w: device [N, K] (row stride ldw) of dtype w_dtype (F32, F16 or BF16; the
+ * value is widened to fp32 exactly, as weight.float() does).
+ * q: device int8 [N, K] (row stride ldq).  scale: device fp32 [N]. */
+int sbq_quantize_per_channel(const void* w, int w_dtype, int64_t N, int64_t K, int64_t ldw,
+                             int8_t* q, int64_t ldq, float* scale, void* stream);
+
+/* Bytes of the packed weight layout for an [N, K] int8 matrix:
+ * round_up(N,16) * round_up(K,64).  The layout is a grid of 1 KiB tiles
+ * [N/16][K/64]; tile (nt,kc) holds rows nt*16..+15, columns kc*64..+63, with
+ * byte  lane*16 + j,  lane = g*16 + r,  equal to  q[nt*16+r][kc*64+g*16+j] ^ 0x80
+ * (offset binary, padding = 0x80 i.e. q = 0).  One tile is exactly one
+ * 64-lane x 16-byte wavefront load and one MFMA 16x16 operand fragment pair. */
+int64_t sbq_packed_bytes(int64_t N, int64_t K);
+
+/* Repack (the loader hook of spikingbrain_cpu/loader.py:46-51,94; the buffers of
+ * quant.py:33-39 and the prepack of quant.py:57-61):
+ *   q: device int8 [N, K] (row stride ldq)  ->  packed: device, sbq_packed_bytes(N,K)
+ *   colsum: device int32 [N] or NULL; colsum[n] = sum_k q[n,k]  (needed by
+ *   sbq_linear_w8a8 for the activation zero-point correction). */
+int sbq_repack_w8(const int8_t* q, int64_t N, int64_t K, int64_t ldq,
+                  uint8_t* packed, int32_t* colsum, void* stream);
+
+/* Inverse of sbq_repack_w8: packed -> q [N, K] (row stride ldq). */
+int sbq_unpack_w8(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_t ldq,
+                  void* stream);
+
+/* ---- int8 weight-only linear (Int8Linear.forward, quant.py:41-53) -------- */
+
+/* y[m,n] = (sum_k x[m,k] * q[n,k]) * scale[n] (+ bias[n])
+ * x: device [M, K] (row stride ldx), dtype F32, F16 or BF16.
+ *    F16/BF16 inputs are used exactly; F32 inputs are split into a bf16
+ *    high part and a bf16 remainder (relative representation error <= 2^-16).
+ * packed: from sbq_repack_w8.  scale: device fp32 [N].  bias: device fp32 [N]
+ * or NULL.  y: device [M, N] (row stride ldy), dtype F32, F16 or BF16.
+ * Accumulation is fp32.  M <= 16 runs the HBM-streaming MFMA GEMV; larger M
+ * runs the LDS-tiled MFMA GEMM.
+ * workspace: unused by this entry point (pass NULL, 0). */
+int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                  const uint8_t* packed, const float* scale, const float* bias, int64_t N,
+                  void* y, int y_dtype, int64_t ldy,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- int8-dyn W8A8 linear (DynamicInt8Linear.forward, quant.py:63-66) ---- */
+
+/* Workspace bytes sbq_linear_w8a8 / sbq_act_qparams need for an [M, K] input. */
+int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K);
+
+/* The activation quantization parameters that fbgemm's dynamic linear chooses
+ * for the whole tensor x [M, K] (uint8, qmin 0, qmax 255, no range reduction):
+ *   lo = min(min x, 0), hi = max(max x, 0)
+ *   scale = (double)(hi - lo) / 255, replaced by 0.1 when fp32(scale) == 0 or
+ *   1/fp32(scale) overflows; scales below 6.1e-5 are raised to 6.1e-5 with
+ *   lo/hi rescaled; zero_point chosen from lo or hi by the smaller error term
+ *   and rounded half-even (all in double), clamped to [0, 255].
+ * Results: *scale_out (device fp32[1]) and *zp_out (device int32[1]). */
+int sbq_act_qparams(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                    float* scale_out, int32_t* zp_out,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* y[m,n] = fp32(acc[m,n]) * fp32(s_x * scale[n]) (+ bias[n]) where
+ *   xq[m,k]  = clamp(rint(fma(x[m,k], 1/s_x, zp)), 0, 255)   (one rounding)
+ *   acc[m,n] = sum_k (xq[m,k] - zp) * q[n,k]                  (exact int32)
+ * which is bit-exact with torch.ops.quantized.linear_dynamic (fbgemm) on the
+ * same fp32 inputs.  colsum: from sbq_repack_w8 (required).
+ * acc_out: device int32 [M, N] (row stride N) or NULL; when given, the raw
+ * int32 accumulators are written too (the bit-exactness check).
+ * workspace: >= sbq_w8a8_workspace_bytes(M, K) bytes of device memory. */
+int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                    const uint8_t* packed, const float* scale, const int32_t* colsum,
+                    const float* bias, int64_t N,
+                    void* y, int y_dtype, int64_t ldy, int32_t* acc_out,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SBQ_H_ */

@@ -1,0 +1,89 @@
+"""CPU baseline timing of the reference path (TEST/BENCH INFRASTRUCTURE ONLY).
+
+Used only by bench.py's cpu_baseline leg.  The reference's own files never
+travel to the GPU box, so this restates, with torch CPU operators, what the
+reference executes (paths relative to the reference repository):
+
+* int8:     Int8Linear.forward, quant.py:46-53 - 128-row blocks dequantized to
+            fp32, fp32 sgemm per block, torch.cat, then * scale.
+* int8-dyn: DynamicInt8Linear.forward, quant.py:57-66 - fbgemm prepack of the
+            per-channel qint8 weight, then torch.ops.quantized.linear_dynamic.
+"""
+from __future__ import annotations
+
+import os
+import platform
+import time
+
+import numpy as np
+import torch
+
+
+def int8_forward(x2: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, block: int = 128) -> torch.Tensor:
+    parts = [x2 @ qweight[lo:lo + block].float().t() for lo in range(0, qweight.shape[0], block)]
+    return torch.cat(parts, -1) * scale
+
+
+def dyn_prepack(q: torch.Tensor, scale: torch.Tensor):
+    qw = torch._make_per_channel_quantized_tensor(q, scale.double(), torch.zeros_like(scale, dtype=torch.long), 0)
+    return torch.ops.quantized.linear_prepack(qw, None)
+
+
+def dyn_forward(x2: torch.Tensor, packed) -> torch.Tensor:
+    return torch.ops.quantized.linear_dynamic(x2.contiguous(), packed)
+
+
+def cpu_info() -> dict:
+    model = platform.processor()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu": model, "capability": torch.backends.cpu.get_cpu_capability(), "torch": torch.__version__,
+            "host_threads": len(os.sched_getaffinity(0))}
+
+
+def time_calls(fn, budget_s: float, min_reps: int = 2) -> float:
+    """Median seconds per call over repetitions filling about budget_s."""
+    fn()  # warm-up
+    times = []
+    start = time.perf_counter()
+    while len(times) < min_reps or (time.perf_counter() - start) < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 1000:
+            break
+    return float(np.median(times))
+
+
+def decode_step_baseline(shapes, M: int, threads: int, budget_s: float, seed: int = 0) -> dict:
+    """Time one pass of the int8 weight-only forward over `shapes` [(N, K)] at
+    batch M on `threads` host threads; returns seconds per step and bytes."""
+    old = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        g = torch.Generator().manual_seed(seed)
+        layers = []
+        nbytes = 0
+        for N, K in shapes:
+            w = torch.randn(N, K, generator=g) * 0.02
+            s = w.abs().amax(dim=1).clamp(min=1e-8) / 127.0
+            q = torch.round(w / s[:, None]).clamp(-127, 127).to(torch.int8)
+            x = torch.randn(M, K, generator=g).half().float()
+            layers.append((x, q, s))
+            nbytes += N * K + 4 * N + M * K * 2 + M * N * 2
+            del w
+
+        def step():
+            for x, q, s in layers:
+                int8_forward(x, q, s)
+
+        sec = time_calls(step, budget_s)
+    finally:
+        torch.set_num_threads(old)
+    return {"seconds_per_step": sec, "bytes_per_step": nbytes, "threads": threads}

@@ -1,0 +1,156 @@
+// sbq_abi.hip - the extern "C" entry points of libsbq.so (declared in
+// include/sbq.h).  Argument validation and kernel selection only: no device
+// allocation, no mutable global state, every call asynchronous on the given
+// stream.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "sbq.h"
+#include "sbq_common.h"
+#include "sbq_launch.h"
+
+namespace {
+
+constexpr int64_t kIntMax = 0x7fffffff;
+// Largest M the streaming GEMV kernel takes (four 16-row token tiles); larger
+// batches use the LDS-tiled GEMM.
+constexpr int64_t kGemvMaxM = 64;
+
+inline bool valid_dtype(int t) { return t == SBQ_F32 || t == SBQ_F16 || t == SBQ_BF16; }
+inline int64_t esize(int t) { return t == SBQ_F32 ? 4 : 2; }
+inline bool aligned(const void* p, int64_t a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+
+// Common shape / pointer checks of the linear entry points.
+int check_linear(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, const void* packed, const float* scale,
+                 int64_t N, const void* y, int yt, int64_t ldy) {
+  if (!valid_dtype(xt) || !valid_dtype(yt)) return SBQ_ERR_DTYPE;
+  if (M < 0 || N < 1 || K < 1 || M > kIntMax || N > kIntMax || K > kIntMax) return SBQ_ERR_ARG;
+  if (M == 0) return SBQ_OK;
+  if (ldx < K || ldy < N) return SBQ_ERR_ARG;
+  if (!x || !packed || !scale || !y) return SBQ_ERR_ARG;
+  if (!aligned(packed, 16)) return SBQ_ERR_ALIGN;
+  return SBQ_OK;
+}
+
+inline bool x_vec_ok(const void* x, int xt, int64_t ldx) {
+  return aligned(x, 16) && (ldx * esize(xt)) % 16 == 0;
+}
+inline bool y_vec_ok(const void* y, int yt, int64_t ldy, int64_t N) {
+  const int64_t a = 4 * esize(yt);
+  return aligned(y, a) && (ldy * esize(yt)) % a == 0 && N % 4 == 0;
+}
+
+inline float2* ws_partials(void* workspace) {
+  return (float2*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sbq_version(void) { return "sbq 0.1.0 gfx950"; }
+
+const char* sbq_status_string(int status) {
+  switch (status) {
+    case SBQ_OK: return "ok";
+    case SBQ_ERR_ARG: return "invalid argument (size, stride or null pointer)";
+    case SBQ_ERR_DTYPE: return "unsupported dtype";
+    case SBQ_ERR_ALIGN: return "pointer not 16-byte aligned";
+    case SBQ_ERR_WORKSPACE: return "workspace missing or too small";
+    case SBQ_ERR_LAUNCH: return "HIP kernel launch failed";
+    case SBQ_ERR_DEVICE: return "current device is not gfx950";
+  }
+  return "unknown status";
+}
+
+int sbq_check_device(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return SBQ_ERR_DEVICE;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return SBQ_ERR_DEVICE;
+  return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? SBQ_OK : SBQ_ERR_DEVICE;
+}
+
+int sbq_quantize_per_channel(const void* w, int w_dtype, int64_t N, int64_t K, int64_t ldw, int8_t* q, int64_t ldq,
+                             float* scale, void* stream) {
+  if (!valid_dtype(w_dtype)) return SBQ_ERR_DTYPE;
+  if (N < 0 || K < 1 || ldw < K || ldq < K) return SBQ_ERR_ARG;
+  if (N == 0) return SBQ_OK;
+  if (!w || !q || !scale) return SBQ_ERR_ARG;
+  return sbq::launch_quantize_per_channel(w, w_dtype, N, K, ldw, q, ldq, scale, (hipStream_t)stream);
+}
+
+int64_t sbq_packed_bytes(int64_t N, int64_t K) {
+  if (N < 1 || K < 1) return 0;
+  return ((N + 15) / 16) * 16 * ((K + 63) / 64) * 64;
+}
+
+int sbq_repack_w8(const int8_t* q, int64_t N, int64_t K, int64_t ldq, uint8_t* packed, int32_t* colsum,
+                  void* stream) {
+  if (N < 1 || K < 1 || ldq < K || N > kIntMax || K > kIntMax) return SBQ_ERR_ARG;
+  if (!q || !packed) return SBQ_ERR_ARG;
+  if (!aligned(packed, 16)) return SBQ_ERR_ALIGN;
+  return sbq::launch_repack(q, N, K, ldq, packed, colsum, (hipStream_t)stream);
+}
+
+int sbq_unpack_w8(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_t ldq, void* stream) {
+  if (N < 1 || K < 1 || ldq < K) return SBQ_ERR_ARG;
+  if (!q || !packed) return SBQ_ERR_ARG;
+  return sbq::launch_unpack(packed, N, K, q, ldq, (hipStream_t)stream);
+}
+
+int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
+                  const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  int rc = check_linear(x, x_dtype, M, K, ldx, packed, scale, N, y, y_dtype, ldy);
+  if (rc || M == 0) return rc;
+  const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
+  hipStream_t st = (hipStream_t)stream;
+  if (M <= kGemvMaxM) return sbq::launch_gemv_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
+  return sbq::launch_gemm_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
+}
+
+int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K) {
+  (void)M;
+  (void)K;
+  return 256 + (int64_t)sbq::kMinMaxPartials * (int64_t)sizeof(float2);
+}
+
+int sbq_act_qparams(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, float* scale_out,
+                    int32_t* zp_out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!valid_dtype(x_dtype)) return SBQ_ERR_DTYPE;
+  if (M < 1 || K < 1 || ldx < K || M > kIntMax || K > kIntMax) return SBQ_ERR_ARG;
+  if (!x || !scale_out || !zp_out) return SBQ_ERR_ARG;
+  if (!workspace || (int64_t)workspace_bytes < sbq_w8a8_workspace_bytes(M, K)) return SBQ_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  float2* parts = ws_partials(workspace);
+  const int np = sbq::minmax_nparts(M, K);
+  int rc = sbq::launch_minmax_partials(x, x_dtype, M, K, ldx, parts, np, st);
+  if (rc) return rc;
+  return sbq::launch_qparams(parts, np, scale_out, zp_out, st);
+}
+
+int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
+                    const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int y_dtype,
+                    int64_t ldy, int32_t* acc_out, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_linear(x, x_dtype, M, K, ldx, packed, scale, N, y, y_dtype, ldy);
+  if (rc || M == 0) return rc;
+  if (!colsum) return SBQ_ERR_ARG;
+  if (!workspace || (int64_t)workspace_bytes < sbq_w8a8_workspace_bytes(M, K)) return SBQ_ERR_WORKSPACE;
+  const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
+  hipStream_t st = (hipStream_t)stream;
+  float2* parts = ws_partials(workspace);
+  const int np = sbq::minmax_nparts(M, K);
+  rc = sbq::launch_minmax_partials(x, x_dtype, M, K, ldx, parts, np, st);
+  if (rc) return rc;
+  if (M <= kGemvMaxM)
+    return sbq::launch_gemv_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
+                                 parts, np, st, yv);
+  return sbq::launch_gemm_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
+                               parts, np, st, yv);
+}
+
+}  // extern "C"

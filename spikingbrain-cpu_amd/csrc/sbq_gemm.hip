@@ -1,0 +1,401 @@
+// sbq_gemm.hip - prefill (large-M) quantized linear, MFMA bound.
+//
+// Replaces spikingbrain_cpu/quant.py:41-53 (Int8Linear.forward) and
+// quant.py:63-66 (DynamicInt8Linear.forward) for the prompt chunks the model
+// feeds (model.py:439: up to 512 tokens per chunk) and larger batches.
+//
+// Block tile BN (output channels) x BM (tokens) x 64 (K per stage), WN x WM
+// waves.  Each stage copies BN/16 packed weight tiles verbatim into LDS and the
+// BM x 64 activation slab into an XOR-swizzled LDS tile; the next stage is
+// prefetched into registers while MFMAs run on the current one (two LDS
+// buffers, one barrier per stage).
+//   W-only: weights are converted int8 -> fp16/bf16 in registers (exact) and
+//           multiplied on v_mfma_f32_16x16x32_{f16,bf16}; fp32 activations run
+//           as bf16 hi + lo planes.  Epilogue: * scale[n] (+ bias[n]).
+//   W8A8:   the activation slab is quantized to s8 (xq - 128) while it is
+//           staged, weights are used as s8, v_mfma_i32_16x16x64_i8 accumulates
+//           exactly; epilogue adds (128 - zp) * colsum[n] and applies
+//           fp32(s_x * scale[n]) (+ bias[n] fused), as fbgemm does.
+#include "sbq_common.h"
+#include "sbq_launch.h"
+
+namespace sbq {
+
+// LDS activation tile for 2-byte operands: 64 K-columns per row = 8 chunks of
+// 16 bytes; chunk c of row r lives at slot c ^ (r & 7) so that the 16 rows a
+// quarter-wave reads for one fragment spread over all banks.
+__device__ __forceinline__ int xs_off(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
+// LDS activation tile for s8 operands: 64 bytes per row = 4 chunks.
+__device__ __forceinline__ int xq_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
+
+template <int XT>
+struct GemmOp;
+template <>
+struct GemmOp<XT_F16> {
+  typedef f16x8 V;
+  static constexpr int NS = 1;
+  static __device__ __forceinline__ void wconv(u32x4 w, V& a, V& b) { u8x16_to_f16(w, a, b); }
+  static __device__ __forceinline__ f32x4 mma(V a, V b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct GemmOp<XT_BF16> {
+  typedef bf16x8 V;
+  static constexpr int NS = 1;
+  static __device__ __forceinline__ void wconv(u32x4 w, V& a, V& b) { u8x16_to_bf16(w, a, b); }
+  static __device__ __forceinline__ f32x4 mma(V a, V b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct GemmOp<XT_F32> {
+  typedef bf16x8 V;
+  static constexpr int NS = 2;
+  static __device__ __forceinline__ void wconv(u32x4 w, V& a, V& b) { u8x16_to_bf16(w, a, b); }
+  static __device__ __forceinline__ f32x4 mma(V a, V b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Convert 8 fp32 activations into the operand plane(s) (16 bytes each).
+template <int XT>
+__device__ __forceinline__ void x8_to_planes(const float* t, u32x4* planes) {
+  if constexpr (XT == XT_F16) {
+    f16x8 h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (_Float16)t[j];
+    planes[0] = __builtin_bit_cast(u32x4, h);
+  } else if constexpr (XT == XT_BF16) {
+    bf16x8 h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (__bf16)t[j];
+    planes[0] = __builtin_bit_cast(u32x4, h);
+  } else {
+    bf16x8 h, l;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      __bf16 a, b;
+      split_bf16(t[j], a, b);
+      h[j] = a;
+      l[j] = b;
+    }
+    planes[0] = __builtin_bit_cast(u32x4, h);
+    planes[1] = __builtin_bit_cast(u32x4, l);
+  }
+}
+
+// Raw 16-byte chunk load for 2-byte activations on the fast path (no
+// conversion through fp32).
+template <int XT>
+__device__ __forceinline__ void load_x_chunk(const void* x, int64_t ldx, int M, int K, int m, int k0, bool xvec,
+                                             u32x4* planes) {
+  if constexpr (XT != XT_F32) {
+    if (m < M && xvec && k0 + 8 <= K) {
+      planes[0] = *(const u32x4*)((const uint16_t*)x + (int64_t)m * ldx + k0);
+      return;
+    }
+  }
+  float t[8];
+  load8_f32<XT>(x, ldx, M, K, m, k0, xvec, t);
+  x8_to_planes<XT>(t, planes);
+}
+
+template <int XT, int BN, int BM, int WN, int WM>
+__global__ __launch_bounds__(WN* WM * 64) void gemm_w8_kernel(const void* __restrict__ x, int64_t ldx, int M,
+                                                              int K, int Kc, const uint8_t* __restrict__ packed,
+                                                              const float* __restrict__ scale,
+                                                              const float* __restrict__ bias, int N, int Nt,
+                                                              void* __restrict__ y, int yt, int64_t ldy,
+                                                              int flags) {
+  typedef GemmOp<XT> Op;
+  typedef typename Op::V V;
+  constexpr int NS = Op::NS;
+  constexpr int NT = WN * WM * 64;
+  constexpr int TN = BN / WN, TM = BM / WM;
+  constexpr int FN = TN / 16, FM = TM / 16;
+  constexpr int WCH = BN * 4 / NT;  // 16-byte weight chunks per thread per stage
+  constexpr int XCH = BM * 8 / NT;  // 16-byte activation chunks (8 values) per thread per stage
+  static_assert(WCH * NT == BN * 4 && XCH * NT == BM * 8, "tile/thread mismatch");
+
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2][BN * 64];
+  __shared__ __attribute__((aligned(16))) uint8_t xl[2][NS][BM * 128];
+
+  const bool xvec = flags & 1, yvec = flags & 2;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int wn = wave / WM, wm = wave % WM;
+  const int nt0 = blockIdx.x * (BN / 16);
+  const int m0 = blockIdx.y * BM;
+
+  u32x4 wreg[WCH];
+  u32x4 xreg[XCH][NS];
+
+  auto gload = [&](int kc) {
+#pragma unroll
+    for (int i = 0; i < WCH; ++i) {
+      const int c = tid + i * NT;
+      const int j = c >> 6, slot = c & 63;
+      if (nt0 + j < Nt) wreg[i] = *(const u32x4*)(packed + ((int64_t)(nt0 + j) * Kc + kc) * 1024 + slot * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = tid + i * NT;
+      const int row = c >> 3, ch = c & 7;
+      load_x_chunk<XT>(x, ldx, M, K, m0 + row, kc * 64 + ch * 8, xvec, xreg[i]);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < WCH; ++i) {
+      const int c = tid + i * NT;
+      *(u32x4*)(&wl[buf][c * 16]) = wreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = tid + i * NT;
+      const int row = c >> 3, ch = c & 7;
+#pragma unroll
+      for (int h = 0; h < NS; ++h) *(u32x4*)(&xl[buf][h][xs_off(row, ch)]) = xreg[i][h];
+    }
+  };
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int a = 0; a < FN; ++a)
+#pragma unroll
+    for (int b = 0; b < FM; ++b) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+
+  for (int kc = 0; kc < Kc; ++kc) {
+    const int buf = kc & 1;
+    if (kc + 1 < Kc) gload(kc + 1);
+
+    V wf[FN][2];
+#pragma unroll
+    for (int a = 0; a < FN; ++a) {
+      const u32x4 w = *(const u32x4*)(&wl[buf][(wn * FN + a) * 1024 + lane * 16]);
+      Op::wconv(w, wf[a][0], wf[a][1]);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+      for (int b = 0; b < FM; ++b) {
+        const int row = wm * TM + b * 16 + r;
+        V xf[NS];
+#pragma unroll
+        for (int h = 0; h < NS; ++h) xf[h] = *(const V*)(&xl[buf][h][xs_off(row, 2 * g + s)]);
+#pragma unroll
+        for (int a = 0; a < FN; ++a) {
+#pragma unroll
+          for (int h = NS - 1; h >= 0; --h) acc[a][b] = Op::mma(wf[a][s], xf[h], acc[a][b]);
+        }
+      }
+    }
+    if (kc + 1 < Kc) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds y[m0 + wm*TM + b*16 + r][n0 + (wn*FN + a)*16 + 4g + v]
+#pragma unroll
+  for (int a = 0; a < FN; ++a) {
+    const int n = (nt0 + wn * FN + a) * 16 + 4 * g;
+    if (n >= N) continue;
+    const int nvalid = min(4, N - n);
+    f32x4 sc, bi;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int nn = min(n + v, N - 1);
+      sc[v] = scale[nn];
+      bi[v] = bias ? bias[nn] : 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < FM; ++b) {
+      const int m = m0 + wm * TM + b * 16 + r;
+      if (m >= M) continue;
+      f32x4 o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float out = acc[a][b][v] * sc[v];
+        if (bias) out = out + bi[v];
+        o[v] = out;
+      }
+      store_y4(y, yt, (int64_t)m * ldy + n, o, yvec && nvalid == 4, nvalid);
+    }
+  }
+}
+
+template <int XT, int BN, int BM, int WN, int WM>
+__global__ __launch_bounds__(WN* WM * 64) void gemm_w8a8_kernel(
+    const void* __restrict__ x, int64_t ldx, int M, int K, int Kc, const uint8_t* __restrict__ packed,
+    const float* __restrict__ scale, const int32_t* __restrict__ colsum, const float* __restrict__ bias, int N,
+    int Nt, void* __restrict__ y, int yt, int64_t ldy, int32_t* __restrict__ acc_out,
+    const float2* __restrict__ partials, int nparts, int flags) {
+  constexpr int NT = WN * WM * 64;
+  constexpr int TN = BN / WN, TM = BM / WM;
+  constexpr int FN = TN / 16, FM = TM / 16;
+  constexpr int WCH = BN * 4 / NT;
+  constexpr int XCH = BM * 4 / NT;  // 16-value chunks (16 s8 bytes) per thread
+  static_assert(WCH * NT == BN * 4 && XCH * NT == BM * 4, "tile/thread mismatch");
+
+  __shared__ __attribute__((aligned(16))) uint8_t wl[2][BN * 64];
+  __shared__ __attribute__((aligned(16))) uint8_t xl[2][BM * 64];
+  __shared__ float qred[32];
+
+  const ActQParams qp = block_qparams_from_partials(partials, nparts, qred);
+  const bool xvec = flags & 1, yvec = flags & 2;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int wn = wave / WM, wm = wave % WM;
+  const int nt0 = blockIdx.x * (BN / 16);
+  const int m0 = blockIdx.y * BM;
+
+  u32x4 wreg[WCH];
+  u32x4 xreg[XCH];
+
+  auto gload = [&](int kc) {
+#pragma unroll
+    for (int i = 0; i < WCH; ++i) {
+      const int c = tid + i * NT;
+      const int j = c >> 6, slot = c & 63;
+      if (nt0 + j < Nt) wreg[i] = *(const u32x4*)(packed + ((int64_t)(nt0 + j) * Kc + kc) * 1024 + slot * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = tid + i * NT;
+      const int row = c >> 2, ch = c & 3;
+      const int m = m0 + row, k0 = kc * 64 + ch * 16;
+      float t[16];
+      load8_f32<XT>(x, ldx, M, K, m, k0, xvec, t);
+      load8_f32<XT>(x, ldx, M, K, m, k0 + 8, xvec, t + 8);
+      uint32_t d[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int jj = 4 * p + j;
+          const int qv = (m < M && k0 + jj < K) ? quant_act_s8(t[jj], qp.inv, qp.zpf) : 0;
+          word |= ((uint32_t)qv & 0xffu) << (8 * j);
+        }
+        d[p] = word;
+      }
+      xreg[i] = (u32x4){d[0], d[1], d[2], d[3]};
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < WCH; ++i) {
+      const int c = tid + i * NT;
+      *(u32x4*)(&wl[buf][c * 16]) = wreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = tid + i * NT;
+      *(u32x4*)(&xl[buf][xq_off(c >> 2, c & 3)]) = xreg[i];
+    }
+  };
+
+  i32x4 acc[FN][FM];
+#pragma unroll
+  for (int a = 0; a < FN; ++a)
+#pragma unroll
+    for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+
+  for (int kc = 0; kc < Kc; ++kc) {
+    const int buf = kc & 1;
+    if (kc + 1 < Kc) gload(kc + 1);
+    i32x4 wf[FN];
+#pragma unroll
+    for (int a = 0; a < FN; ++a) {
+      const u32x4 w = *(const u32x4*)(&wl[buf][(wn * FN + a) * 1024 + lane * 16]);
+      wf[a] = (i32x4){(int)(w.x ^ 0x80808080u), (int)(w.y ^ 0x80808080u), (int)(w.z ^ 0x80808080u),
+                      (int)(w.w ^ 0x80808080u)};
+    }
+#pragma unroll
+    for (int b = 0; b < FM; ++b) {
+      const int row = wm * TM + b * 16 + r;
+      const i32x4 xf = *(const i32x4*)(&xl[buf][xq_off(row, g)]);
+#pragma unroll
+      for (int a = 0; a < FN; ++a) acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[a], xf, acc[a][b], 0, 0, 0);
+    }
+    if (kc + 1 < Kc) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  const int corr = 128 - qp.zp;
+#pragma unroll
+  for (int a = 0; a < FN; ++a) {
+    const int n = (nt0 + wn * FN + a) * 16 + 4 * g;
+    if (n >= N) continue;
+    const int nvalid = min(4, N - n);
+    int cs[4];
+    f32x4 mult, bi;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int nn = min(n + v, N - 1);
+      cs[v] = colsum[nn];
+      mult[v] = qp.scale * scale[nn];
+      bi[v] = bias ? bias[nn] : 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < FM; ++b) {
+      const int m = m0 + wm * TM + b * 16 + r;
+      if (m >= M) continue;
+      f32x4 o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int av = acc[a][b][v] + corr * cs[v];
+        if (acc_out && v < nvalid) acc_out[(int64_t)m * N + n + v] = av;
+        o[v] = bias ? __builtin_fmaf((float)av, mult[v], bi[v]) : (float)av * mult[v];
+      }
+      store_y4(y, yt, (int64_t)m * ldy + n, o, yvec && nvalid == 4, nvalid);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+constexpr int kBN = 128, kBM = 128, kWN = 2, kWM = 2;
+
+int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
+                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
+                   bool yvec) {
+  const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
+  dim3 grid((unsigned)((Nt + kBN / 16 - 1) / (kBN / 16)), (unsigned)((M + kBM - 1) / kBM)), block(kWN * kWM * 64);
+  const int flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
+  switch (xt) {
+    case XT_F16: hipLaunchKernelGGL((gemm_w8_kernel<XT_F16, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, flags); break;
+    case XT_BF16: hipLaunchKernelGGL((gemm_w8_kernel<XT_BF16, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, flags); break;
+    case XT_F32: hipLaunchKernelGGL((gemm_w8_kernel<XT_F32, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, flags); break;
+    default: return -2;
+  }
+  return check_launch();
+}
+
+int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
+                     const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
+                     int64_t ldy, int32_t* acc_out, const float2* partials, int nparts, hipStream_t st, bool yvec) {
+  const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
+  dim3 grid((unsigned)((Nt + kBN / 16 - 1) / (kBN / 16)), (unsigned)((M + kBM - 1) / kBM)), block(kWN * kWM * 64);
+  const int flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
+  switch (xt) {
+    case XT_F16: hipLaunchKernelGGL((gemm_w8a8_kernel<XT_F16, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, partials, nparts, flags); break;
+    case XT_BF16: hipLaunchKernelGGL((gemm_w8a8_kernel<XT_BF16, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, partials, nparts, flags); break;
+    case XT_F32: hipLaunchKernelGGL((gemm_w8a8_kernel<XT_F32, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, partials, nparts, flags); break;
+    default: return -2;
+  }
+  return check_launch();
+}
+
+}  // namespace sbq

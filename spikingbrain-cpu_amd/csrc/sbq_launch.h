@@ -1,0 +1,45 @@
+// sbq_launch.h - internal host-side launchers shared between the kernel files
+// and the C ABI (sbq_abi.hip).  Return 0 or a negative SBQ_ERR_* code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sbq {
+
+inline int check_launch() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : -5;
+}
+
+int launch_quantize_per_channel(const void* w, int wt, int64_t N, int64_t K, int64_t ldw, int8_t* q,
+                                int64_t ldq, float* scale, hipStream_t st);
+int launch_repack(const int8_t* q, int64_t N, int64_t K, int64_t ldq, uint8_t* packed, int32_t* colsum,
+                  hipStream_t st);
+int launch_unpack(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_t ldq, hipStream_t st);
+
+int minmax_nparts(int64_t M, int64_t K);
+int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, float2* partials,
+                           int nparts, hipStream_t st);
+int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t* zp_out, hipStream_t st);
+
+// Weight-only linear.  xvec: x and every row of x start 16-byte aligned (vector
+// loads allowed).  yvec: y rows are 16-byte aligned and N % 4 == 0.
+int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
+                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
+                   bool yvec);
+int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
+                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
+                   bool yvec);
+
+// W8A8 (fbgemm dynamic semantics); partials from launch_minmax_partials.
+int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
+                     const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
+                     int64_t ldy, int32_t* acc_out, const float2* partials, int nparts, hipStream_t st,
+                     bool yvec);
+int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
+                     const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
+                     int64_t ldy, int32_t* acc_out, const float2* partials, int nparts, hipStream_t st,
+                     bool yvec);
+
+}  // namespace sbq

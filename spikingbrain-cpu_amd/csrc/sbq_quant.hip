@@ -1,0 +1,190 @@
+// sbq_quant.hip - weight quantization, packing and activation statistics.
+//
+//   quantize_per_channel  (spikingbrain_cpu/quant.py:25-29)
+//   repack / unpack / colsum (the device-side form of the buffers built by
+//                            quant.py:33-39 and the prepack of quant.py:57-61)
+//   activation min/max partials (first step of fbgemm's dynamic quantization,
+//                                reached from quant.py:65)
+#include "sbq_common.h"
+#include "sbq_launch.h"
+
+namespace sbq {
+
+// One wavefront per weight row: exact max|w| reduction, then IEEE fp32
+// divisions and round-half-even, matching torch's CPU expression.
+template <int WT>
+__global__ __launch_bounds__(256) void quantize_per_channel_kernel(const void* __restrict__ wv, int64_t N,
+                                                                   int64_t K, int64_t ldw,
+                                                                   int8_t* __restrict__ q, int64_t ldq,
+                                                                   float* __restrict__ scale) {
+  typedef typename XElem<WT>::T T;
+  const T* w = (const T*)wv;
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const T* row = w + n * ldw;
+  float amax = 0.0f;
+  for (int64_t k = lane; k < K; k += 64) amax = fmaxf(amax, __builtin_fabsf(XElem<WT>::to_f32(row[k])));
+  amax = wave_max(amax);
+  const float s = fmaxf(amax, 1e-8f) / 127.0f;
+  if (lane == 0) scale[n] = s;
+  int8_t* qrow = q + n * ldq;
+  for (int64_t k = lane; k < K; k += 64) {
+    float t = __builtin_rintf(XElem<WT>::to_f32(row[k]) / s);
+    t = fminf(fmaxf(t, -127.0f), 127.0f);
+    qrow[k] = (int8_t)(int)t;
+  }
+}
+
+// One thread per 16-byte lane slot of the packed layout.
+__global__ __launch_bounds__(256) void repack_kernel(const int8_t* __restrict__ q, int64_t N, int64_t K,
+                                                     int64_t ldq, int64_t Kc, int64_t nslots,
+                                                     uint8_t* __restrict__ packed) {
+  const int64_t slot = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (slot >= nslots) return;
+  const int lane = (int)(slot & 63);
+  const int64_t tile = slot >> 6;
+  const int64_t nt = tile / Kc, kc = tile % Kc;
+  const int64_t n = nt * 16 + (lane & 15);
+  const int64_t k0 = kc * 64 + (lane >> 4) * 16;
+  uint32_t d[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t k = k0 + i * 4 + j;
+      const uint32_t b = (n < N && k < K) ? (uint32_t)(uint8_t)q[n * ldq + k] : 0u;
+      word |= ((b ^ 0x80u) & 0xffu) << (8 * j);
+    }
+    d[i] = word;
+  }
+  *(u32x4*)(packed + slot * 16) = (u32x4){d[0], d[1], d[2], d[3]};
+}
+
+__global__ __launch_bounds__(256) void unpack_kernel(const uint8_t* __restrict__ packed, int64_t N, int64_t K,
+                                                     int64_t Kc, int8_t* __restrict__ q, int64_t ldq) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= N * K) return;
+  const int64_t n = idx / K, k = idx % K;
+  const int64_t nt = n >> 4, r = n & 15, kc = k >> 6, g = (k & 63) >> 4, j = k & 15;
+  const uint8_t u = packed[((nt * Kc + kc) * 64 + g * 16 + r) * 16 + j];
+  q[n * ldq + k] = (int8_t)(u ^ 0x80u);
+}
+
+// colsum[n] = sum_k q[n,k]  (exact int32: |sum| <= 127 * K).
+__global__ __launch_bounds__(256) void colsum_kernel(const int8_t* __restrict__ q, int64_t N, int64_t K,
+                                                     int64_t ldq, int32_t* __restrict__ colsum) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  int s = 0;
+  for (int64_t k = lane; k < K; k += 64) s += (int)q[n * ldq + k];
+  s = wave_sum_i(s);
+  if (lane == 0) colsum[n] = s;
+}
+
+// Per-block (min, max) of x [M, K]; block b covers flat rows/columns
+// b, b + gridDim.x, ... in 256-element strides.
+template <int XT>
+__global__ __launch_bounds__(256) void minmax_partial_kernel(const void* __restrict__ xv, int64_t M, int64_t K,
+                                                             int64_t ldx, float2* __restrict__ partials) {
+  typedef typename XElem<XT>::T T;
+  const T* x = (const T*)xv;
+  float mn = 0.0f, mx = 0.0f;
+  const int64_t total = M * K;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / K, k = i - m * K;
+    const float v = XElem<XT>::to_f32(x[m * ldx + k]);
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+  }
+  __shared__ float red[8];
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  const int wid = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[2 * wid] = mn;
+    red[2 * wid + 1] = mx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) {
+      mn = fminf(mn, red[2 * w]);
+      mx = fmaxf(mx, red[2 * w + 1]);
+    }
+    partials[blockIdx.x] = make_float2(mn, mx);
+  }
+}
+
+__global__ __launch_bounds__(256) void qparams_kernel(const float2* __restrict__ partials, int nparts,
+                                                      float* __restrict__ scale_out, int32_t* __restrict__ zp_out) {
+  __shared__ float red[8];
+  ActQParams p = block_qparams_from_partials(partials, nparts, red);
+  if (threadIdx.x == 0) {
+    *scale_out = p.scale;
+    *zp_out = p.zp;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+int launch_quantize_per_channel(const void* w, int wt, int64_t N, int64_t K, int64_t ldw, int8_t* q,
+                                int64_t ldq, float* scale, hipStream_t st) {
+  dim3 grid((unsigned)((N + 3) / 4)), block(256);
+  switch (wt) {
+    case XT_F32: hipLaunchKernelGGL(quantize_per_channel_kernel<XT_F32>, grid, block, 0, st, w, N, K, ldw, q, ldq, scale); break;
+    case XT_F16: hipLaunchKernelGGL(quantize_per_channel_kernel<XT_F16>, grid, block, 0, st, w, N, K, ldw, q, ldq, scale); break;
+    case XT_BF16: hipLaunchKernelGGL(quantize_per_channel_kernel<XT_BF16>, grid, block, 0, st, w, N, K, ldw, q, ldq, scale); break;
+    default: return -2;
+  }
+  return check_launch();
+}
+
+int launch_repack(const int8_t* q, int64_t N, int64_t K, int64_t ldq, uint8_t* packed, int32_t* colsum,
+                  hipStream_t st) {
+  const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
+  const int64_t nslots = Nt * Kc * 64;
+  hipLaunchKernelGGL(repack_kernel, dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, st, q, N, K, ldq, Kc,
+                     nslots, packed);
+  int rc = check_launch();
+  if (rc || !colsum) return rc;
+  hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, q, N, K, ldq, colsum);
+  return check_launch();
+}
+
+int launch_unpack(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_t ldq, hipStream_t st) {
+  const int64_t Kc = (K + 63) / 64;
+  const int64_t total = N * K;
+  hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, packed, N, K, Kc, q,
+                     ldq);
+  return check_launch();
+}
+
+int minmax_nparts(int64_t M, int64_t K) {
+  const int64_t total = M * K;
+  int64_t p = (total + 4095) / 4096;  // >= 16 elements per thread
+  if (p < 1) p = 1;
+  if (p > kMinMaxPartials) p = kMinMaxPartials;
+  return (int)p;
+}
+
+int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, float2* partials,
+                           int nparts, hipStream_t st) {
+  dim3 grid((unsigned)nparts), block(256);
+  switch (xt) {
+    case XT_F32: hipLaunchKernelGGL(minmax_partial_kernel<XT_F32>, grid, block, 0, st, x, M, K, ldx, partials); break;
+    case XT_F16: hipLaunchKernelGGL(minmax_partial_kernel<XT_F16>, grid, block, 0, st, x, M, K, ldx, partials); break;
+    case XT_BF16: hipLaunchKernelGGL(minmax_partial_kernel<XT_BF16>, grid, block, 0, st, x, M, K, ldx, partials); break;
+    default: return -2;
+  }
+  return check_launch();
+}
+
+int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t* zp_out, hipStream_t st) {
+  hipLaunchKernelGGL(qparams_kernel, dim3(1), dim3(256), 0, st, partials, nparts, scale_out, zp_out);
+  return check_launch();
+}
+
+}  // namespace sbq

@@ -1,0 +1,330 @@
+"""Weight storage formats for linear layers, MI355X (gfx950) edition.
+
+Drop-in for ``spikingbrain_cpu/quant.py`` (same names, arguments, attributes
+and errors; paths relative to the reference repository).  The two quantized
+formats run on hand-written gfx950 kernels through libsbq.so:
+
+``int8``      symmetric per-output-channel int8 weights with fp32 scales,
+              weight-only (quant.py:32-53).  Decode shapes stream the packed
+              weights from HBM through MFMA; prefill shapes use an LDS-tiled
+              MFMA GEMM.  fp16/bf16 activations are used exactly, fp32
+              activations as bf16 hi + lo.
+``int8-dyn``  int8 weights with activations quantized per tensor at run time
+              (quant.py:56-66): the fbgemm dynamic-linear arithmetic,
+              reproduced bit for bit (uint8 activations, exact int32
+              accumulation on i8 MFMA, fp32 epilogue).
+``float32`` / ``bfloat16`` / ``float16``
+              plain torch GPU linears kept so that ``make_linear`` accepts every
+              format the reference does; they are not part of the quantized
+              path.
+
+Device placement: modules are built on the GPU that holds the weight (the
+current GPU for a CPU weight).  ``forward`` accepts a GPU tensor on that device
+or a CPU tensor; a CPU input is copied to the GPU and the result copied back,
+so the module also works inside the CPU-resident reference model.  Without a
+ROCm GPU every entry point raises: there is no CPU implementation here.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+
+FORMATS = ("float32", "bfloat16", "float16", "int8", "int8-dyn")
+
+_DTYPE_CODE = {torch.float32: _lib.SBQ_F32, torch.float16: _lib.SBQ_F16, torch.bfloat16: _lib.SBQ_BF16}
+
+
+# ---------------------------------------------------------------------------
+# device plumbing
+# ---------------------------------------------------------------------------
+def _gpu_for(t: torch.Tensor) -> torch.device:
+    if t.is_cuda:
+        return t.device
+    if not torch.cuda.is_available():
+        raise RuntimeError("sbq: no ROCm GPU is available; the quantized formats run only on gfx950 GPUs")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise ValueError(f"sbq: unsupported dtype {dtype}; expected float32, float16 or bfloat16") from None
+
+
+def _as_activation(x2: torch.Tensor) -> torch.Tensor:
+    if x2.dtype not in _DTYPE_CODE:
+        x2 = x2.float()
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return x2
+
+
+# ---------------------------------------------------------------------------
+# functional API over the C ABI (GPU tensors in, GPU tensors out)
+# ---------------------------------------------------------------------------
+def quantize_per_channel_gpu(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """quant.py:25-29 on the GPU: (int8 [N,K], fp32 scale [N])."""
+    if weight.dim() != 2:
+        raise ValueError("quantize_per_channel expects a 2-D weight")
+    w = weight if weight.dtype in _DTYPE_CODE else weight.float()
+    if w.stride(-1) != 1:
+        w = w.contiguous()
+    N, K = w.shape
+    q = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    scale = torch.empty((N,), dtype=torch.float32, device=w.device)
+    with torch.cuda.device(w.device):
+        _lib.check(_lib.load().sbq_quantize_per_channel(_ptr(w), _code(w.dtype), N, K, w.stride(0), _ptr(q),
+                                                        q.stride(0), _ptr(scale), _stream(w.device)),
+                   "sbq_quantize_per_channel")
+    return q, scale
+
+
+def repack(q: torch.Tensor, with_colsum: bool = True) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """int8 [N,K] (GPU) -> (packed uint8 tiles, int32 colsum [N] or None)."""
+    if q.dtype != torch.int8 or q.dim() != 2 or not q.is_cuda:
+        raise ValueError("repack expects a 2-D int8 GPU tensor")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    N, K = q.shape
+    L = _lib.load()
+    packed = torch.empty((L.sbq_packed_bytes(N, K),), dtype=torch.uint8, device=q.device)
+    colsum = torch.empty((N,), dtype=torch.int32, device=q.device) if with_colsum else None
+    with torch.cuda.device(q.device):
+        _lib.check(L.sbq_repack_w8(_ptr(q), N, K, q.stride(0), _ptr(packed), _ptr(colsum), _stream(q.device)),
+                   "sbq_repack_w8")
+    return packed, colsum
+
+
+def unpack(packed: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    q = torch.empty((N, K), dtype=torch.int8, device=packed.device)
+    with torch.cuda.device(packed.device):
+        _lib.check(_lib.load().sbq_unpack_w8(_ptr(packed), N, K, _ptr(q), K, _stream(packed.device)),
+                   "sbq_unpack_w8")
+    return q
+
+
+def linear_w8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None, N: int,
+              out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = (x2 @ q^T) * scale (+ bias) for x2 [M, K] on the GPU."""
+    x2 = _as_activation(x2)
+    M, K = x2.shape
+    y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x2.device)
+    with torch.cuda.device(x2.device):
+        _lib.check(_lib.load().sbq_linear_w8(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
+                                             _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype), y.stride(0),
+                                             None, 0, _stream(x2.device)),
+                   "sbq_linear_w8")
+    return y
+
+
+def w8a8_workspace(M: int, K: int, device: torch.device) -> torch.Tensor:
+    n = _lib.load().sbq_w8a8_workspace_bytes(M, K)
+    return torch.empty((n,), dtype=torch.uint8, device=device)
+
+
+def linear_w8a8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, colsum: torch.Tensor,
+                bias: torch.Tensor | None, N: int, out_dtype: torch.dtype = torch.float32,
+                acc_out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """fbgemm dynamic linear (per-tensor asymmetric uint8 activations)."""
+    x2 = _as_activation(x2)
+    M, K = x2.shape
+    y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x2.device)
+    ws = workspace if workspace is not None else w8a8_workspace(M, K, x2.device)
+    if acc_out is not None and (acc_out.dtype != torch.int32 or tuple(acc_out.shape) != (M, N)
+                                or not acc_out.is_contiguous()):
+        raise ValueError("acc_out must be a contiguous int32 [M, N] tensor")
+    with torch.cuda.device(x2.device):
+        _lib.check(_lib.load().sbq_linear_w8a8(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
+                                               _ptr(scale), _ptr(colsum), _ptr(bias), N, _ptr(y), _code(y.dtype),
+                                               y.stride(0), _ptr(acc_out), _ptr(ws), ws.numel(),
+                                               _stream(x2.device)),
+                   "sbq_linear_w8a8")
+    return y
+
+
+def act_qparams(x2: torch.Tensor) -> tuple[float, int]:
+    """The per-tensor (scale, zero_point) the int8-dyn path uses for x2 [M, K]."""
+    x2 = _as_activation(x2)
+    M, K = x2.shape
+    s = torch.empty((1,), dtype=torch.float32, device=x2.device)
+    z = torch.empty((1,), dtype=torch.int32, device=x2.device)
+    ws = w8a8_workspace(M, K, x2.device)
+    with torch.cuda.device(x2.device):
+        _lib.check(_lib.load().sbq_act_qparams(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(s), _ptr(z),
+                                               _ptr(ws), ws.numel(), _stream(x2.device)),
+                   "sbq_act_qparams")
+    return float(s.item()), int(z.item())
+
+
+# ---------------------------------------------------------------------------
+# reference API (spikingbrain_cpu/quant.py)
+# ---------------------------------------------------------------------------
+def quantize_per_channel(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """quant.py:25-29.  Runs on the GPU; results are returned on the weight's
+    device (a CPU weight is uploaded, quantized, and the results copied back)."""
+    q, scale = quantize_per_channel_gpu(weight.to(_gpu_for(weight)))
+    if not weight.is_cuda:
+        q, scale = q.cpu(), scale.cpu()
+    return q, scale
+
+
+def _run_on_device(x: torch.Tensor, device: torch.device, fn):
+    """Run fn on x moved to `device`; return the result on x's device."""
+    if x.device == device:
+        return fn(x)
+    if x.is_cuda:
+        raise ValueError(f"sbq: input on {x.device} but the layer lives on {device}")
+    return fn(x.to(device, non_blocking=False)).cpu()
+
+
+class Int8Linear(nn.Module):
+    """quant.py:32-53.  Buffers ``qweight`` (int8 [N,K]) and ``scale`` (fp32
+    [N]) as in the reference state_dict; ``packed`` is the tiled device layout
+    the kernels stream (not persisted).  ``block`` is kept for API parity: the
+    GPU kernels need no block-wise dequantization."""
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, block: int = 128):
+        super().__init__()
+        device = _gpu_for(weight)
+        q, scale = quantize_per_channel_gpu(weight.to(device))
+        self.register_buffer("qweight", q)
+        self.register_buffer("scale", scale)
+        self.bias = None if bias is None else nn.Parameter(bias.to(device).float(), requires_grad=False)
+        self.block = block
+        packed, _ = repack(q, with_colsum=False)
+        self.register_buffer("packed", packed, persistent=False)
+        self.out_dtype = torch.float32
+
+    @property
+    def in_features(self) -> int:
+        return self.qweight.shape[1]
+
+    @property
+    def out_features(self) -> int:
+        return self.qweight.shape[0]
+
+    def _refresh(self):
+        # packed follows qweight across .to()/.cuda(); rebuild if it was lost
+        if self.packed.device != self.qweight.device or self.packed.numel() == 0:
+            self.packed = repack(self.qweight, with_colsum=False)[0]
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not self.qweight.is_cuda:
+            raise RuntimeError("sbq Int8Linear: weights are on the CPU; move the module to a ROCm GPU")
+        self._refresh()
+        shape = x.shape
+        N = self.out_features
+
+        def run(xd):
+            x2 = xd.reshape(-1, shape[-1])
+            scale = self.scale if self.scale.dtype == torch.float32 else self.scale.float()
+            bias = None if self.bias is None else self.bias.float()
+            return linear_w8(x2, self.packed, scale, bias, N, self.out_dtype)
+
+        out = _run_on_device(x, self.qweight.device, run)
+        return out.reshape(*shape[:-1], -1)
+
+
+class DynamicInt8Linear(nn.Module):
+    """quant.py:56-66.  The reference keeps only an opaque fbgemm prepacked
+    weight (``packed``) and no state_dict entries; here ``packed`` is the tiled
+    device layout and ``scale``/``colsum`` are non-persistent buffers."""
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None):
+        super().__init__()
+        device = _gpu_for(weight)
+        q, scale = quantize_per_channel_gpu(weight.to(device))
+        packed, colsum = repack(q, with_colsum=True)
+        self.register_buffer("packed", packed, persistent=False)
+        self.register_buffer("scale", scale, persistent=False)
+        self.register_buffer("colsum", colsum, persistent=False)
+        self.register_buffer("bias", None if bias is None else bias.to(device).float(), persistent=False)
+        self.in_features = q.shape[1]
+        self.out_features = q.shape[0]
+        self.out_dtype = torch.float32
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not self.packed.is_cuda:
+            raise RuntimeError("sbq DynamicInt8Linear: weights are on the CPU; move the module to a ROCm GPU")
+        shape = x.shape
+
+        def run(xd):
+            x2 = xd.reshape(-1, shape[-1])
+            scale = self.scale if self.scale.dtype == torch.float32 else self.scale.float()
+            return linear_w8a8(x2, self.packed, scale, self.colsum, self.bias, self.out_features, self.out_dtype)
+
+        out = _run_on_device(x, self.packed.device, run)
+        return out.reshape(*shape[:-1], -1)
+
+
+class FP16Linear(nn.Module):
+    """quant.py:69-77 (fp16 weights, fp32 activations): plain torch GPU linear,
+    outside the quantized path."""
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None):
+        super().__init__()
+        device = _gpu_for(weight)
+        self.register_buffer("weight", weight.to(device=device, dtype=torch.float16).contiguous())
+        self.bias = None if bias is None else nn.Parameter(bias.to(device).float(), requires_grad=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return _run_on_device(x, self.weight.device,
+                              lambda xd: F.linear(xd.float(), self.weight.float(), self.bias))
+
+
+class BF16Linear(nn.Module):
+    """quant.py:80-87: plain torch GPU bf16 linear, outside the quantized path."""
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None):
+        super().__init__()
+        device = _gpu_for(weight)
+        self.register_buffer("weight", weight.to(device=device, dtype=torch.bfloat16).contiguous())
+        self.bias = None if bias is None else nn.Parameter(bias.to(device=device, dtype=torch.bfloat16),
+                                                           requires_grad=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return _run_on_device(x, self.weight.device,
+                              lambda xd: F.linear(xd.to(torch.bfloat16), self.weight, self.bias).float())
+
+
+class FloatLinear(nn.Module):
+    """quant.py:90-97: plain torch GPU fp32 linear, outside the quantized path."""
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None):
+        super().__init__()
+        device = _gpu_for(weight)
+        self.register_buffer("weight", weight.to(device=device, dtype=torch.float32).contiguous())
+        self.bias = None if bias is None else nn.Parameter(bias.to(device).float(), requires_grad=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return _run_on_device(x, self.weight.device, lambda xd: F.linear(xd.float(), self.weight, self.bias))
+
+
+def make_linear(fmt: str, weight: torch.Tensor, bias: torch.Tensor | None = None) -> nn.Module:
+    """quant.py:100-111 - same dispatch and the same ValueError for unknown formats."""
+    if fmt == "float32":
+        return FloatLinear(weight, bias)
+    if fmt == "bfloat16":
+        return BF16Linear(weight, bias)
+    if fmt == "float16":
+        return FP16Linear(weight, bias)
+    if fmt == "int8":
+        return Int8Linear(weight, bias)
+    if fmt == "int8-dyn":
+        return DynamicInt8Linear(weight, bias)
+    raise ValueError("unknown weight format " + fmt)

@@ -1,0 +1,90 @@
+"""CPU checks of the C ABI: libsbq.so loads, exports every entry point that
+include/sbq.h declares, and rejects bad arguments before touching a GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "sbq.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sbq_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from sbq import _lib
+
+    return _lib.load()
+
+
+def test_header_declares_the_expected_entry_points():
+    syms = declared_symbols()
+    for s in ("sbq_quantize_per_channel", "sbq_repack_w8", "sbq_linear_w8", "sbq_linear_w8a8", "sbq_act_qparams"):
+        assert s in syms
+
+
+def test_every_declared_symbol_is_exported(lib):
+    from sbq import _lib
+
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+    assert set(_lib.SIGNATURES) == set(declared_symbols())
+
+
+def test_version_and_status_strings(lib):
+    assert lib.sbq_version().decode().startswith("sbq ")
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        assert lib.sbq_status_string(code).decode() != "unknown status"
+    assert lib.sbq_status_string(-99).decode() == "unknown status"
+
+
+def test_packed_bytes(lib):
+    assert lib.sbq_packed_bytes(4096, 4096) == 4096 * 4096
+    assert lib.sbq_packed_bytes(4, 4096) == 16 * 4096
+    assert lib.sbq_packed_bytes(151936, 4096) == 151936 * 4096
+    assert lib.sbq_packed_bytes(13, 200) == 16 * 256
+    assert lib.sbq_packed_bytes(0, 5) == 0
+    assert lib.sbq_w8a8_workspace_bytes(1, 4096) >= 256 * 8
+
+
+def test_argument_validation_without_gpu(lib):
+    P = ctypes.c_void_p
+    dummy = P(4096)  # never dereferenced: every call below fails validation first
+    # unknown activation dtype
+    assert lib.sbq_linear_w8(dummy, 7, 1, 64, 64, dummy, dummy, None, 16, dummy, 0, 16, None, 0, None) == -2
+    # N < 1, K < 1, ldx < K
+    assert lib.sbq_linear_w8(dummy, 0, 1, 64, 64, dummy, dummy, None, 0, dummy, 0, 16, None, 0, None) == -1
+    assert lib.sbq_linear_w8(dummy, 0, 1, 0, 64, dummy, dummy, None, 16, dummy, 0, 16, None, 0, None) == -1
+    assert lib.sbq_linear_w8(dummy, 0, 1, 64, 32, dummy, dummy, None, 16, dummy, 0, 16, None, 0, None) == -1
+    # M == 0 is a no-op
+    assert lib.sbq_linear_w8(None, 0, 0, 64, 64, None, None, None, 16, None, 0, 16, None, 0, None) == 0
+    # null pointers, misaligned packed weights
+    assert lib.sbq_linear_w8(None, 0, 1, 64, 64, dummy, dummy, None, 16, dummy, 0, 16, None, 0, None) == -1
+    assert lib.sbq_linear_w8(dummy, 0, 1, 64, 64, P(4097), dummy, None, 16, dummy, 0, 16, None, 0, None) == -3
+    # W8A8 needs colsum and a workspace
+    assert lib.sbq_linear_w8a8(dummy, 0, 1, 64, 64, dummy, dummy, None, None, 16, dummy, 0, 16, None, dummy,
+                               4096, None) == -1
+    assert lib.sbq_linear_w8a8(dummy, 0, 1, 64, 64, dummy, dummy, dummy, None, 16, dummy, 0, 16, None, None,
+                               0, None) == -4
+    assert lib.sbq_linear_w8a8(dummy, 0, 1, 64, 64, dummy, dummy, dummy, None, 16, dummy, 0, 16, None, dummy,
+                               16, None) == -4
+    assert lib.sbq_quantize_per_channel(dummy, 5, 4, 4, 4, dummy, 4, dummy, None) == -2
+    assert lib.sbq_repack_w8(dummy, 4, 64, 32, dummy, None, None) == -1
+    assert lib.sbq_act_qparams(dummy, 0, 1, 64, 64, dummy, dummy, None, 0, None) == -4
+
+
+def test_python_binding_maps_status_to_exceptions():
+    from sbq import _lib
+
+    _lib.check(0, "ok")
+    with pytest.raises(ValueError, match="unsupported dtype"):
+        _lib.check(-2, "x")
+    with pytest.raises(_lib.SbqError, match="launch failed"):
+        _lib.check(-5, "x")

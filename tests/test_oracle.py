@@ -1,0 +1,249 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+
+Each oracle function is checked against something it does not share code
+with: torch's CPU operators evaluating the reference expressions
+(spikingbrain_cpu/quant.py:25-29, :47-52), the live fbgemm operator
+torch.ops.quantized.linear_dynamic (quant.py:65), the committed golden
+fixtures, and closed forms (integer-valued activations make every dot product
+exact).  Planted mistakes - in copies of the oracle's arithmetic, on the CPU -
+must be caught by the same checks.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def torch_quantize(w):
+    w = torch.as_tensor(w).float()
+    scale = w.abs().amax(dim=1).clamp(min=1e-8) / 127.0
+    q = torch.round(w / scale[:, None]).clamp(-127, 127).to(torch.int8)
+    return q.numpy(), scale.numpy()
+
+
+def torch_dyn(x, q, scale, bias=None):
+    qw = torch._make_per_channel_quantized_tensor(torch.as_tensor(q), torch.as_tensor(scale).double(),
+                                                  torch.zeros(len(scale), dtype=torch.long), 0)
+    packed = torch.ops.quantized.linear_prepack(qw, None if bias is None else torch.as_tensor(bias))
+    return torch.ops.quantized.linear_dynamic(torch.as_tensor(x).contiguous(), packed).numpy()
+
+
+def rand_x(M, K, seed, outliers=True, scale=1.0):
+    g = np.random.default_rng(seed)
+    x = (g.standard_normal((M, K)) * scale).astype(np.float32)
+    if outliers:
+        idx = g.permutation(K)[: max(1, K // 100)]
+        x[:, idx] *= 20
+    return x
+
+
+def rand_q(N, K, seed):
+    g = np.random.default_rng(seed)
+    return oracle.quantize_per_channel((g.standard_normal((N, K)) * 0.02).astype(np.float32))
+
+
+# ---------------------------------------------------------------------------
+# quantize_per_channel (quant.py:25-29)
+# ---------------------------------------------------------------------------
+def test_quantize_matches_golden_fixture():
+    d = np.load(GOLD / "quantize_per_channel.npz")
+    for impl in (oracle.quantize_per_channel, oracle.quantize_per_channel_c):
+        q, s = impl(d["f32_w"])
+        np.testing.assert_array_equal(q, d["f32_q"])
+        np.testing.assert_array_equal(s.view(np.uint32), d["f32_scale"].view(np.uint32))
+        wb = torch.from_numpy(d["bf16_w_bits"]).view(torch.bfloat16).float().numpy()
+        q, s = impl(wb)
+        np.testing.assert_array_equal(q, d["bf16_q"])
+        np.testing.assert_array_equal(s.view(np.uint32), d["bf16_scale"].view(np.uint32))
+
+
+def test_quantize_fixture_has_ties_and_zero_row():
+    d = np.load(GOLD / "quantize_per_channel.npz")
+    w, s = d["f32_w"][5], d["f32_scale"][5]
+    t = w / s
+    ties = np.abs(t - np.trunc(t)) == 0.5
+    assert ties.sum() >= 200
+    # round-half-even on every tie
+    assert np.all(d["f32_q"][5][ties] % 2 == 0)
+    assert np.all(d["f32_q"][3] == 0) and d["f32_scale"][3] == np.float32(np.float32(1e-8) / np.float32(127))
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_quantize_matches_torch_live(seed):
+    g = np.random.default_rng(seed)
+    w = (g.standard_normal((257, 300)) * 0.02).astype(np.float32)
+    w[0] = 0
+    qt, st = torch_quantize(w)
+    for impl in (oracle.quantize_per_channel, oracle.quantize_per_channel_c):
+        q, s = impl(w)
+        np.testing.assert_array_equal(q, qt)
+        np.testing.assert_array_equal(s, st)
+
+
+def test_quantize_mutants_are_caught():
+    """Plausible slips: the scale formed by reciprocal multiply instead of IEEE
+    division, and round-half-away-from-zero instead of half-even."""
+    d = np.load(GOLD / "quantize_per_channel.npz")
+    w = d["f32_w"]
+    s = d["f32_scale"]
+    away = np.clip(np.sign(w / s[:, None]) * np.floor(np.abs(w / s[:, None]) + 0.5), -127, 127).astype(np.int8)
+    assert not np.array_equal(away, d["f32_q"])
+    big = (np.random.default_rng(9).standard_normal((4096, 512)) * 0.02).astype(np.float32)
+    _, st = torch_quantize(big)
+    amax = np.abs(big).max(axis=1)
+    s_recip = (amax * (np.float32(1) / np.float32(127))).astype(np.float32)
+    assert not np.array_equal(s_recip, st)
+    _, so = oracle.quantize_per_channel_c(big)
+    np.testing.assert_array_equal(so, st)
+
+
+# ---------------------------------------------------------------------------
+# Int8Linear.forward (quant.py:41-53)
+# ---------------------------------------------------------------------------
+def test_int8_linear_golden_fixture():
+    d = np.load(GOLD / "int8_linear.npz")
+    for i in range(len(d["cases"])):
+        x, q, s, y = d[f"c{i}_x"], d[f"c{i}_q"], d[f"c{i}_scale"], d[f"c{i}_y"]
+        assert oracle.rel_l2(oracle.int8_linear(x, q, s), y) < 1e-6
+        assert oracle.rel_l2(oracle.int8_linear_c(x, q, s), y) < 1e-6
+
+
+def test_int8_linear_exact_on_integer_activations():
+    """With small-integer x every dot product is an exact integer, so the
+    result is fixed bit for bit: fp32(sum) * scale, scale applied last."""
+    g = np.random.default_rng(4)
+    q, s = rand_q(96, 512, 5)
+    x = g.integers(-3, 4, size=(9, 512)).astype(np.float32)
+    exact = (x.astype(np.int64) @ q.astype(np.int64).T).astype(np.float32) * s
+    np.testing.assert_array_equal(oracle.int8_linear(x, q, s), exact)
+    np.testing.assert_array_equal(oracle.int8_linear_c(x, q, s), exact)
+    # the torch block loop of the reference agrees exactly too
+    yt = (torch.from_numpy(x) @ torch.from_numpy(q).float().t() * torch.from_numpy(s)).numpy()
+    np.testing.assert_array_equal(yt, exact)
+    # planted mistake: scale folded into the weights before the sum
+    folded = (x @ (q.astype(np.float32) * s[:, None]).T).astype(np.float32)
+    assert not np.array_equal(folded, exact)
+
+
+def test_int8_linear_transposed_operand_mutant_caught():
+    q, s = rand_q(256, 256, 7)
+    x = rand_x(4, 256, 8, outliers=False)
+    good = oracle.int8_linear(x, q, s)
+    bad = (x.astype(np.float64) @ q.astype(np.float64)).astype(np.float32) * s
+    assert oracle.rel_l2(bad, good) > 0.5
+
+
+def test_int8_linear_bias_and_batch_shape():
+    q, s = rand_q(40, 128, 11)
+    x = rand_x(6, 128, 12, outliers=False).reshape(2, 3, 128)
+    b = np.random.default_rng(13).standard_normal(40).astype(np.float32)
+    y = oracle.int8_linear(x, q, s, b)
+    assert y.shape == (2, 3, 40)
+    ref = torch.from_numpy(x.reshape(6, 128)) @ torch.from_numpy(q).float().t() * torch.from_numpy(s) + torch.from_numpy(b)
+    assert oracle.rel_l2(y.reshape(6, 40), ref.numpy()) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# int8-dyn (fbgemm dynamic linear, quant.py:63-66)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K,seed", [(1, 512, 4096, 0), (128, 512, 4096, 1), (2048, 64, 4096, 2), (5, 4, 4096, 3),
+                                        (3, 64, 2560, 4), (7, 13, 256, 5), (33, 1024, 256, 6), (17, 128, 96, 7)])
+def test_dyn_bit_exact_vs_fbgemm(M, N, K, seed):
+    x = rand_x(M, K, seed)
+    q, s = rand_q(N, K, seed + 100)
+    np.testing.assert_array_equal(oracle.dyn_linear(x, q, s), torch_dyn(x, q, s))
+
+
+@pytest.mark.parametrize("kind", ["zeros", "tiny", "tinypos", "tinyneg", "positive", "negative", "const", "huge"])
+def test_dyn_edge_inputs_bit_exact(kind):
+    g = np.random.default_rng(42)
+    x = g.standard_normal((4, 512)).astype(np.float32)
+    x = {"zeros": x * 0, "tiny": x * 1e-6, "tinypos": np.abs(x) * 1e-6, "tinyneg": -np.abs(x) * 1e-6,
+         "positive": np.abs(x) + 1, "negative": -np.abs(x) - 1, "const": np.full_like(x, 0.37),
+         "huge": x * 3e4}[kind].astype(np.float32)
+    q, s = rand_q(24, 512, 43)
+    np.testing.assert_array_equal(oracle.dyn_linear(x, q, s), torch_dyn(x, q, s))
+
+
+def test_dyn_bias_is_fused_like_fbgemm():
+    x = rand_x(64, 512, 50)
+    q, s = rand_q(96, 512, 51)
+    b = np.random.default_rng(52).standard_normal(96).astype(np.float32)
+    ref = torch_dyn(x, q, s, b)
+    np.testing.assert_array_equal(oracle.dyn_linear(x, q, s, b), ref)
+    # planted mistake: bias added after a separately rounded product
+    sep = (oracle.dyn_linear(x, q, s) + b).astype(np.float32)
+    assert not np.array_equal(sep, ref)
+
+
+def test_dyn_golden_fixture():
+    d = np.load(GOLD / "int8_dyn.npz")
+    for i, kind in enumerate(d["kinds"]):
+        bias = d[f"c{i}_bias"] if f"c{i}_bias" in d else None
+        y = oracle.dyn_linear(d[f"c{i}_x"], d[f"c{i}_q"], d[f"c{i}_scale"], bias)
+        np.testing.assert_array_equal(y, d[f"c{i}_y"], err_msg=str(kind))
+
+
+def test_dyn_c_and_numpy_layers_agree():
+    x = rand_x(9, 700, 60)
+    q, s = rand_q(33, 700, 61)
+    b = np.random.default_rng(62).standard_normal(33).astype(np.float32)
+    yn, info_n = oracle.dyn_linear(x, q, s, b, return_intermediates=True)
+    yc, info_c = oracle.dyn_linear_c(x, q, s, b)
+    np.testing.assert_array_equal(yn, yc)
+    np.testing.assert_array_equal(info_n["xq"], info_c["xq"])
+    np.testing.assert_array_equal(info_n["acc"], info_c["acc"])
+    assert (info_n["scale"], info_n["zero_point"]) == (info_c["scale"], info_c["zero_point"])
+
+
+def test_dyn_mutants_are_caught():
+    """Quantizing as rint(x*inv)+zp (two roundings) and epilogue (acc*s_x)*s_w
+    are the plausible misreadings of fbgemm; both must disagree with it."""
+    x = rand_x(2048, 1024, 70)
+    q, s = rand_q(64, 1024, 71)
+    ref = torch_dyn(x, q, s)
+    _, info = oracle.dyn_linear(x, q, s, return_intermediates=True)
+    sx, zp = info["scale"], info["zero_point"]
+    inv = np.float32(1) / np.float32(sx)
+    xq_bad = np.clip(np.rint(x * inv) + zp, 0, 255)
+    acc_bad = ((xq_bad.astype(np.float64) - zp) @ q.astype(np.float64).T).astype(np.int32)
+    y_bad = acc_bad.astype(np.float32) * (np.float32(sx) * s)
+    assert not np.array_equal(y_bad, ref)
+    y_bad2 = (info["acc"].astype(np.float32) * np.float32(sx)) * s
+    assert not np.array_equal(y_bad2.astype(np.float32), ref)
+
+
+def test_dyn_acc_is_exact_integer_gemm():
+    x = rand_x(16, 4096, 80)
+    q, s = rand_q(32, 4096, 81)
+    _, info = oracle.dyn_linear(x, q, s, return_intermediates=True)
+    exact = (info["xq"].astype(np.int64) - info["zero_point"]) @ q.astype(np.int64).T
+    np.testing.assert_array_equal(info["acc"], exact.astype(np.int32))
+    # independent route: torch's int8 GEMM on xq - 128, plus the shift times
+    # the weight row sums
+    xs = torch.from_numpy((info["xq"].astype(np.int16) - 128).astype(np.int8))
+    ti = torch._int_mm(xs, torch.from_numpy(q).t().contiguous()).numpy().astype(np.int64)
+    colsum = q.astype(np.int64).sum(axis=1)
+    np.testing.assert_array_equal(ti + (128 - info["zero_point"]) * colsum, exact)
+
+
+# ---------------------------------------------------------------------------
+# packed layout model
+# ---------------------------------------------------------------------------
+def test_pack_layout_model():
+    q = (np.arange(20 * 70) % 251 - 125).astype(np.int8).reshape(20, 70)
+    p = oracle.pack_w8(q)
+    assert p.size == 32 * 128
+    Kc = 2
+    for n, k in [(0, 0), (5, 17), (15, 63), (16, 64), (19, 69), (3, 40)]:
+        nt, r, kc, g, j = n // 16, n % 16, k // 64, (k % 64) // 16, k % 16
+        off = ((nt * Kc + kc) * 64 + g * 16 + r) * 16 + j
+        assert p[off] == (int(q[n, k]) & 0xFF) ^ 0x80
+    # padding decodes to q = 0
+    off = ((1 * Kc + 1) * 64 + 0 * 16 + 10) * 16 + 0  # row 26 (padded)
+    assert p[off] == 0x80

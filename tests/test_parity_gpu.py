@@ -1,0 +1,286 @@
+"""GPU parity of the HIP path against the CPU oracle (run on the MI355X box).
+
+Bars (written in each test):
+  * quantize_per_channel, repack, int8-dyn int32 accumulators and outputs:
+    bit-exact.
+  * int8 weight-only outputs: relative L2 <= 1e-3 against the oracle (the
+    fp32-accumulation tolerance of the path; fp16/bf16 activations are used
+    exactly, fp32 activations as bf16 hi + lo).
+Full-size shapes are checked on sampled output rows (the oracle on all rows
+would take minutes); int8-dyn parameters always come from the whole tensor.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import announce
+from sbq import quant
+
+pytestmark = pytest.mark.gpu
+
+GOLD = Path(__file__).resolve().parent / "golden"
+W8_TOL = 1e-3
+
+DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def make_weights(N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(N, K, generator=g) * 0.02
+
+
+def make_x(M, K, seed, outliers=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    if outliers:
+        idx = torch.randperm(K, generator=g)[: max(1, K // 100)]
+        x[:, idx] *= 20
+    return x
+
+
+# ---------------------------------------------------------------------------
+# quantize_per_channel + repack
+# ---------------------------------------------------------------------------
+def test_quantize_golden_bitexact(dev):
+    announce("quantize golden fixture")
+    d = np.load(GOLD / "quantize_per_channel.npz")
+    q, s = quant.quantize_per_channel_gpu(torch.from_numpy(d["f32_w"]).to(dev))
+    np.testing.assert_array_equal(q.cpu().numpy(), d["f32_q"])
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), d["f32_scale"].view(np.uint32))
+    wb = torch.from_numpy(d["bf16_w_bits"]).view(torch.bfloat16)
+    q, s = quant.quantize_per_channel_gpu(wb.to(dev))
+    np.testing.assert_array_equal(q.cpu().numpy(), d["bf16_q"])
+    np.testing.assert_array_equal(s.cpu().numpy(), d["bf16_scale"])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("N,K", [(1, 1), (5, 3), (257, 300), (1024, 4096)])
+def test_quantize_bitexact(dev, dtype, N, K):
+    announce(f"quantize {dtype} {N}x{K}")
+    w = make_weights(N, K, N * 7 + K).to(DT[dtype])
+    if N > 2:
+        w[1] = 0
+    q, s = quant.quantize_per_channel_gpu(w.to(dev))
+    qo, so = oracle.quantize_per_channel_c(w.float().numpy())
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)
+    np.testing.assert_array_equal(s.cpu().numpy(), so)
+
+
+def test_quantize_reference_api_returns_on_weight_device(dev):
+    announce("quantize api devices")
+    w = make_weights(33, 70, 5)
+    q, s = quant.quantize_per_channel(w)
+    assert q.device.type == "cpu" and q.dtype == torch.int8 and s.dtype == torch.float32
+    qo, so = oracle.quantize_per_channel(w.numpy())
+    np.testing.assert_array_equal(q.numpy(), qo)
+    q2, _ = quant.quantize_per_channel(w.to(dev))
+    assert q2.is_cuda
+
+
+@pytest.mark.parametrize("N,K", [(4, 4096), (13, 200), (64, 96), (16, 64), (4096, 128), (130, 2560)])
+def test_repack_roundtrip_and_colsum(dev, N, K):
+    announce(f"repack {N}x{K}")
+    g = torch.Generator().manual_seed(N + K)
+    q = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    packed, colsum = quant.repack(q.to(dev))
+    np.testing.assert_array_equal(packed.cpu().numpy(), oracle.pack_w8(q.numpy()))
+    np.testing.assert_array_equal(colsum.cpu().numpy(), q.numpy().astype(np.int64).sum(1))
+    np.testing.assert_array_equal(quant.unpack(packed, N, K).cpu().numpy(), q.numpy())
+
+
+# ---------------------------------------------------------------------------
+# int8 weight-only
+# ---------------------------------------------------------------------------
+W8_CASES = [
+    # (M, N, K): decode GEMV (M <= 64) and prefill GEMM (M > 64), odd shapes of
+    # the real checkpoint (router N=4, lora K=128, K=2560) and tails.
+    (1, 4096, 4096), (1, 4, 2560), (1, 64, 4096), (1, 4096, 128), (2, 200, 96), (4, 6144, 256),
+    (16, 1024, 4096), (17, 300, 512), (33, 96, 1000), (64, 512, 2560),
+    (65, 256, 512), (128, 1024, 1024), (200, 130, 4096), (512, 2048, 512), (300, 13, 200),
+]
+
+
+@pytest.mark.parametrize("xd", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("M,N,K", W8_CASES)
+def test_w8_parity(dev, M, N, K, xd):
+    announce(f"w8 M={M} N={N} K={K} x={xd}")
+    w = make_weights(N, K, 1000 + N + K)
+    x = make_x(M, K, 2000 + M + K).to(DT[xd])
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref = oracle.int8_linear(x.float().numpy(), q, s)
+    lin = quant.Int8Linear(w, None)
+    y = lin(x.to(dev))
+    assert y.dtype == torch.float32 and y.shape == (M, N) and y.is_contiguous()
+    err = oracle.rel_l2(y.cpu().numpy(), ref)
+    assert err <= W8_TOL, err
+    if xd != "f32":
+        assert err <= 2e-6, err  # exact inputs: only fp32 summation order differs
+
+
+@pytest.mark.parametrize("yd", ["f16", "bf16"])
+@pytest.mark.parametrize("M", [1, 9, 100])
+def test_w8_low_precision_output(dev, M, yd):
+    announce(f"w8 out={yd} M={M}")
+    N, K = 264, 1024
+    w = make_weights(N, K, 7)
+    x = make_x(M, K, 8).half()
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref = oracle.int8_linear(x.float().numpy(), q, s)
+    lin = quant.Int8Linear(w, None)
+    y = quant.linear_w8(x.to(dev), lin.packed, lin.scale, None, N, DT[yd])
+    assert y.dtype == DT[yd]
+    assert oracle.rel_l2(y.float().cpu().numpy(), ref) <= 4e-3
+
+
+def test_w8_bias_and_strided_input(dev):
+    announce("w8 bias + strided")
+    N, K, M = 96, 512, 20
+    w = make_weights(N, K, 9)
+    b = torch.randn(N)
+    big = make_x(M, K + 64, 10)
+    x = big[:, 32:32 + K]  # row stride K + 64, 16-byte aligned rows
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref = oracle.int8_linear(x.numpy(), q, s, b.numpy())
+    lin = quant.Int8Linear(w, b)
+    x_dev = big.to(dev)[:, 32:32 + K]
+    y = quant.linear_w8(x_dev, lin.packed, lin.scale, lin.bias, N)
+    assert oracle.rel_l2(y.cpu().numpy(), ref) <= 1e-5
+    # misaligned row start (offset of one element) takes the scalar path
+    x_dev2 = big.to(dev)[:, 1:1 + K]
+    ref2 = oracle.int8_linear(big[:, 1:1 + K].numpy(), q, s, b.numpy())
+    y2 = quant.linear_w8(x_dev2, lin.packed, lin.scale, lin.bias, N)
+    assert oracle.rel_l2(y2.cpu().numpy(), ref2) <= 1e-5
+
+
+def test_w8_golden_fixture(dev):
+    announce("w8 golden fixture")
+    d = np.load(GOLD / "int8_linear.npz")
+    for i in range(len(d["cases"])):
+        x, q, s, y = d[f"c{i}_x"], d[f"c{i}_q"], d[f"c{i}_scale"], d[f"c{i}_y"]
+        packed, _ = quant.repack(torch.from_numpy(q).to(dev))
+        out = quant.linear_w8(torch.from_numpy(x).to(dev), packed, torch.from_numpy(s).to(dev), None, q.shape[0])
+        assert oracle.rel_l2(out.cpu().numpy(), y) <= 1e-5, i
+
+
+def test_w8_integer_activations_exact(dev):
+    """Small-integer activations: every product and partial sum is exact in
+    fp32, so the GPU result must equal fp32(sum) * scale bit for bit."""
+    announce("w8 integer activations")
+    N, K, M = 200, 1024, 12
+    w = make_weights(N, K, 11)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randint(-3, 4, (M, K), generator=g).half()
+    q, s = oracle.quantize_per_channel(w.numpy())
+    exact = (x.numpy().astype(np.int64) @ q.astype(np.int64).T).astype(np.float32) * s
+    lin = quant.Int8Linear(w, None)
+    np.testing.assert_array_equal(lin(x.to(dev)).cpu().numpy(), exact)
+    xb = x.float().repeat(8, 1).half()  # M = 96 -> GEMM path
+    exact_b = np.tile(exact, (8, 1))
+    np.testing.assert_array_equal(lin(xb.to(dev)).cpu().numpy(), exact_b)
+
+
+# ---------------------------------------------------------------------------
+# int8-dyn (W8A8, fbgemm semantics): bit-exact
+# ---------------------------------------------------------------------------
+W8A8_CASES = [(1, 4096, 4096), (1, 4, 2560), (5, 64, 4096), (16, 13, 96), (33, 512, 256), (64, 100, 1000),
+              (65, 64, 4096), (128, 1024, 4096), (300, 130, 200)]
+
+
+@pytest.mark.parametrize("xd", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("M,N,K", W8A8_CASES)
+def test_w8a8_bitexact(dev, M, N, K, xd):
+    announce(f"w8a8 M={M} N={N} K={K} x={xd}")
+    w = make_weights(N, K, 3000 + N + K)
+    x = make_x(M, K, 4000 + M + K, outliers=True).to(DT[xd])
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref, info = oracle.dyn_linear(x.float().numpy(), q, s, return_intermediates=True)
+    lin = quant.DynamicInt8Linear(w, None)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y = quant.linear_w8a8(x.to(dev), lin.packed, lin.scale, lin.colsum, None, N, acc_out=acc)
+    np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
+    np.testing.assert_array_equal(y.cpu().numpy(), ref)
+    sx, zp = quant.act_qparams(x.to(dev))
+    assert (np.float32(sx), zp) == (np.float32(info["scale"]), info["zero_point"])
+
+
+def test_w8a8_golden_fixture(dev):
+    announce("w8a8 golden fixture")
+    d = np.load(GOLD / "int8_dyn.npz")
+    for i, kind in enumerate(d["kinds"]):
+        x, q, s, yref = d[f"c{i}_x"], d[f"c{i}_q"], d[f"c{i}_scale"], d[f"c{i}_y"]
+        bias = torch.from_numpy(d[f"c{i}_bias"]).to(dev) if f"c{i}_bias" in d else None
+        packed, colsum = quant.repack(torch.from_numpy(q).to(dev))
+        y = quant.linear_w8a8(torch.from_numpy(x).to(dev), packed, torch.from_numpy(s).to(dev), colsum, bias,
+                              q.shape[0])
+        np.testing.assert_array_equal(y.cpu().numpy(), yref, err_msg=str(kind))
+
+
+@pytest.mark.parametrize("kind", ["zeros", "tiny", "tinypos", "tinyneg", "positive", "negative", "const", "huge"])
+def test_w8a8_qparams_edge_cases(dev, kind):
+    announce(f"qparams {kind}")
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(6, 700, generator=g)
+    x = {"zeros": x * 0, "tiny": x * 1e-6, "tinypos": x.abs() * 1e-6, "tinyneg": -x.abs() * 1e-6,
+         "positive": x.abs() + 1, "negative": -x.abs() - 1, "const": torch.full_like(x, 0.37),
+         "huge": x * 3e4}[kind]
+    sx, zp = quant.act_qparams(x.to(dev))
+    so, zo = oracle.act_qparams(x.numpy())
+    assert (np.float32(sx), zp) == (np.float32(so), zo)
+    w = make_weights(40, 700, 6)
+    q, s = oracle.quantize_per_channel(w.numpy())
+    lin = quant.DynamicInt8Linear(w, None)
+    np.testing.assert_array_equal(lin(x.to(dev)).cpu().numpy(), oracle.dyn_linear(x.numpy(), q, s))
+
+
+def test_w8a8_bias_fused(dev):
+    announce("w8a8 bias")
+    N, K = 72, 512
+    w = make_weights(N, K, 21)
+    b = torch.randn(N)
+    for M in (3, 150):
+        x = make_x(M, K, 22 + M, outliers=True)
+        q, s = oracle.quantize_per_channel(w.numpy())
+        lin = quant.DynamicInt8Linear(w, b)
+        np.testing.assert_array_equal(lin(x.to(dev)).cpu().numpy(), oracle.dyn_linear(x.numpy(), q, s, b.numpy()))
+
+
+# ---------------------------------------------------------------------------
+# full-size shapes (sampled rows)
+# ---------------------------------------------------------------------------
+FULL_W8 = [(1, 4096, 4096), (1, 6144, 4096), (4, 24576, 4096), (16, 4096, 12288), (2048, 12288, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", FULL_W8)
+def test_w8_full_size_sampled(dev, M, N, K):
+    announce(f"w8 full M={M} N={N} K={K}")
+    w = (torch.randn(N, K, generator=torch.Generator().manual_seed(0)) * 0.02)
+    x = make_x(M, K, 1).half()
+    lin = quant.Int8Linear(w.to(dev), None)
+    y = lin(x.to(dev)).cpu().numpy()
+    q = lin.qweight.cpu().numpy()
+    s = lin.scale.cpu().numpy()
+    rows = np.unique(np.linspace(0, M - 1, min(M, 24)).astype(int))
+    ref = oracle.int8_linear(x.float().numpy()[rows], q, s)
+    assert oracle.rel_l2(y[rows], ref) <= 2e-6
+
+
+@pytest.mark.parametrize("M,N", [(1, 4096), (128, 12288), (2048, 12288)])
+def test_w8a8_full_size_sampled(dev, M, N):
+    announce(f"w8a8 full M={M} N={N}")
+    K = 4096
+    w = torch.randn(N, K, generator=torch.Generator().manual_seed(0)) * 0.02
+    x = make_x(M, K, 1, outliers=True).half()
+    lin = quant.DynamicInt8Linear(w.to(dev), None)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y = quant.linear_w8a8(x.to(dev), lin.packed, lin.scale, lin.colsum, None, N, acc_out=acc)
+    q, s = oracle.quantize_per_channel(w.numpy())
+    xf = x.float().numpy()
+    sx, zp = oracle.act_qparams(xf)  # parameters of the WHOLE tensor
+    rows = np.unique(np.linspace(0, M - 1, min(M, 24)).astype(int))
+    xq = oracle.quantize_act(xf[rows], sx, zp)
+    acc_ref = ((xq.astype(np.int64) - zp) @ q.astype(np.int64).T).astype(np.int32)
+    np.testing.assert_array_equal(acc.cpu().numpy()[rows], acc_ref)
+    np.testing.assert_array_equal(y.cpu().numpy()[rows], oracle.dyn_epilogue(acc_ref, sx, s))
