@@ -7,7 +7,8 @@ projections (int8 per-channel weights, fp16 activations, fp16 outputs), with
 inputs resident in HBM.  ``value`` = algorithmic bytes per step (N*K weights +
 4N scales + M*K*2 activations + M*N*2 outputs) x steps / time, in GB/s.
 Weights rotate over enough distinct copies (>= 512 MB) that the 256 MB
-Infinity Cache cannot serve them.  Each step is one HIP graph replay.
+Infinity Cache cannot serve them.  The steps run as HIP graph replays, one
+graph holding one step per weight copy.
 
 Also reported (``extra``): M=4/16 decode, the 4096x4096 single GEMV (fp32 and
 fp16 activations), the prefill GEMM at M=512/2048/8192 (N=12288, K=4096,
@@ -114,6 +115,28 @@ class Ctx:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps
 
+    def time_steps(self, step, copies, steps, warmup):
+        """ms per step for exactly `steps` steps; step(c) runs one step on weight
+        copy c.  One graph holds `copies` consecutive steps (so the host replays
+        once per `copies` steps); a second graph holds the remainder."""
+        torch = self.torch
+        full = self.graph(lambda: [step(c) for c in range(copies)])
+        rem_n = steps % copies
+        rem = self.graph(lambda: [step(c) for c in range(rem_n)]) if rem_n else None
+        for _ in range(max(1, -(-warmup // copies))):
+            full.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps // copies):
+            full.replay()
+        if rem is not None:
+            rem.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
 
 # ---------------------------------------------------------------------------
 # decode (weight-only GEMV)
@@ -137,12 +160,11 @@ def decode_bench(ctx, M, steps, warmup, shapes=DECODE_SHAPES, xdtype=None):
         for (packed, s, _), x, y, (N, K) in zip(layers[c], xs, ys, shapes):
             quant.linear_w8(x, packed, s, None, N, out=y)
 
-    graphs = [ctx.graph(lambda c=c: step(c)) for c in range(copies)]
-    ms = ctx.time_graphs(graphs, steps, warmup)
+    ms = ctx.time_steps(step, copies, steps, warmup)
     gbs = step_bytes / (ms * 1e-3) / 1e9
     out = {"ms_per_step": ms, "GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "bytes_per_step": step_bytes,
            "weight_copies": copies}
-    del graphs, layers
+    del layers
     return out
 
 
@@ -180,8 +202,7 @@ def prefill_bench(ctx, M, N=12288, K=4096, steps=10, warmup=3):
     packed, s, _ = ctx.weights(N, K, 900)
     x = ctx.act(M, K, 901)
     y = ctx.torch.empty((M, N), dtype=ctx.torch.float16, device=ctx.dev)
-    g = ctx.graph(lambda: quant.linear_w8(x, packed, s, None, N, out=y))
-    ms = ctx.time_graphs([g], steps, warmup)
+    ms = ctx.time_steps(lambda c: quant.linear_w8(x, packed, s, None, N, out=y), 1, steps, warmup)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     return {"M": M, "N": N, "K": K, "ms": ms, "TFLOPs": tflops, "mfma_frac": tflops / F16_PEAK_TFLOPS}
 
@@ -194,9 +215,11 @@ def w8a8_bench(ctx, M, N, K=4096, steps=10, warmup=3):
     x = ctx.act(M, K, 951, outliers=True)
     y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
     ws = quant.w8a8_workspace(M, K, ctx.dev)
-    graphs = [ctx.graph(lambda L=L: quant.linear_w8a8(x, L[0], L[1], L[2], None, N, torch.float16,
-                                                       workspace=ws, out=y)) for L in layers]
-    ms = ctx.time_graphs(graphs, steps, warmup)
+    def step(c):
+        L = layers[c]
+        quant.linear_w8a8(x, L[0], L[1], L[2], None, N, torch.float16, workspace=ws, out=y)
+
+    ms = ctx.time_steps(step, copies, max(steps, copies), warmup)
     res = {"M": M, "N": N, "K": K, "ms": ms}
     tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     res["TOPs"] = tops

@@ -13,9 +13,6 @@
 namespace {
 
 constexpr int64_t kIntMax = 0x7fffffff;
-// Largest M the streaming GEMV kernel takes (four 16-row token tiles); larger
-// batches use the LDS-tiled GEMM.
-constexpr int64_t kGemvMaxM = 64;
 
 inline bool valid_dtype(int t) { return t == SBQ_F32 || t == SBQ_F16 || t == SBQ_BF16; }
 inline int64_t esize(int t) { return t == SBQ_F32 ? 4 : 2; }
@@ -109,7 +106,7 @@ int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
   if (rc || M == 0) return rc;
   const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
   hipStream_t st = (hipStream_t)stream;
-  if (M <= kGemvMaxM) return sbq::launch_gemv_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
+  if (sbq::gemv_supports(M, K, false, x_dtype)) return sbq::launch_gemv_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
   return sbq::launch_gemm_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
 }
 
@@ -146,7 +143,7 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
   const int np = sbq::minmax_nparts(M, K);
   rc = sbq::launch_minmax_partials(x, x_dtype, M, K, ldx, parts, np, st);
   if (rc) return rc;
-  if (M <= kGemvMaxM)
+  if (sbq::gemv_supports(M, K, true, x_dtype))
     return sbq::launch_gemv_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
                                  parts, np, st, yv);
   return sbq::launch_gemm_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,

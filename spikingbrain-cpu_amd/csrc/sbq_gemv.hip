@@ -5,212 +5,161 @@
 // W8A8) at the decode shapes the engine issues (engine.py:106: M = 1).
 //
 // Work decomposition: a workgroup owns G consecutive 16-row weight tiles and
-// splits K over its waves; each wave streams its contiguous run of 1 KiB
-// packed tiles (one 16-byte non-temporal load per lane per tile), converts
-// them in registers and feeds MFMA 16x16 instructions with the activation
-// fragment as the second operand.  The per-wave partial tiles are summed in
-// LDS in a fixed wave order (deterministic), then scale/bias are applied and
-// four consecutive outputs per lane are stored as one vector.
+// splits K over its (up to 16) waves, P 64-wide K tiles per wave.  A wave
+// issues every one of its G*P 1 KiB tile loads (16 bytes per lane,
+// non-temporal) before it consumes any, so a kernel has its whole working set
+// in flight at once instead of one round trip per K step.  The activation
+// fragments are loaded before the weights: loads retire in order, so waiting
+// for them never waits for the weight stream.  Tiles are converted in
+// registers and fed to MFMA 16x16 instructions with the activation fragment
+// as the second operand.  Per-wave partial tiles are summed in LDS in a fixed
+// wave order (deterministic), then scale/bias are applied and each lane stores
+// four consecutive outputs as one vector.
+#include <algorithm>
+#include <type_traits>
+
 #include "sbq_common.h"
 #include "sbq_launch.h"
 
 namespace sbq {
 
 // ---------------------------------------------------------------------------
-// Activation fragments: lane (r, g) of M-tile mt holds x[mt*16 + r][k0 .. k0+15]
-// with k0 = kc*64 + g*16.  Rows >= M and columns >= K read as zero.
+// Raw activations of one lane: x[m][k0 .. k0+15], m = mt*16 + r,
+// k0 = kc*64 + g*16.  Rows >= M and columns >= K read as zero.
 // ---------------------------------------------------------------------------
 template <int XT>
-struct XFrag;
+struct XRaw;
 
 template <>
-struct XFrag<XT_F16> {
-  static constexpr int NS = 1;
-  typedef f16x8 V;
-  V v[2][1];
+struct XRaw<XT_F16> {
+  f16x8 a, b;
   __device__ __forceinline__ void load(const void* x, int64_t ldx, int M, int K, int m, int k0, bool xvec) {
     const _Float16* p = (const _Float16*)x + (int64_t)m * ldx + k0;
     if (m < M && xvec && k0 + 16 <= K) {
-      v[0][0] = *(const f16x8*)p;
-      v[1][0] = *(const f16x8*)(p + 8);
+      a = *(const f16x8*)p;
+      b = *(const f16x8*)(p + 8);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        v[0][0][j] = (m < M && k0 + j < K) ? p[j] : (_Float16)0.0f;
-        v[1][0][j] = (m < M && k0 + 8 + j < K) ? p[8 + j] : (_Float16)0.0f;
+        a[j] = (m < M && k0 + j < K) ? p[j] : (_Float16)0.0f;
+        b[j] = (m < M && k0 + 8 + j < K) ? p[8 + j] : (_Float16)0.0f;
       }
+    }
+  }
+  __device__ __forceinline__ float get(int j) const { return j < 8 ? (float)a[j] : (float)b[j - 8]; }
+  __device__ __forceinline__ void load_lds(const uint8_t* xl, int Kp, int M, int m, int k0) {
+    if (m < M) {
+      const _Float16* p = (const _Float16*)xl + m * Kp + k0;
+      a = *(const f16x8*)p;
+      b = *(const f16x8*)(p + 8);
+    } else {
+      a = f16x8{};
+      b = f16x8{};
     }
   }
 };
 
 template <>
-struct XFrag<XT_BF16> {
-  static constexpr int NS = 1;
-  typedef bf16x8 V;
-  V v[2][1];
+struct XRaw<XT_BF16> {
+  bf16x8 a, b;
   __device__ __forceinline__ void load(const void* x, int64_t ldx, int M, int K, int m, int k0, bool xvec) {
     const __bf16* p = (const __bf16*)x + (int64_t)m * ldx + k0;
     if (m < M && xvec && k0 + 16 <= K) {
-      v[0][0] = *(const bf16x8*)p;
-      v[1][0] = *(const bf16x8*)(p + 8);
+      a = *(const bf16x8*)p;
+      b = *(const bf16x8*)(p + 8);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        v[0][0][j] = (m < M && k0 + j < K) ? p[j] : (__bf16)0.0f;
-        v[1][0][j] = (m < M && k0 + 8 + j < K) ? p[8 + j] : (__bf16)0.0f;
+        a[j] = (m < M && k0 + j < K) ? p[j] : (__bf16)0.0f;
+        b[j] = (m < M && k0 + 8 + j < K) ? p[8 + j] : (__bf16)0.0f;
       }
+    }
+  }
+  __device__ __forceinline__ float get(int j) const { return j < 8 ? (float)a[j] : (float)b[j - 8]; }
+  __device__ __forceinline__ void load_lds(const uint8_t* xl, int Kp, int M, int m, int k0) {
+    if (m < M) {
+      const __bf16* p = (const __bf16*)xl + m * Kp + k0;
+      a = *(const bf16x8*)p;
+      b = *(const bf16x8*)(p + 8);
+    } else {
+      a = bf16x8{};
+      b = bf16x8{};
     }
   }
 };
 
-// fp32 activations: each value is split into bf16 hi + bf16 remainder, two
-// MFMA passes per step.
 template <>
-struct XFrag<XT_F32> {
-  static constexpr int NS = 2;
-  typedef bf16x8 V;
-  V v[2][2];
+struct XRaw<XT_F32> {
+  f32x4 v[4];
   __device__ __forceinline__ void load(const void* x, int64_t ldx, int M, int K, int m, int k0, bool xvec) {
-    float t[16];
-    load8_f32<XT_F32>(x, ldx, M, K, m, k0, xvec, t);
-    load8_f32<XT_F32>(x, ldx, M, K, m, k0 + 8, xvec, t + 8);
+    const float* p = (const float*)x + (int64_t)m * ldx + k0;
+    if (m < M && xvec && k0 + 16 <= K) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = *(const f32x4*)(p + 4 * i);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j >> 2][j & 3] = (m < M && k0 + j < K) ? p[j] : 0.0f;
+    }
+  }
+  __device__ __forceinline__ float get(int j) const { return v[j >> 2][j & 3]; }
+  __device__ __forceinline__ void load_lds(const uint8_t* xl, int Kp, int M, int m, int k0) {
+    if (m < M) {
+      const float* p = (const float*)xl + m * Kp + k0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = *(const f32x4*)(p + 4 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = f32x4{};
+    }
+  }
+};
+
+// Element bytes of an activation type.
+template <int XT>
+constexpr int x_bytes() { return XT == XT_F32 ? 4 : 2; }
+
+// Default number of 16-byte chunks of x per thread the LDS staging holds.
+constexpr int kStageChunks = 4;
+
+// Weight tile (16 offset-binary bytes of one lane) x activation fragment ->
+// MFMA into acc.  fp16/bf16 activations are exact operands; fp32 activations
+// run as bf16 hi + bf16 remainder (two passes, remainder first).
+template <int XT>
+__device__ __forceinline__ void tile_mma(u32x4 w, const XRaw<XT>& x, f32x4& acc) {
+  if constexpr (XT == XT_F16) {
+    f16x8 w0, w1;
+    u8x16_to_f16(w, w0, w1);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w0, x.a, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1, x.b, acc, 0, 0, 0);
+  } else if constexpr (XT == XT_BF16) {
+    bf16x8 w0, w1;
+    u8x16_to_bf16(w, w0, w1);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, x.a, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, x.b, acc, 0, 0, 0);
+  } else {
+    bf16x8 w0, w1, h0, h1, l0, l1;
+    u8x16_to_bf16(w, w0, w1);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       __bf16 h, l;
-      split_bf16(t[j], h, l);
-      v[0][0][j] = h;
-      v[0][1][j] = l;
-      split_bf16(t[8 + j], h, l);
-      v[1][0][j] = h;
-      v[1][1][j] = l;
+      split_bf16(x.get(j), h, l);
+      h0[j] = h;
+      l0[j] = l;
+      split_bf16(x.get(8 + j), h, l);
+      h1[j] = h;
+      l1[j] = l;
     }
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, l0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, l1, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, h0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, h1, acc, 0, 0, 0);
   }
-};
+}
 
-// Weight fragment conversion + MFMA for one 16x64 tile against one activation
-// fragment.
+// s8 activation fragment (xq - 128) from raw values; columns >= K and rows
+// >= M become 0 (they meet zero weights or are never stored).
 template <int XT>
-struct TileMma {
-  static __device__ __forceinline__ void run(u32x4 w, const XFrag<XT>& xf, f32x4& acc);
-};
-
-template <>
-__device__ __forceinline__ void TileMma<XT_F16>::run(u32x4 w, const XFrag<XT_F16>& xf, f32x4& acc) {
-  f16x8 w0, w1;
-  u8x16_to_f16(w, w0, w1);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w0, xf.v[0][0], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1, xf.v[1][0], acc, 0, 0, 0);
-}
-
-template <>
-__device__ __forceinline__ void TileMma<XT_BF16>::run(u32x4 w, const XFrag<XT_BF16>& xf, f32x4& acc) {
-  bf16x8 w0, w1;
-  u8x16_to_bf16(w, w0, w1);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xf.v[0][0], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xf.v[1][0], acc, 0, 0, 0);
-}
-
-template <>
-__device__ __forceinline__ void TileMma<XT_F32>::run(u32x4 w, const XFrag<XT_F32>& xf, f32x4& acc) {
-  bf16x8 w0, w1;
-  u8x16_to_bf16(w, w0, w1);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xf.v[0][1], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xf.v[1][1], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xf.v[0][0], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xf.v[1][0], acc, 0, 0, 0);
-}
-
-__device__ __forceinline__ u32x4 load_tile_nt(const uint8_t* p) {
-  return __builtin_nontemporal_load((const u32x4*)p);
-}
-
-// ---------------------------------------------------------------------------
-// Weight-only
-// ---------------------------------------------------------------------------
-template <int XT, int G, int MT>
-__global__ __launch_bounds__(1024) void gemv_w8_kernel(const void* __restrict__ x, int64_t ldx, int M, int K,
-                                                       int Kc, const uint8_t* __restrict__ packed,
-                                                       const float* __restrict__ scale,
-                                                       const float* __restrict__ bias, int N, int Nt,
-                                                       void* __restrict__ y, int yt, int64_t ldy, int flags) {
-  extern __shared__ f32x4 red[];  // [waves][G*MT][64]
-  const bool xvec = flags & 1;
-  const int nw = blockDim.x >> 6;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r = lane & 15, g = lane >> 4;
-  const int nt0 = blockIdx.x * G;
-  const int per = (Kc + nw - 1) / nw;
-  const int kb = wave * per;
-  const int ke = min(Kc, kb + per);
-
-  f32x4 acc[G][MT];
-#pragma unroll
-  for (int t = 0; t < G; ++t)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  const uint8_t* tp[G];
-#pragma unroll
-  for (int t = 0; t < G; ++t) tp[t] = packed + ((int64_t)(nt0 + t) * Kc) * 1024 + lane * 16;
-
-  for (int kc = kb; kc < ke; ++kc) {
-    u32x4 w[G];
-#pragma unroll
-    for (int t = 0; t < G; ++t) {
-      if (nt0 + t < Nt) w[t] = load_tile_nt(tp[t] + (int64_t)kc * 1024);
-    }
-    XFrag<XT> xf[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xf[mt].load(x, ldx, M, K, mt * 16 + r, kc * 64 + g * 16, xvec);
-#pragma unroll
-    for (int t = 0; t < G; ++t) {
-      if (nt0 + t < Nt) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) TileMma<XT>::run(w[t], xf[mt], acc[t][mt]);
-      }
-    }
-  }
-
-#pragma unroll
-  for (int t = 0; t < G; ++t)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) red[(wave * G * MT + t * MT + mt) * 64 + lane] = acc[t][mt];
-  __syncthreads();
-
-  const bool yvec_ok = flags & 2;
-  for (int p = threadIdx.x; p < G * MT * 64; p += blockDim.x) {
-    const int l = p & 63, tm = p >> 6;
-    const int t = tm / MT, mt = tm % MT;
-    const int m = mt * 16 + (l & 15);
-    const int nt = nt0 + t;
-    if (m >= M || nt >= Nt) continue;
-    f32x4 s = red[tm * 64 + l];
-    for (int w = 1; w < nw; ++w) s += red[(w * G * MT + tm) * 64 + l];
-    const int n = nt * 16 + (l >> 4) * 4;
-    if (n >= N) continue;
-    const int nvalid = min(4, N - n);
-    f32x4 o;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int nn = min(n + v, N - 1);
-      float out = s[v] * scale[nn];
-      if (bias) out = out + bias[nn];
-      o[v] = out;
-    }
-    store_y4(y, yt, (int64_t)m * ldy + n, o, yvec_ok && nvalid == 4, nvalid);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// W8A8: activations quantized on the fly with the per-tensor parameters,
-// i8 MFMA 16x16x64 with exact int32 accumulation.
-// ---------------------------------------------------------------------------
-template <int XT>
-__device__ __forceinline__ i32x4 load_xq16(const void* x, int64_t ldx, int M, int K, int m, int k0, bool xvec,
-                                           float inv, float zpf) {
-  float t[16];
-  load8_f32<XT>(x, ldx, M, K, m, k0, xvec, t);
-  load8_f32<XT>(x, ldx, M, K, m, k0 + 8, xvec, t + 8);
+__device__ __forceinline__ i32x4 quant_frag(const XRaw<XT>& x, int M, int K, int m, int k0, float inv, float zpf) {
   uint32_t d[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -218,8 +167,7 @@ __device__ __forceinline__ i32x4 load_xq16(const void* x, int64_t ldx, int M, in
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int jj = 4 * i + j;
-      const bool valid = m < M && k0 + jj < K;
-      const int qv = valid ? quant_act_s8(t[jj], inv, zpf) : 0;
+      const int qv = (m < M && k0 + jj < K) ? quant_act_s8(x.get(jj), inv, zpf) : 0;
       word |= ((uint32_t)qv & 0xffu) << (8 * j);
     }
     d[i] = word;
@@ -232,88 +180,387 @@ __device__ __forceinline__ i32x4 tile_to_s8(u32x4 w) {
                  (int)(w.w ^ 0x80808080u)};
 }
 
-template <int XT, int G, int MT>
-__global__ __launch_bounds__(1024) void gemv_w8a8_kernel(const void* __restrict__ x, int64_t ldx, int M, int K,
-                                                         int Kc, const uint8_t* __restrict__ packed,
-                                                         const float* __restrict__ scale,
-                                                         const int32_t* __restrict__ colsum,
-                                                         const float* __restrict__ bias, int N, int Nt,
-                                                         void* __restrict__ y, int yt, int64_t ldy,
-                                                         int32_t* __restrict__ acc_out,
-                                                         const float2* __restrict__ partials, int nparts,
-                                                         int flags) {
-  const bool xvec = flags & 1;
-  extern __shared__ i32x4 redi[];  // [waves][G*MT][64]
-  __shared__ float qred[32];
-  const ActQParams qp = block_qparams_from_partials(partials, nparts, qred);
-  const int nw = blockDim.x >> 6;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r = lane & 15, g = lane >> 4;
-  const int nt0 = blockIdx.x * G;
-  const int per = (Kc + nw - 1) / nw;
-  const int kb = wave * per;
-  const int ke = min(Kc, kb + per);
+__device__ __forceinline__ u32x4 load_tile_nt(const uint8_t* p) {
+  return __builtin_nontemporal_load((const u32x4*)p);
+}
 
-  i32x4 acc[G][MT];
+// ---------------------------------------------------------------------------
+// Persistent streaming kernel (weight-only and W8A8).
+//
+// A workgroup of `waves` waves owns a fixed K split: wave w always covers K
+// tiles [w*P, w*P + P).  Groups of G weight tiles are assigned round-robin
+// (group = blockIdx.x + i * gridDim.x).  The weight tiles of the next NB-1
+// groups (and their scale/bias/colsum values) are in flight while the current
+// group is multiplied, reduced across waves in LDS and stored.
+//
+// Activation modes (XM):
+//   XM_REG   each wave loads the fragments of its K split once, into registers
+//   XM_LDS   the workgroup stages x[M][K] in LDS once; fragments are read on use
+//   XM_CHUNK fragments are re-read from global memory (L2) per group, XC K tiles
+//            at a time (for x too large for LDS; used with NB = 1)
+// In every mode the first activation loads are issued before the weight loads:
+// loads retire in order, so waiting for them never waits for the weights.
+// ---------------------------------------------------------------------------
+enum XMode { XM_REG = 0, XM_LDS = 1, XM_CHUNK = 2 };
+
+struct GemvArgs {
+  const void* x;
+  int64_t ldx;
+  int M, K, Kc;
+  const uint8_t* packed;
+  const float* scale;
+  const float* bias;
+  const int32_t* colsum;
+  int N, Nt, ngroups;
+  void* y;
+  int yt;
+  int64_t ldy;
+  int32_t* acc_out;
+  const float2* partials;
+  int nparts;
+  int flags;
+};
+
+// Per-thread epilogue operands of one group: thread t < G*MT*64 finishes pair
+// (tile t/64/MT, token tile (t/64)%MT, lane t%64), i.e. outputs n..n+3 of row m.
+struct EpiVals {
+  f32x4 sc, bi;
+  i32x4 cs;
+};
+
+template <int G, int MT, bool W8A8>
+__device__ __forceinline__ void load_epi(const GemvArgs& a, int grp, EpiVals& e) {
+  const int p = threadIdx.x;
+  if (p >= G * MT * 64 || grp >= a.ngroups) return;
+  const int l = p & 63, t = (p >> 6) / MT;
+  const int n = (grp * G + t) * 16 + (l >> 4) * 4;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int nn = min(n + v, a.N - 1);
+    e.sc[v] = a.scale[nn];
+    e.bi[v] = a.bias ? a.bias[nn] : 0.0f;
+    if constexpr (W8A8) e.cs[v] = a.colsum[nn];
+  }
+}
+
+template <int G, int P>
+__device__ __forceinline__ void load_w(const GemvArgs& a, int grp, int kb, int lane, u32x4 (&w)[G][P]) {
+  if (grp >= a.ngroups) return;
 #pragma unroll
   for (int t = 0; t < G; ++t)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = (i32x4){0, 0, 0, 0};
-
-  const uint8_t* tp[G];
-#pragma unroll
-  for (int t = 0; t < G; ++t) tp[t] = packed + ((int64_t)(nt0 + t) * Kc) * 1024 + lane * 16;
-
-  for (int kc = kb; kc < ke; ++kc) {
-    u32x4 w[G];
-#pragma unroll
-    for (int t = 0; t < G; ++t) {
-      if (nt0 + t < Nt) w[t] = load_tile_nt(tp[t] + (int64_t)kc * 1024);
+    for (int p = 0; p < P; ++p) {
+      const int nt = grp * G + t;
+      if (nt < a.Nt && kb + p < a.Kc) w[t][p] = load_tile_nt(a.packed + ((int64_t)nt * a.Kc + kb + p) * 1024 + lane * 16);
     }
-    i32x4 xq[MT];
+}
+
+// Activation fragments of K tiles [kb+p0, kb+p0+CNT) from global memory.
+template <int XT, int MT, int CNT>
+__device__ __forceinline__ void load_x_frags(const GemvArgs& a, int kb, int p0, int pend, int lane,
+                                             XRaw<XT> (&xr)[CNT][MT]) {
+  const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int p = 0; p < CNT; ++p)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
-      xq[mt] = load_xq16<XT>(x, ldx, M, K, mt * 16 + r, kc * 64 + g * 16, xvec, qp.inv, qp.zpf);
+      if (p0 + p < pend && kb + p0 + p < a.Kc)
+        xr[p][mt].load(a.x, a.ldx, a.M, a.K, mt * 16 + r, (kb + p0 + p) * 64 + g * 16, a.flags & 1);
+}
+
+// Multiply-accumulate one K tile of every weight tile of the group.
+template <int XT, int MT, int G, bool W8A8, typename Acc>
+__device__ __forceinline__ void mma_ktile(const u32x4 (&wk)[G], const XRaw<XT> (&xf)[MT], const i32x4* xq,
+                                          int nt0, int Nt, const GemvArgs& a, int lane, int k0, const ActQParams& qp,
+                                          Acc (&acc)[G][MT]) {
 #pragma unroll
-    for (int t = 0; t < G; ++t) {
-      if (nt0 + t < Nt) {
-        const i32x4 ws = tile_to_s8(w[t]);
+  for (int t = 0; t < G; ++t) {
+    if (nt0 + t >= Nt) continue;
+    if constexpr (W8A8) {
+      const i32x4 ws = tile_to_s8(wk[t]);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          acc[t][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ws, xq[mt], acc[t][mt], 0, 0, 0);
+      for (int mt = 0; mt < MT; ++mt) {
+        const i32x4 q = xq ? xq[mt] : quant_frag<XT>(xf[mt], a.M, a.K, mt * 16 + (lane & 15), k0, qp.inv, qp.zpf);
+        acc[t][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ws, q, acc[t][mt], 0, 0, 0);
       }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) tile_mma<XT>(wk[t], xf[mt], acc[t][mt]);
     }
   }
+}
 
+// Cross-wave reduction of the group in LDS (fixed wave order), epilogue and
+// vector store of four outputs per lane.
+template <int G, int MT, bool W8A8, typename Acc>
+__device__ __forceinline__ void reduce_store(const GemvArgs& a, int grp, int lane, const Acc (&acc)[G][MT],
+                                             const EpiVals& e, const ActQParams& qp, void* red) {
+  const int wave = threadIdx.x >> 6;
+  const int nt0 = grp * G;
+  Acc* redv = (Acc*)red;
 #pragma unroll
   for (int t = 0; t < G; ++t)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) redi[(wave * G * MT + t * MT + mt) * 64 + lane] = acc[t][mt];
+    for (int mt = 0; mt < MT; ++mt) redv[(wave * G * MT + t * MT + mt) * 64 + lane] = acc[t][mt];
   __syncthreads();
 
-  const bool yvec_ok = flags & 2;
-  const int corr = 128 - qp.zp;
-  for (int p = threadIdx.x; p < G * MT * 64; p += blockDim.x) {
-    const int l = p & 63, tm = p >> 6;
+  const int pidx = threadIdx.x;
+  if (pidx < G * MT * 64) {
+    const int nw = blockDim.x >> 6;
+    const int l = pidx & 63, tm = pidx >> 6;
     const int t = tm / MT, mt = tm % MT;
     const int m = mt * 16 + (l & 15);
     const int nt = nt0 + t;
-    if (m >= M || nt >= Nt) continue;
-    i32x4 s = redi[tm * 64 + l];
-    for (int w = 1; w < nw; ++w) s += redi[(w * G * MT + tm) * 64 + l];
     const int n = nt * 16 + (l >> 4) * 4;
-    if (n >= N) continue;
-    const int nvalid = min(4, N - n);
-    f32x4 o;
+    if (m < a.M && nt < a.Nt && n < a.N) {
+      Acc s = redv[tm * 64 + l];
+      for (int ww = 1; ww < nw; ++ww) s += redv[(ww * G * MT + tm) * 64 + l];
+      const int nvalid = min(4, a.N - n);
+      f32x4 o;
+      if constexpr (W8A8) {
+        const int corr = 128 - qp.zp;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int nn = min(n + v, N - 1);
-      const int a = s[v] + corr * colsum[nn];
-      if (acc_out && v < nvalid) acc_out[(int64_t)m * N + n + v] = a;
-      const float mult = qp.scale * scale[nn];
-      o[v] = bias ? __builtin_fmaf((float)a, mult, bias[nn]) : (float)a * mult;
+        for (int v = 0; v < 4; ++v) {
+          const int av = s[v] + corr * e.cs[v];
+          if (a.acc_out && v < nvalid) a.acc_out[(int64_t)m * a.N + n + v] = av;
+          const float mult = qp.scale * e.sc[v];
+          o[v] = a.bias ? __builtin_fmaf((float)av, mult, e.bi[v]) : (float)av * mult;
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float out = s[v] * e.sc[v];
+          if (a.bias) out = out + e.bi[v];
+          o[v] = out;
+        }
+      }
+      store_y4(a.y, a.yt, (int64_t)m * a.ldy + n, o, (a.flags & 2) && nvalid == 4, nvalid);
     }
-    store_y4(y, yt, (int64_t)m * ldy + n, o, yvec_ok && nvalid == 4, nvalid);
+  }
+  __syncthreads();  // the next group reuses the reduction buffer
+}
+
+template <int XT, int MT, int G, int P, bool W8A8, int XM, int XR, int XC>
+__device__ __forceinline__ void process_group(const GemvArgs& a, int grp, int kb, int lane,
+                                              const u32x4 (&w)[G][P], XRaw<XT> (&xr)[XR][MT],
+                                              const i32x4 (&xq)[XM == XM_REG ? P : 1][MT], const EpiVals& e,
+                                              const ActQParams& qp, void* red, const uint8_t* xl, int Kp) {
+  typedef typename std::conditional<W8A8, i32x4, f32x4>::type Acc;
+  const int r = lane & 15, g = lane >> 4;
+  const int nt0 = grp * G;
+  Acc acc[G][MT];
+#pragma unroll
+  for (int t = 0; t < G; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = Acc{0, 0, 0, 0};
+
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int kc = kb + p;
+    if (kc >= a.Kc) continue;
+    // LDS / chunked activations: keep the per-tile activation reads next to
+    // their use (hoisting all of them would exceed the register budget)
+    if constexpr (XM != XM_REG) {
+      if (p > 0) __builtin_amdgcn_sched_barrier(0);
+    }
+    u32x4 wk[G];
+#pragma unroll
+    for (int t = 0; t < G; ++t) wk[t] = w[t][p];
+    if constexpr (XM == XM_REG) {
+      mma_ktile<XT, MT, G, W8A8>(wk, xr[p], W8A8 ? xq[p] : nullptr, nt0, a.Nt, a, lane, kc * 64 + g * 16, qp, acc);
+    } else if constexpr (XM == XM_LDS) {
+      XRaw<XT> xf[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) xf[mt].load_lds(xl, Kp, a.M, mt * 16 + r, kc * 64 + g * 16);
+      mma_ktile<XT, MT, G, W8A8>(wk, xf, nullptr, nt0, a.Nt, a, lane, kc * 64 + g * 16, qp, acc);
+    }
+  }
+  reduce_store<G, MT, W8A8>(a, grp, lane, acc, e, qp, red);
+}
+
+// XM_CHUNK: the wave's P K tiles run as a pipeline of XC-tile sub-chunks; the
+// activations (re-read from L2 per group) and weight tiles of sub-chunk c+1
+// are loaded while sub-chunk c is multiplied.
+template <int XT, int MT, int G, int P, bool W8A8, int XC>
+__device__ __forceinline__ void process_group_chunked(const GemvArgs& a, int grp, int kb, int lane,
+                                                      const EpiVals& e, const ActQParams& qp, void* red) {
+  typedef typename std::conditional<W8A8, i32x4, f32x4>::type Acc;
+  constexpr int NCH = (P + XC - 1) / XC;
+  const int g = lane >> 4;
+  const int nt0 = grp * G;
+  XRaw<XT> xc[2][XC][MT];
+  u32x4 wc[2][G][XC];
+  auto load_chunk = [&](int c, int b) {
+    load_x_frags<XT, MT, XC>(a, kb, c * XC, P, lane, xc[b]);
+#pragma unroll
+    for (int t = 0; t < G; ++t)
+#pragma unroll
+      for (int j = 0; j < XC; ++j) {
+        const int p = c * XC + j, nt = nt0 + t;
+        if (p < P && nt < a.Nt && kb + p < a.Kc)
+          wc[b][t][j] = load_tile_nt(a.packed + ((int64_t)nt * a.Kc + kb + p) * 1024 + lane * 16);
+      }
+  };
+  Acc acc[G][MT];
+#pragma unroll
+  for (int t = 0; t < G; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = Acc{0, 0, 0, 0};
+  load_chunk(0, 0);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (c + 1 < NCH) load_chunk(c + 1, (c + 1) & 1);
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+      const int p = c * XC + j, kc = kb + p;
+      if (p >= P || kc >= a.Kc) continue;
+      u32x4 wk[G];
+#pragma unroll
+      for (int t = 0; t < G; ++t) wk[t] = wc[c & 1][t][j];
+      mma_ktile<XT, MT, G, W8A8>(wk, xc[c & 1][j], nullptr, nt0, a.Nt, a, lane, kc * 64 + g * 16, qp, acc);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  reduce_store<G, MT, W8A8>(a, grp, lane, acc, e, qp, red);
+}
+
+template <int XT, int MT, int G, int P, bool W8A8, int XM, int NB, int SC = kStageChunks>
+__global__ __launch_bounds__(1024) void gemv_kernel(const GemvArgs a) {
+  // dynamic LDS: [waves][G*MT][64] accumulators (the head doubles as qparams
+  // scratch), then with XM_LDS the activations x[M][Kp] (zero padded)
+  extern __shared__ f32x4 red[];
+  constexpr int XC = XT == XT_F32 ? 1 : 2;                           // XM_CHUNK sub-chunk (K tiles)
+  constexpr int XR = XM == XM_REG ? P : 1;
+  constexpr int XSZ = x_bytes<XT>();
+  static_assert(XM != XM_CHUNK || NB == 1, "chunked activations reload per group: one weight buffer");
+  const int nw = blockDim.x >> 6;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kb = wave * P;
+  const int Kp = a.Kc * 64;
+  uint8_t* xl = (uint8_t*)(red + nw * G * MT * 64);
+  int grp = blockIdx.x;
+
+  // W8A8: activation min/max partials first (nparts <= 256, blockDim.x >= 64)
+  float2 part[4];
+  if constexpr (W8A8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = threadIdx.x + i * blockDim.x;
+      part[i] = idx < a.nparts ? a.partials[idx] : make_float2(0.0f, 0.0f);
+    }
+  }
+  XRaw<XT> xr[XR][MT];
+  u32x4 stg[XM == XM_LDS ? SC : 1];
+  const int row_chunks = Kp * XSZ / 16;
+  if constexpr (XM == XM_LDS) {
+#pragma unroll
+    for (int i = 0; i < SC; ++i) {
+      const int c = threadIdx.x + i * blockDim.x;
+      if (c < a.M * row_chunks) {
+        const int m = c / row_chunks;
+        const int k0 = (c - m * row_chunks) * (16 / XSZ);
+        const uint8_t* src = (const uint8_t*)a.x + ((int64_t)m * a.ldx + k0) * XSZ;
+        if ((a.flags & 1) && k0 + 16 / XSZ <= a.K) {
+          stg[i] = *(const u32x4*)src;
+        } else {
+          uint8_t b[16];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) b[j] = (k0 + j / XSZ < a.K) ? src[j] : (uint8_t)0;
+          stg[i] = __builtin_bit_cast(u32x4, b);
+        }
+      }
+    }
+  } else if constexpr (XM == XM_REG) {
+    load_x_frags<XT, MT, XR>(a, kb, 0, P, lane, xr);
+  }
+
+  // weight ring (the chunked mode keeps its own sub-chunk buffers)
+  constexpr int WP = XM == XM_CHUNK ? 1 : P;
+  u32x4 wbuf[NB][G][WP];
+  EpiVals ebuf[NB];
+  if constexpr (XM != XM_CHUNK) {
+#pragma unroll
+    for (int b = 0; b < (NB > 1 ? NB - 1 : 1); ++b) {
+      load_w<G, P>(a, grp + b * (int)gridDim.x, kb, lane, wbuf[b]);
+      load_epi<G, MT, W8A8>(a, grp + b * (int)gridDim.x, ebuf[b]);
+    }
+  } else {
+    load_epi<G, MT, W8A8>(a, grp, ebuf[0]);
+  }
+
+  if constexpr (XM == XM_LDS) {
+#pragma unroll
+    for (int i = 0; i < SC; ++i) {
+      const int c = threadIdx.x + i * blockDim.x;
+      if (c < a.M * row_chunks) *(u32x4*)(xl + (int64_t)c * 16) = stg[i];
+    }
+    __syncthreads();
+  }
+
+  ActQParams qp{};
+  i32x4 xq[XM == XM_REG ? P : 1][MT];
+  if constexpr (W8A8) {
+    float mn = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mn = fminf(mn, part[i].x);
+      mx = fmaxf(mx, part[i].y);
+    }
+    float* qred = (float*)red;
+    mn = wave_min(mn);
+    mx = wave_max(mx);
+    if (lane == 0) {
+      qred[2 * wave] = mn;
+      qred[2 * wave + 1] = mx;
+    }
+    __syncthreads();
+    mn = qred[0];
+    mx = qred[1];
+    for (int i = 1; i < nw; ++i) {
+      mn = fminf(mn, qred[2 * i]);
+      mx = fmaxf(mx, qred[2 * i + 1]);
+    }
+    __syncthreads();
+    qp = choose_act_qparams(mn, mx);
+    if constexpr (XM == XM_REG) {
+      const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          xq[p][mt] = quant_frag<XT>(xr[p][mt], a.M, a.K, mt * 16 + r, (kb + p) * 64 + g * 16, qp.inv, qp.zpf);
+    }
+  }
+
+  if constexpr (XM == XM_CHUNK) {
+    while (true) {
+      process_group_chunked<XT, MT, G, P, W8A8, XC>(a, grp, kb, lane, ebuf[0], qp, red);
+      grp += gridDim.x;
+      if (grp >= a.ngroups) break;
+      load_epi<G, MT, W8A8>(a, grp, ebuf[0]);
+    }
+  } else if constexpr (NB == 1) {
+    while (true) {
+      process_group<XT, MT, G, P, W8A8, XM, XR, XC>(a, grp, kb, lane, wbuf[0], xr, xq, ebuf[0], qp, red, xl, Kp);
+      grp += gridDim.x;
+      if (grp >= a.ngroups) break;
+      load_w<G, P>(a, grp, kb, lane, wbuf[0]);
+      load_epi<G, MT, W8A8>(a, grp, ebuf[0]);
+    }
+  } else {
+    // ring: buffer b holds group grp; the load NB-1 groups ahead goes into the
+    // buffer the previous group just released
+    while (true) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int ahead = grp + (NB - 1) * (int)gridDim.x;
+        load_w<G, P>(a, ahead, kb, lane, wbuf[(b + NB - 1) % NB]);
+        load_epi<G, MT, W8A8>(a, ahead, ebuf[(b + NB - 1) % NB]);
+        if (grp >= a.ngroups) return;
+        process_group<XT, MT, G, P, W8A8, XM, XR, XC>(a, grp, kb, lane, wbuf[b], xr, xq, ebuf[b], qp, red, xl, Kp);
+        grp += gridDim.x;
+      }
+    }
   }
 }
 
@@ -321,51 +568,107 @@ __global__ __launch_bounds__(1024) void gemv_w8a8_kernel(const void* __restrict_
 // launch configuration
 // ---------------------------------------------------------------------------
 struct GemvCfg {
-  int g, mt, waves;
+  int mt, g, p, waves, xm, nb, sc;
+  bool ok;
 };
 
-static GemvCfg pick_gemv(int64_t M, int64_t Nt, int64_t Kc) {
-  GemvCfg c;
-  c.mt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  // K split: 4..16 tiles per wave
-  if (Kc >= 128) c.waves = 16;
-  else if (Kc >= 32) c.waves = 8;
-  else if (Kc >= 8) c.waves = 4;
-  else if (Kc >= 2) c.waves = 2;
-  else c.waves = 1;
+// Measured on MI355X (M = 1, fp16, 4096..151936 x 4096..12288): one-shot
+// workgroups (grid = #groups, no persistence, NB = 1) with 8 KiB of weight
+// tiles per wave beat persistent rings: independent workgroups overlap on the
+// CU by themselves.  P = 8 K tiles per wave (8 waves at K = 4096), P = 12 for
+// K up to 12288, P = Kc below 8.  Activations: staged in LDS with SC 16-byte
+// chunks per thread when x[M][K] allows SC <= 4; otherwise registers
+// (short K splits) or per-group chunks.  Every instance below fits the
+// register budget of its workgroup without spilling.
+static GemvCfg pick_gemv(int64_t M, int64_t Nt, int64_t Kc, bool w8a8, int xt) {
+  (void)Nt;
+  GemvCfg c{};
+  if (M > 32 || Kc > 192) return c;
+  c.mt = M <= 16 ? 1 : 2;
+  c.p = Kc <= 8 ? (Kc <= 1 ? 1 : (Kc <= 2 ? 2 : (Kc <= 4 ? 4 : 8))) : (Kc <= 128 ? 8 : 12);
+  c.waves = (int)((Kc + c.p - 1) / c.p);
   c.g = 1;
-  if (c.mt == 1) {
-    while (c.g < 4 && (Nt / (2 * c.g)) * c.waves >= 4096) c.g *= 2;
+  c.nb = 1;
+  c.ok = true;
+  const int64_t xbytes = M * Kc * 64 * (xt == XT_F32 ? 4 : 2);
+  const int64_t per_thread = (xbytes + 16 * 64 * c.waves - 1) / (16 * 64 * c.waves);
+  if (c.mt == 1 && per_thread <= 4) {
+    c.xm = XM_LDS;
+    c.sc = per_thread <= 1 ? 1 : (per_thread <= 2 ? 2 : 4);
+    return c;
+  }
+  c.sc = 1;
+  const int reg_p = xt == XT_F32 ? 1 : (w8a8 ? 2 : 4);
+  if (c.p > reg_p && Kc <= 16 * reg_p) {  // a shorter K split keeps x in registers
+    c.p = reg_p;
+    c.waves = (int)((Kc + c.p - 1) / c.p);
+  }
+  if (c.p <= reg_p) {
+    c.xm = XM_REG;
+  } else if (c.mt == 1) {
+    c.xm = XM_CHUNK;
+  } else {
+    c.ok = false;
   }
   return c;
 }
 
-template <int XT, int G, int MT>
-static void launch_w8_inst(dim3 grid, dim3 block, size_t lds, hipStream_t st, const void* x, int64_t ldx, int M,
-                           int K, int Kc, const uint8_t* packed, const float* scale, const float* bias, int N, int Nt,
-                           void* y, int yt, int64_t ldy, int flags) {
-  hipLaunchKernelGGL((gemv_w8_kernel<XT, G, MT>), grid, block, lds, st, x, ldx, M, K, Kc, packed, scale, bias, N,
-                     Nt, y, yt, ldy, flags);
+bool gemv_supports(int64_t M, int64_t K, bool w8a8, int xt) {
+  if (M < 1) return false;
+  return pick_gemv(M, 1, (K + 63) / 64, w8a8, xt).ok;
 }
 
-template <int XT>
-static int launch_w8_xt(const GemvCfg& c, hipStream_t st, const void* x, int64_t ldx, int M, int K, int Kc,
-                        const uint8_t* packed, const float* scale, const float* bias, int N, int Nt, void* y, int yt,
-                        int64_t ldy, int flags) {
-  dim3 grid((unsigned)((Nt + c.g - 1) / c.g)), block(64 * c.waves);
-  const size_t lds = (size_t)c.waves * c.g * c.mt * 64 * sizeof(f32x4);
-#define SBQ_W8_CASE(G_, MT_)                                                                               \
-  if (c.g == G_ && c.mt == MT_) {                                                                          \
-    launch_w8_inst<XT, G_, MT_>(grid, block, lds, st, x, ldx, M, K, Kc, packed, scale, bias, N, Nt, y, yt, \
-                                ldy, flags);                                                               \
-    return check_launch();                                                                                 \
+// (MT, P, XM, SC).  Covers every configuration pick_gemv returns: P is one of
+// {1, 2, 4, 8, 12}, SC one of {1, 2, 4}; XM_REG only with P <= 4 (MT 1 or 2);
+// XM_CHUNK only with P in {8, 12} (K > 16 register-held tiles per wave).
+#define SBQ_GEMV_CONFIGS(X) \
+  X(1, 1, XM_LDS, 1)        \
+  X(1, 1, XM_LDS, 2)        \
+  X(1, 1, XM_LDS, 4)        \
+  X(1, 2, XM_LDS, 1)        \
+  X(1, 2, XM_LDS, 2)        \
+  X(1, 2, XM_LDS, 4)        \
+  X(1, 4, XM_LDS, 1)        \
+  X(1, 4, XM_LDS, 2)        \
+  X(1, 4, XM_LDS, 4)        \
+  X(1, 8, XM_LDS, 1)        \
+  X(1, 8, XM_LDS, 2)        \
+  X(1, 8, XM_LDS, 4)        \
+  X(1, 12, XM_LDS, 1)       \
+  X(1, 12, XM_LDS, 2)       \
+  X(1, 12, XM_LDS, 4)       \
+  X(1, 1, XM_REG, 1)        \
+  X(1, 2, XM_REG, 1)        \
+  X(1, 4, XM_REG, 1)        \
+  X(1, 8, XM_CHUNK, 1)      \
+  X(1, 12, XM_CHUNK, 1)     \
+  X(2, 1, XM_REG, 1)        \
+  X(2, 2, XM_REG, 1)        \
+  X(2, 4, XM_REG, 1)
+
+// Instances pick_gemv can select for an activation type / format.
+template <int XT, bool W8A8, int MT, int P, int XM>
+constexpr bool gemv_instance_used() {
+  if (XM == XM_REG) return P <= (XT == XT_F32 ? 1 : (W8A8 ? 2 : 4));
+  if (XM == XM_CHUNK) return MT == 1 && P > (XT == XT_F32 ? 1 : (W8A8 ? 2 : 4));
+  return MT == 1;
+}
+
+template <int XT, bool W8A8>
+static int launch_gemv_xt(const GemvCfg& c, GemvArgs a, hipStream_t st) {
+  a.ngroups = (a.Nt + c.g - 1) / c.g;
+  size_t lds = (size_t)c.waves * c.g * c.mt * 64 * sizeof(f32x4);
+  if (c.xm == XM_LDS) lds += (size_t)a.M * a.Kc * 64 * x_bytes<XT>();
+#define SBQ_GEMV_CASE(MT_, P_, XM_, SC_)                                                                   \
+  if constexpr (gemv_instance_used<XT, W8A8, MT_, P_, XM_>()) {                                          \
+    if (c.mt == MT_ && c.p == P_ && c.xm == XM_ && c.sc == SC_) {                                        \
+      hipLaunchKernelGGL((gemv_kernel<XT, MT_, 1, P_, W8A8, XM_, 1, SC_>), dim3(a.ngroups), dim3(64 * c.waves), \
+                         lds, st, a);                                                                    \
+      return check_launch();                                                                             \
+    }                                                                                                    \
   }
-  SBQ_W8_CASE(1, 1)
-  SBQ_W8_CASE(2, 1)
-  SBQ_W8_CASE(4, 1)
-  SBQ_W8_CASE(1, 2)
-  SBQ_W8_CASE(1, 4)
-#undef SBQ_W8_CASE
+  SBQ_GEMV_CONFIGS(SBQ_GEMV_CASE)
+#undef SBQ_GEMV_CASE
   return -1;
 }
 
@@ -373,45 +676,19 @@ int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
                    const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
                    bool yvec) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
-  const int xvec_i = (xvec ? 1 : 0) | (yvec ? 2 : 0);
-  const GemvCfg c = pick_gemv(M, Nt, Kc);
+  const GemvCfg c = pick_gemv(M, Nt, Kc, false, xt);
+  if (!c.ok) return -1;
+  GemvArgs a{};
+  a.x = x; a.ldx = ldx; a.M = (int)M; a.K = (int)K; a.Kc = (int)Kc;
+  a.packed = packed; a.scale = scale; a.bias = bias;
+  a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy;
+  a.flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
   switch (xt) {
-    case XT_F16: return launch_w8_xt<XT_F16>(c, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, xvec_i);
-    case XT_BF16: return launch_w8_xt<XT_BF16>(c, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, xvec_i);
-    case XT_F32: return launch_w8_xt<XT_F32>(c, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, xvec_i);
+    case XT_F16: return launch_gemv_xt<XT_F16, false>(c, a, st);
+    case XT_BF16: return launch_gemv_xt<XT_BF16, false>(c, a, st);
+    case XT_F32: return launch_gemv_xt<XT_F32, false>(c, a, st);
   }
   return -2;
-}
-
-template <int XT, int G, int MT>
-static void launch_w8a8_inst(dim3 grid, dim3 block, size_t lds, hipStream_t st, const void* x, int64_t ldx, int M,
-                             int K, int Kc, const uint8_t* packed, const float* scale, const int32_t* colsum,
-                             const float* bias, int N, int Nt, void* y, int yt, int64_t ldy, int32_t* acc_out,
-                             const float2* partials, int nparts, int flags) {
-  hipLaunchKernelGGL((gemv_w8a8_kernel<XT, G, MT>), grid, block, lds, st, x, ldx, M, K, Kc, packed, scale, colsum,
-                     bias, N, Nt, y, yt, ldy, acc_out, partials, nparts, flags);
-}
-
-template <int XT>
-static int launch_w8a8_xt(const GemvCfg& c, hipStream_t st, const void* x, int64_t ldx, int M, int K, int Kc,
-                          const uint8_t* packed, const float* scale, const int32_t* colsum, const float* bias, int N,
-                          int Nt, void* y, int yt, int64_t ldy, int32_t* acc_out, const float2* partials, int nparts,
-                          int flags) {
-  dim3 grid((unsigned)((Nt + c.g - 1) / c.g)), block(64 * c.waves);
-  const size_t lds = (size_t)c.waves * c.g * c.mt * 64 * sizeof(i32x4);
-#define SBQ_W8A8_CASE(G_, MT_)                                                                                 \
-  if (c.g == G_ && c.mt == MT_) {                                                                              \
-    launch_w8a8_inst<XT, G_, MT_>(grid, block, lds, st, x, ldx, M, K, Kc, packed, scale, colsum, bias, N, Nt, \
-                                  y, yt, ldy, acc_out, partials, nparts, flags);                               \
-    return check_launch();                                                                                     \
-  }
-  SBQ_W8A8_CASE(1, 1)
-  SBQ_W8A8_CASE(2, 1)
-  SBQ_W8A8_CASE(4, 1)
-  SBQ_W8A8_CASE(1, 2)
-  SBQ_W8A8_CASE(1, 4)
-#undef SBQ_W8A8_CASE
-  return -1;
 }
 
 int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
@@ -419,12 +696,18 @@ int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
                      int64_t ldy, int32_t* acc_out, const float2* partials, int nparts, hipStream_t st,
                      bool yvec) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
-  const int xvec_i = (xvec ? 1 : 0) | (yvec ? 2 : 0);
-  const GemvCfg c = pick_gemv(M, Nt, Kc);
+  const GemvCfg c = pick_gemv(M, Nt, Kc, true, xt);
+  if (!c.ok) return -1;
+  GemvArgs a{};
+  a.x = x; a.ldx = ldx; a.M = (int)M; a.K = (int)K; a.Kc = (int)Kc;
+  a.packed = packed; a.scale = scale; a.bias = bias; a.colsum = colsum;
+  a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.acc_out = acc_out;
+  a.partials = partials; a.nparts = nparts;
+  a.flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
   switch (xt) {
-    case XT_F16: return launch_w8a8_xt<XT_F16>(c, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, partials, nparts, xvec_i);
-    case XT_BF16: return launch_w8a8_xt<XT_BF16>(c, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, partials, nparts, xvec_i);
-    case XT_F32: return launch_w8a8_xt<XT_F32>(c, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, partials, nparts, xvec_i);
+    case XT_F16: return launch_gemv_xt<XT_F16, true>(c, a, st);
+    case XT_BF16: return launch_gemv_xt<XT_BF16, true>(c, a, st);
+    case XT_F32: return launch_gemv_xt<XT_F32, true>(c, a, st);
   }
   return -2;
 }

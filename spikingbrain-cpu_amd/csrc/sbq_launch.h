@@ -23,6 +23,9 @@ int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t 
                            int nparts, hipStream_t st);
 int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t* zp_out, hipStream_t st);
 
+// True when the streaming GEMV kernels take this M and K (otherwise the GEMM).
+bool gemv_supports(int64_t M, int64_t K, bool w8a8, int xt);
+
 // Weight-only linear.  xvec: x and every row of x start 16-byte aligned (vector
 // loads allowed).  yvec: y rows are 16-byte aligned and N % 4 == 0.
 int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
