@@ -364,6 +364,159 @@ __global__ __launch_bounds__(WN* WM * 64) void gemm_w8a8_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Direct-to-LDS pipelined GEMM (weight-only, fp16/bf16 activations, K % 64 == 0)
+//
+// Block tile BN output channels x BM tokens x 64 K, WN x WM waves.  Used with
+// 256 x 128, 8 waves (4 x 2, wave tile 64 x 64) and 2 stages: measured on
+// MI355X this beats 4-wave / 3-stage variants, because two 64 KiB workgroups
+// share a CU (4 waves per SIMD) and hide each other's LDS and barrier stalls.  Each stage is filled by global_load_lds_dwordx4 (16 bytes
+// per lane straight into LDS, no register staging): the 16 packed weight tiles
+// land verbatim, the 128 activation rows land with their 16-byte chunks
+// XOR-swizzled by ((row >> 1) & 7), which spreads the 16 rows one
+// ds_read_b128 quarter-wave touches over all 64 LDS banks.  With NS stages,
+// NS-1 are in flight while one is multiplied.
+// Rows >= M and tiles >= Nt are loaded from clamped (in-bounds) addresses and
+// never stored.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) (n < 64) leaving the other counters unconstrained.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Workgroup barrier without the release/acquire fence of __syncthreads():
+// the fence would wait for every outstanding load, including the LDS DMA of
+// the stages still in flight.  Each wave waits for its own DMA of the stage it
+// is about to read (wait_vmcnt) before arriving here; the asm clobbers keep
+// the compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void barrier_nofence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ int xsw_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+
+template <int XT, int BN, int BM, int WN, int WM, int NS>
+__global__ __launch_bounds__(WN* WM * 64) void gemm_w8_dl_kernel(const void* __restrict__ x, int64_t ldx, int M,
+                                                                 int Kc, const uint8_t* __restrict__ packed,
+                                                                 const float* __restrict__ scale,
+                                                                 const float* __restrict__ bias, int N, int Nt,
+                                                                 void* __restrict__ y, int yt, int64_t ldy,
+                                                                 int flags) {
+  typedef GemmOp<XT> Op;
+  typedef typename Op::V V;
+  constexpr int NWAVES = WN * WM;
+  constexpr int TN = BN / WN, TM = BM / WM, FN = TN / 16, FM = TM / 16;
+  constexpr int WT = BN / 16;          // weight tiles per stage
+  constexpr int XR = BM * 128 / 1024;  // 1 KiB activation chunks (8 rows) per stage
+  constexpr int WBYTES = WT * 1024, STAGE = WBYTES + BM * 128;
+  constexpr int LPS = (WT + XR) / NWAVES;  // DMA instructions per wave per stage
+  static_assert(WT % NWAVES == 0 && XR % NWAVES == 0, "even DMA split");
+  static_assert(NS == 2 || NS == 3, "stages");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int wn = wave / WM, wm = wave % WM;
+  const int nt0 = blockIdx.x * WT;
+  const int m0 = blockIdx.y * BM;
+  const bool yvec = flags & 2;
+  const uint8_t* xb = (const uint8_t*)x;
+
+  auto issue = [&](int kc, int st) {
+    uint8_t* base = lds + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < WT / NWAVES; ++i) {
+      const int j = wave * (WT / NWAVES) + i;
+      const int nt = min(nt0 + j, Nt - 1);
+      lds_dma16(packed + ((int64_t)nt * Kc + kc) * 1024 + lane * 16, base + j * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < XR / NWAVES; ++i) {
+      const int j = wave * (XR / NWAVES) + i;
+      const int row = j * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+      const int m = min(m0 + row, M - 1);
+      lds_dma16(xb + ((int64_t)m * ldx + kc * 64 + chunk * 8) * 2, base + WBYTES + j * 1024);
+    }
+  };
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int a = 0; a < FN; ++a)
+#pragma unroll
+    for (int b = 0; b < FM; ++b) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if (i < Kc) issue(i, i);
+  for (int kc = 0; kc < Kc; ++kc) {
+    const int st = kc % NS;
+    // this wave's DMA of stage kc is complete once at most the younger
+    // in-flight stages (NS - 2 of them, fewer at the end) remain outstanding
+    if constexpr (NS == 3) {
+      if (kc + 1 < Kc) wait_vmcnt<LPS>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    barrier_nofence();
+    if (kc + NS - 1 < Kc) issue(kc + NS - 1, (kc + NS - 1) % NS);
+    const uint8_t* wb = lds + st * STAGE;
+    const uint8_t* xs = wb + WBYTES;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      V xf[FM];
+#pragma unroll
+      for (int b = 0; b < FM; ++b) xf[b] = *(const V*)(xs + xsw_off(wm * TM + b * 16 + r, 2 * g + s));
+#pragma unroll
+      for (int a = 0; a < FN; ++a) {
+        const u32x2 raw = *(const u32x2*)(wb + (wn * FN + a) * 1024 + lane * 16 + s * 8);
+        V wf0, wf1;
+        Op::wconv((u32x4){raw.x, raw.y, 0u, 0u}, wf0, wf1);
+#pragma unroll
+        for (int b = 0; b < FM; ++b) acc[a][b] = Op::mma(wf0, xf[b], acc[a][b]);
+      }
+    }
+    if constexpr (NS == 2) barrier_nofence();  // stage st is overwritten by the next issue
+  }
+
+#pragma unroll
+  for (int a = 0; a < FN; ++a) {
+    const int n = (nt0 + wn * FN + a) * 16 + 4 * g;
+    if (n >= N) continue;
+    const int nvalid = min(4, N - n);
+    f32x4 sc, bi;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int nn = min(n + v, N - 1);
+      sc[v] = scale[nn];
+      bi[v] = bias ? bias[nn] : 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < FM; ++b) {
+      const int m = m0 + wm * TM + b * 16 + r;
+      if (m >= M) continue;
+      f32x4 o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float out = acc[a][b][v] * sc[v];
+        if (bias) out = out + bi[v];
+        o[v] = out;
+      }
+      store_y4(y, yt, (int64_t)m * ldy + n, o, yvec && nvalid == 4, nvalid);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 constexpr int kBN = 128, kBM = 128, kWN = 2, kWM = 2;
@@ -372,8 +525,16 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
                    const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
                    bool yvec) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
-  dim3 grid((unsigned)((Nt + kBN / 16 - 1) / (kBN / 16)), (unsigned)((M + kBM - 1) / kBM)), block(kWN * kWM * 64);
   const int flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
+  if (xvec && K % 64 == 0 && xt != XT_F32) {
+    dim3 g2((unsigned)((Nt + 15) / 16), (unsigned)((M + 127) / 128));
+    if (xt == XT_F16)
+      hipLaunchKernelGGL((gemm_w8_dl_kernel<XT_F16, 256, 128, 4, 2, 2>), g2, dim3(512), 0, st, x, ldx, (int)M, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, flags);
+    else
+      hipLaunchKernelGGL((gemm_w8_dl_kernel<XT_BF16, 256, 128, 4, 2, 2>), g2, dim3(512), 0, st, x, ldx, (int)M, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, flags);
+    return check_launch();
+  }
+  dim3 grid((unsigned)((Nt + kBN / 16 - 1) / (kBN / 16)), (unsigned)((M + kBM - 1) / kBM)), block(kWN * kWM * 64);
   switch (xt) {
     case XT_F16: hipLaunchKernelGGL((gemm_w8_kernel<XT_F16, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, flags); break;
     case XT_BF16: hipLaunchKernelGGL((gemm_w8_kernel<XT_BF16, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, flags); break;
