@@ -274,6 +274,125 @@ def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3):
 
 
 # ---------------------------------------------------------------------------
+# profile helpers: the workload of the two rocprofv3 --pmc passes, and the
+# summaries of rocprofv3 output that are committed under profiles/
+# ---------------------------------------------------------------------------
+CAL_BYTES = 1 << 30  # calibration copy: 1 GiB read + 1 GiB written, beyond the 256 MB Infinity Cache
+DOMINANT_BLOCK = 512  # the gate+up launch at M=1: one 512-lane group (8 waves) per 16 rows
+DOMINANT_GRID = ((DOMINANT[0] + 15) // 16) * DOMINANT_BLOCK
+
+
+def traffic_probe(ctx, launches=24, cal_reps=4):
+    """Eager launches of the dominant kernel (weights rotating beyond the
+    Infinity Cache) followed by a plain copy kernel of known size (torch.neg
+    on 1 GiB of fp16), for FETCH_SIZE / WRITE_SIZE counter passes."""
+    torch, quant = ctx.torch, ctx.quant
+    N, K = DOMINANT
+    copies = math.ceil(ROTATE_BYTES / (N * K)) + 1
+    layers = [ctx.weights(N, K, 500 + c) for c in range(copies)]
+    x = ctx.act(1, K, 7)
+    y = torch.empty((1, N), dtype=torch.float16, device=ctx.dev)
+    a = torch.ones(CAL_BYTES // 2, dtype=torch.float16, device=ctx.dev)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for i in range(launches):
+        packed, s, _ = layers[i % copies]
+        quant.linear_w8(x, packed, s, None, N, out=y)
+    torch.cuda.synchronize()
+    for _ in range(cal_reps):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    log(f"traffic probe: {launches} gate+up launches, {cal_reps} copies of {CAL_BYTES >> 20} MiB")
+
+
+def _csv_rows(d, suffix):
+    import csv
+
+    files = sorted(Path(d).rglob(f"*{suffix}"))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {d}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            rows += list(csv.DictReader(fh))
+    return rows
+
+
+def _short(name):
+    name = name.replace("void ", "")
+    return name.split("(")[0] if name.startswith("sbq::") else name[:60]
+
+
+def summarize_trace(d, command):
+    """Markdown summary of a rocprofv3 --kernel-trace --stats run: kernels by
+    total time, split by launch grid, and the dominant kernel's average."""
+    import statistics
+
+    rows = _csv_rows(d, "kernel_trace.csv")
+    agg = {}
+    for r in rows:
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        key = (_short(r["Kernel_Name"]), grid, int(r["Workgroup_Size_X"]))
+        agg.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    total = sum(sum(v) for v in agg.values())
+    out = ["# rocprofv3 kernel trace of the default bench run", "", "Command:", "", "```", command, "```", "",
+           f"Dispatches: {sum(len(v) for v in agg.values())}, kernel time {total / 1e3:.1f} ms.", "",
+           "| kernel | grid (work-items) | block | calls | avg us | median us | min us | % time |",
+           "|---|---|---|---|---|---|---|---|"]
+    for (name, grid, wg), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:25]:
+        out.append(f"| `{name}` | {grid} | {wg} | {len(v)} | {statistics.mean(v):.2f} | {statistics.median(v):.2f} | "
+                   f"{min(v):.2f} | {100 * sum(v) / total:.1f} |")
+    dom = [(k, v) for k, v in agg.items()
+           if k[0].startswith("sbq::gemv_kernel") and k[1] == DOMINANT_GRID and k[2] == DOMINANT_BLOCK]
+    if dom:
+        (name, grid, wg), v = max(dom, key=lambda kv: len(kv[1]))
+        nbytes = gemv_bytes(1, *DOMINANT)
+        out += ["", f"Dominant kernel (gate+up {DOMINANT[0]}x{DOMINANT[1]}, M=1): `{name}`, grid {grid}: "
+                f"{len(v)} calls, average {statistics.mean(v):.3f} us, median {statistics.median(v):.3f} us "
+                f"-> {nbytes / (statistics.mean(v) * 1e3):.0f} GB/s of algorithmic bytes ({nbytes} per launch)."]
+    stats = sorted(Path(d).rglob("*kernel_stats.csv"))
+    if stats:
+        out += ["", "rocprofv3 --stats (by kernel name, top 12):", "", "```"]
+        for line in stats[0].read_text().splitlines()[:13]:
+            name, _, rest = line.partition('",')
+            out.append((name[:110] + ('..."' if len(name) > 110 else '"')) + "," + rest)
+        out += ["```"]
+    return "\n".join(out) + "\n"
+
+
+def summarize_pmc(fetch_dir, write_dir, commands):
+    """HBM traffic per launch of the dominant kernel from FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch), each scaled by what the same counter reads
+    for the calibration copy of CAL_BYTES."""
+    import statistics
+
+    def per_dispatch(d, counter):
+        acc = {}
+        for r in _csv_rows(d, "counter_collection.csv"):
+            if r["Counter_Name"] != counter:
+                continue
+            k = (r["Dispatch_Id"], r["Kernel_Name"], int(r["Grid_Size"]), int(r["Workgroup_Size"]))
+            acc[k] = acc.get(k, 0.0) + float(r["Counter_Value"])
+        return acc
+
+    res = {"commands": commands, "calibration": f"torch.neg on {CAL_BYTES} bytes of fp16 (reads and writes "
+                                                 f"{CAL_BYTES} bytes)"}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        acc = per_dispatch(d, counter)
+        dom = [v for (i, n, g, b), v in acc.items() if "gemv_kernel" in n and g == DOMINANT_GRID and b == DOMINANT_BLOCK]
+        cal = [v for (i, n, g, b), v in acc.items() if "neg" in n.lower() and v > CAL_BYTES / 1024 / 4]
+        if not dom or not cal:
+            raise SystemExit(f"{counter}: dominant ({len(dom)}) or calibration ({len(cal)}) dispatches not found")
+        factor = (CAL_BYTES / 1024) / statistics.median(cal)
+        res[counter] = {"dominant_KiB_per_dispatch": statistics.median(dom), "dispatches": len(dom),
+                        "calibration_KiB": statistics.median(cal), "scale": factor,
+                        "bytes_per_launch": statistics.median(dom) * 1024 * factor}
+    res["algorithmic_bytes_per_launch"] = gemv_bytes(1, *DOMINANT)
+    res["traffic_bytes_per_launch"] = res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"]
+    res["traffic_over_algorithmic"] = res["traffic_bytes_per_launch"] / res["algorithmic_bytes_per_launch"]
+    return json.dumps(res, indent=1) + "\n"
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed PMC
     summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy-kernel calibration)."""
@@ -310,7 +429,19 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the dominant kernel and a calibration copy (workload of the --pmc passes)")
+    ap.add_argument("--summarize-trace", metavar="DIR", help="print a markdown summary of a rocprofv3 kernel trace")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print the traffic JSON from FETCH_SIZE and WRITE_SIZE passes over --traffic-probe")
+    ap.add_argument("--command", default="", help="the profiling command(s), recorded in the summary")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.command), end="")
+        return
+    if args.summarize_pmc:
+        print(summarize_pmc(*args.summarize_pmc, args.command), end="")
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported in this build "
               "(the sharding design is described in DESIGN.md)", file=sys.stderr)
@@ -321,6 +452,9 @@ def main():
 
     ctx = Ctx()
     torch = ctx.torch
+    if args.traffic_probe:
+        traffic_probe(ctx)
+        return
     log("decode M=1 (headline)")
     head = decode_bench(ctx, 1, args.steps, args.warmup)
     log(f"  {head['GBps']:.0f} GB/s, {head['ms_per_step'] * 1e3:.1f} us/step")
