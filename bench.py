@@ -189,7 +189,7 @@ def dominant_kernel(ctx, M=1, launches_per_copy=8, reps=5):
     ms = ctx.time_graphs([g], reps, 1)
     us = ms * 1e3 / n
     bytes_per_launch = gemv_bytes(M, N, K)
-    return {"kernel": "sbq::gemv_w8_kernel (gate+up 24576x4096, M=1, fp16 x, fp16 y)", "avg_us": us,
+    return {"kernel": "sbq::gemv_fast_kernel (gate+up 24576x4096, M=1, fp16 x, fp16 y)", "avg_us": us,
             "bytes_per_launch": bytes_per_launch, "GBps": bytes_per_launch / (us * 1e-6) / 1e9,
             "launches": n * reps}
 
@@ -278,8 +278,11 @@ def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3):
 # summaries of rocprofv3 output that are committed under profiles/
 # ---------------------------------------------------------------------------
 CAL_BYTES = 1 << 30  # calibration copy: 1 GiB read + 1 GiB written, beyond the 256 MB Infinity Cache
-DOMINANT_BLOCK = 512  # the gate+up launch at M=1: one 512-lane group (8 waves) per 16 rows
-DOMINANT_GRID = ((DOMINANT[0] + 15) // 16) * DOMINANT_BLOCK
+# the gate+up launch at M=1 (fp16 x): sbq::gemv_fast_kernel, two 16-row tiles per
+# 256-lane workgroup (4 waves splitting K)
+DOMINANT_KERNEL = "gemv_fast_kernel"
+DOMINANT_BLOCK = 256
+DOMINANT_GRID = ((DOMINANT[0] + 31) // 32) * DOMINANT_BLOCK
 
 
 def traffic_probe(ctx, launches=24, cal_reps=4):
@@ -342,14 +345,24 @@ def summarize_trace(d, command):
     for (name, grid, wg), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:25]:
         out.append(f"| `{name}` | {grid} | {wg} | {len(v)} | {statistics.mean(v):.2f} | {statistics.median(v):.2f} | "
                    f"{min(v):.2f} | {100 * sum(v) / total:.1f} |")
-    dom = [(k, v) for k, v in agg.items()
-           if k[0].startswith("sbq::gemv_kernel") and k[1] == DOMINANT_GRID and k[2] == DOMINANT_BLOCK]
-    if dom:
-        (name, grid, wg), v = max(dom, key=lambda kv: len(kv[1]))
+    # the dominant launch signature; the M=1 back-to-back run that bench.py's
+    # roofline times is the part of it whose neighbours are the same launch
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    is_dom = [DOMINANT_KERNEL in r["Kernel_Name"] and int(r["Workgroup_Size_X"]) == DOMINANT_BLOCK and
+              int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]) == DOMINANT_GRID for r in rows]
+    dur = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0 for r in rows]
+    allv = [d for d, f in zip(dur, is_dom) if f]
+    run = [dur[i] for i in range(1, len(rows) - 1) if is_dom[i - 1] and is_dom[i] and is_dom[i + 1]]
+    if run:
         nbytes = gemv_bytes(1, *DOMINANT)
-        out += ["", f"Dominant kernel (gate+up {DOMINANT[0]}x{DOMINANT[1]}, M=1): `{name}`, grid {grid}: "
-                f"{len(v)} calls, average {statistics.mean(v):.3f} us, median {statistics.median(v):.3f} us "
-                f"-> {nbytes / (statistics.mean(v) * 1e3):.0f} GB/s of algorithmic bytes ({nbytes} per launch)."]
+        name = _short(next(r["Kernel_Name"] for r, f in zip(rows, is_dom) if f))
+        out += ["", f"Dominant kernel (gate+up {DOMINANT[0]}x{DOMINANT[1]}, M=1): `{name}`, grid {DOMINANT_GRID}, "
+                f"block {DOMINANT_BLOCK}.",
+                f"Back-to-back launches (the run bench.py's roofline times): {len(run)}, average "
+                f"{statistics.mean(run):.3f} us, median {statistics.median(run):.3f} us -> "
+                f"{nbytes / (statistics.mean(run) * 1e3):.0f} GB/s of algorithmic bytes ({nbytes} per launch).",
+                f"All launches with this signature (also the M=1 and M=4 decode steps): {len(allv)}, average "
+                f"{statistics.mean(allv):.3f} us."]
     stats = sorted(Path(d).rglob("*kernel_stats.csv"))
     if stats:
         out += ["", "rocprofv3 --stats (by kernel name, top 12):", "", "```"]
@@ -379,7 +392,8 @@ def summarize_pmc(fetch_dir, write_dir, commands):
                                                  f"{CAL_BYTES} bytes)"}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         acc = per_dispatch(d, counter)
-        dom = [v for (i, n, g, b), v in acc.items() if "gemv_kernel" in n and g == DOMINANT_GRID and b == DOMINANT_BLOCK]
+        dom = [v for (i, n, g, b), v in acc.items()
+               if DOMINANT_KERNEL in n and g == DOMINANT_GRID and b == DOMINANT_BLOCK]
         cal = [v for (i, n, g, b), v in acc.items() if "neg" in n.lower() and v > CAL_BYTES / 1024 / 4]
         if not dom or not cal:
             raise SystemExit(f"{counter}: dominant ({len(dom)}) or calibration ({len(cal)}) dispatches not found")

@@ -1,0 +1,347 @@
+// sbq_gemv_fast.hip - decode GEMV for the aligned common case.
+//
+// Replaces spikingbrain_cpu/quant.py:41-53 (Int8Linear.forward, weight-only)
+// and quant.py:63-66 (DynamicInt8Linear.forward, W8A8) at decode shapes when
+// M <= 16, K % 64 == 0 and the activation rows are 16-byte aligned - every
+// projection of the model (K = 128, 2560, 4096, 9728, 12288).  Other shapes
+// take the general kernel in sbq_gemv.hip.
+//
+// A workgroup of KS waves owns G consecutive 16-row weight tiles.  Wave ks
+// covers the K tiles [ks*KW, ks*KW + KW) and streams them D at a time: the D
+// (x G) tile loads of the next step are issued right after the tiles of the
+// current step are consumed.  Loads are never guarded by branches (indexes are
+// clamped instead, and the few surplus tiles of the last step are not
+// multiplied), so the compiler's s_waitcnt counting is exact: each tile waits
+// for itself only.
+//
+// Activations, in one of two modes:
+//   XL   the workgroup copies x[M][K] into LDS with global_load_lds (16 bytes
+//        per lane straight into LDS) before its weight loads, waits for those
+//        copies only (vmcnt = number of weight loads issued after them) and
+//        reads fragments from LDS on use;
+//   direct  each lane loads its 16-element fragment of row min(r, M-1) per
+//        tile from global memory (L2-resident) next to the weight tile.
+// Lanes of rows >= M compute on a duplicate row and never store.
+//
+// Per-wave partial tiles are summed through LDS in wave order 0..KS-1 by wave
+// t for row tile t, then scale / bias (W8A8: zero-point correction and the
+// fbgemm requantization) are applied and each lane stores 4 outputs.
+// Barriers are s_barrier without __syncthreads()'s fence: the fence would wait
+// for every outstanding weight load.
+#include <type_traits>
+
+#include "sbq_common.h"
+#include "sbq_gemv_ops.h"
+#include "sbq_launch.h"
+
+namespace sbq {
+
+namespace {
+
+constexpr int kFastXLdsBytes = 32768;  // x[M][K] copied to LDS up to this size
+constexpr int kFastMaxWaves = 8;
+
+__device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// LDS writes of this wave complete, then a workgroup barrier with no vmcnt wait.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 16 consecutive activations of one row from global memory or LDS.
+template <int XT>
+__device__ __forceinline__ void load_frag(XRaw<XT>& f, const uint8_t* p) {
+  if constexpr (XT == XT_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.v[i] = *(const f32x4*)(p + 16 * i);
+  } else {
+    typedef decltype(f.a) V;
+    f.a = *(const V*)p;
+    f.b = *(const V*)(p + 16);
+  }
+}
+
+// s8 fragment (xq - 128) of 16 raw activations.
+template <int XT>
+__device__ __forceinline__ i32x4 quant16(const XRaw<XT>& f, float inv, float zpf) {
+  uint32_t d[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) word |= ((uint32_t)quant_act_s8(f.get(4 * i + j), inv, zpf) & 0xffu) << (8 * j);
+    d[i] = word;
+  }
+  return (i32x4){(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+}
+
+// LDS layout: [KS][G][64] partial tiles (16 bytes each), then per-wave
+// (min, max) pairs, then the x copy.
+template <int G>
+__host__ __device__ constexpr int red_bytes(int ks) { return ks * G * 64 * 16; }
+__host__ __device__ constexpr int mm_bytes() { return kFastMaxWaves * 8; }
+
+}  // namespace
+
+template <int XT, int D, int G, bool XL, bool W8A8>
+__global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs a, int KW, int xch) {
+  typedef typename std::conditional<W8A8, i32x4, f32x4>::type Acc;
+  constexpr int EB = x_bytes<XT>();
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int KS = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, ks = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int M = a.M, Kc = a.Kc, K = a.K;
+  const int nt0 = blockIdx.x * G;
+  const int kbeg = ks * KW;
+  const int cnt = min(KW, Kc - kbeg);  // >= 1: the host sizes KS so that every wave has a tile
+  const int mr = min(r, M - 1);
+  Acc* red = (Acc*)smem;
+  float2* mmx = (float2*)(smem + red_bytes<G>(KS));
+  uint8_t* xs = smem + red_bytes<G>(KS) + mm_bytes();
+  const int xrow = K * EB;  // bytes of one x row in LDS
+
+  // epilogue operands of row tile `ks` (wave ks < G finishes tile ks)
+  const int nte = min(nt0 + min(ks, G - 1), a.Nt - 1);
+  const int ne = nte * 16 + 4 * g;
+  f32x4 sc = {0.f, 0.f, 0.f, 0.f}, bi = {0.f, 0.f, 0.f, 0.f};
+  i32x4 cs = {0, 0, 0, 0};
+  if (ks < G) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int nn = min(ne + v, a.N - 1);
+      sc[v] = a.scale[nn];
+      if (a.bias) bi[v] = a.bias[nn];
+      if constexpr (W8A8) cs[v] = a.colsum[nn];
+    }
+  }
+  // W8A8: min/max partials of the activation pre-pass (duplicates are harmless)
+  float2 part = {0.f, 0.f};
+  if constexpr (W8A8) part = a.partials[min(tid, a.nparts - 1)];
+
+  // x copy into LDS: xch 16-byte chunks per thread, sources clamped
+  const uint8_t* xg = (const uint8_t*)a.x;
+  if constexpr (XL) {
+    const int cpr = xrow / 16, nch = M * cpr;
+    for (int i = 0; i < xch; ++i) {
+      const int c0 = i * blockDim.x + ks * 64;  // first chunk of this wave
+      const int c = min(c0 + lane, nch - 1);
+      const int m = c / cpr;
+      lds_copy16(xg + (int64_t)m * a.ldx * EB + (c - m * cpr) * 16, xs + c0 * 16);
+    }
+  }
+
+  // first D tiles (and direct activations)
+  const uint8_t* wp[G];
+#pragma unroll
+  for (int j = 0; j < G; ++j) wp[j] = a.packed + ((int64_t)min(nt0 + j, a.Nt - 1) * Kc + kbeg) * 1024 + lane * 16;
+  const uint8_t* xp = xg + (int64_t)mr * a.ldx * EB + ((int64_t)kbeg * 64 + g * 16) * EB;
+  u32x4 w[D][G];
+  XRaw<XT> xd[XL ? 1 : D];
+#pragma unroll
+  for (int p = 0; p < D; ++p) {
+    const int kt = min(p, cnt - 1);
+    if constexpr (!XL) load_frag<XT>(xd[p], xp + kt * 64 * EB);
+#pragma unroll
+    for (int j = 0; j < G; ++j) w[p][j] = load_tile_nt(wp[j] + kt * 1024);
+  }
+
+  ActQParams qp = {};
+  if constexpr (XL || W8A8) {
+    if constexpr (W8A8) {
+      const float mn = wave_min(part.x), mx = wave_max(part.y);
+      if (lane == 0) mmx[ks] = make_float2(mn, mx);
+    }
+    if constexpr (XL) wait_vm<D * G>();  // this wave's x copies are in LDS; weights stay in flight
+    lds_barrier();
+    if constexpr (W8A8) {
+      float mn = 0.0f, mx = 0.0f;
+      for (int i = 0; i < KS; ++i) {
+        const float2 v = mmx[i];
+        mn = fminf(mn, v.x);
+        mx = fmaxf(mx, v.y);
+      }
+      qp = choose_act_qparams(mn, mx);
+    }
+  }
+
+  Acc acc[G];
+#pragma unroll
+  for (int j = 0; j < G; ++j) acc[j] = Acc{0, 0, 0, 0};
+  const uint8_t* xl = xs + mr * xrow + g * 16 * EB;
+  auto step = [&](int p, int kt) {  // kt: tile index within this wave's range
+    XRaw<XT> f;
+    if constexpr (XL) load_frag<XT>(f, xl + (kbeg + kt) * 64 * EB);
+    else f = xd[p];
+    if constexpr (W8A8) {
+      const i32x4 q = quant16<XT>(f, qp.inv, qp.zpf);
+#pragma unroll
+      for (int j = 0; j < G; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_to_s8(w[p][j]), q, acc[j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < G; ++j) tile_mma<XT>(w[p][j], f, acc[j]);
+    }
+  };
+  int t = 0;
+  for (; t + D < cnt; t += D) {
+#pragma unroll
+    for (int p = 0; p < D; ++p) {
+      step(p, t + p);
+      const int kt = min(t + D + p, cnt - 1);
+      if constexpr (!XL) load_frag<XT>(xd[p], xp + kt * 64 * EB);
+#pragma unroll
+      for (int j = 0; j < G; ++j) w[p][j] = load_tile_nt(wp[j] + kt * 1024);
+      // keep each refill next to the step that freed its registers (otherwise
+      // the refills sink to the end of the batch and the ring drains)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < D; ++p)
+    if (t + p < cnt) step(p, t + p);
+
+  // cross-wave sum in wave order, epilogue by wave j for row tile j
+  if (KS > 1) {
+#pragma unroll
+    for (int j = 0; j < G; ++j) red[(ks * G + j) * 64 + lane] = acc[j];
+    lds_barrier();
+  }
+  if (ks >= G || r >= M) return;
+  const int nt = nt0 + ks;
+  const int n = nt * 16 + 4 * g;
+  if (nt >= a.Nt || n >= a.N) return;
+  Acc s;
+  if (KS > 1) {
+    s = red[ks * 64 + lane];
+    for (int i = 1; i < KS; ++i) s += red[(i * G + ks) * 64 + lane];
+  } else {
+    s = acc[0];  // one wave implies one row tile (the host keeps KS >= G)
+  }
+  const int nvalid = min(4, a.N - n);
+  f32x4 o;
+  if constexpr (W8A8) {
+    const int corr = 128 - qp.zp;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int av = s[v] + corr * cs[v];
+      if (a.acc_out && v < nvalid) a.acc_out[(int64_t)r * a.N + n + v] = av;
+      const float mult = qp.scale * sc[v];
+      o[v] = a.bias ? __builtin_fmaf((float)av, mult, bi[v]) : (float)av * mult;
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float out = s[v] * sc[v];
+      if (a.bias) out = out + bi[v];
+      o[v] = out;
+    }
+  }
+  store_y4(a.y, a.yt, (int64_t)r * a.ldy + n, o, (a.flags & 2) && nvalid == 4, nvalid);
+}
+
+namespace {
+
+// Instances: (D, G, XL).  XL uses LDS-resident x; direct modes keep D
+// fragments in registers, so they use smaller D.
+#define SBQ_FAST_CONFIGS(X) \
+  X(0, 8, 1, true)          \
+  X(1, 16, 1, true)         \
+  X(2, 4, 1, false)         \
+  X(3, 8, 1, false)         \
+  X(4, 4, 2, false)         \
+  X(5, 8, 2, false)
+
+struct FastCfg {
+  int id, D, G;
+  bool XL;
+};
+constexpr FastCfg kFastCfgs[] = {
+#define SBQ_FAST_ROW(id, D, G, XL) {id, D, G, XL},
+    SBQ_FAST_CONFIGS(SBQ_FAST_ROW)
+#undef SBQ_FAST_ROW
+};
+constexpr int kNumFastCfgs = sizeof(kFastCfgs) / sizeof(kFastCfgs[0]);
+
+template <int XT, bool W8A8>
+int launch_fast_typed(int id, const GemvArgs& a, int ks, int KW, int xch, size_t lds, hipStream_t st) {
+  const dim3 block(ks * 64);
+  switch (id) {
+#define SBQ_FAST_CASE(ID, D, G, XL)                                                                         \
+  case ID:                                                                                                  \
+    hipLaunchKernelGGL((gemv_fast_kernel<XT, D, G, XL, W8A8>), dim3((a.Nt + G - 1) / G), block, lds, st, a, KW, \
+                       xch);                                                                                \
+    return check_launch();
+    SBQ_FAST_CONFIGS(SBQ_FAST_CASE)
+#undef SBQ_FAST_CASE
+  }
+  return -1;
+}
+
+}  // namespace
+
+// Launch of fast-path configuration `id` with `ks` waves per workgroup
+// (returns -1 when the configuration cannot run this shape).
+int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, hipStream_t st) {
+  if (id < 0 || id >= kNumFastCfgs || ks < 1 || ks > kFastMaxWaves) return -1;
+  const FastCfg c = kFastCfgs[id];
+  if (a.M < 1 || a.M > 16 || a.K != a.Kc * 64 || !(a.flags & 1)) return -1;
+  const int KW = (a.Kc + ks - 1) / ks;
+  ks = (a.Kc + KW - 1) / KW;  // every wave gets at least one K tile
+  if (ks < c.G) return -1;                  // each row tile's epilogue belongs to one wave
+  if (w8a8 && ks * 64 < a.nparts) return -1;  // one min/max partial per thread
+  const int eb = xt == XT_F32 ? 4 : 2;
+  const int64_t xbytes = (int64_t)a.M * a.K * eb;
+  if (c.XL && xbytes > kFastXLdsBytes) return -1;
+  if (c.D * c.G > 32) return -1;
+  const int T = ks * 64;
+  const int xch = c.XL ? (int)((xbytes / 16 + T - 1) / T) : 0;
+  const size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
+  switch (xt) {
+    case XT_F16: return w8a8 ? launch_fast_typed<XT_F16, true>(id, a, ks, KW, xch, lds, st)
+                             : launch_fast_typed<XT_F16, false>(id, a, ks, KW, xch, lds, st);
+    case XT_BF16: return w8a8 ? launch_fast_typed<XT_BF16, true>(id, a, ks, KW, xch, lds, st)
+                              : launch_fast_typed<XT_BF16, false>(id, a, ks, KW, xch, lds, st);
+    case XT_F32: return w8a8 ? launch_fast_typed<XT_F32, true>(id, a, ks, KW, xch, lds, st)
+                             : launch_fast_typed<XT_F32, false>(id, a, ks, KW, xch, lds, st);
+  }
+  return -2;
+}
+
+// Fast-path choice for a shape (false: the general kernel runs).  Measured on
+// MI355X over the decode shapes (M = 1, 4, 16; K = 4096, 12288; N = 4096 ..
+// 151936): 4-tile steps over two row tiles per wave for wide K = 4096 layers,
+// 8-tile steps over one row tile for long K or narrow N, two waves per row tile
+// once M > 4 (the activation fragments then dominate the registers), and
+// 4-tile single-row-tile steps for fp32 / bf16 activations (costlier
+// conversion, larger fragments).
+bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks) {
+  if (M < 1 || M > 16 || K % 64 != 0 || !xvec) return false;
+  const int64_t Kc = K / 64, Nt = (N + 15) / 16;
+  if (xt != XT_F16) {
+    *id = 2;  // D=4, G=1
+    *ks = Kc >= 128 ? 8 : 4;
+  } else if (M <= 4) {
+    const bool wide = Kc < 128 && Nt >= 384;
+    *id = wide ? 4 : 3;  // D=4, G=2 | D=8, G=1
+    *ks = 4;
+  } else {
+    const bool wide = Kc <= 64 && Nt >= 384;
+    *id = wide ? 5 : 3;  // D=8, G=2 | D=8, G=1
+    *ks = 2;
+  }
+  if (w8a8 && *ks * 64 < std::min<int64_t>(kMinMaxPartials, (M * K + 4095) / 4096)) *ks = 4;
+  return true;
+}
+
+}  // namespace sbq

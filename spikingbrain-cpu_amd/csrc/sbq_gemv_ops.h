@@ -1,0 +1,191 @@
+// sbq_gemv_ops.h - activation fragments and MFMA steps shared by the decode
+// GEMV kernels (sbq_gemv.hip: general shapes; sbq_gemv_fast.hip: the common
+// aligned case).
+#pragma once
+#include <type_traits>
+
+#include "sbq_common.h"
+
+namespace sbq {
+
+// Arguments of the decode GEMV kernels (one struct, passed by value).
+struct GemvArgs {
+  const void* x;
+  int64_t ldx;
+  int M, K, Kc;
+  const uint8_t* packed;
+  const float* scale;
+  const float* bias;
+  const int32_t* colsum;
+  int N, Nt, ngroups;
+  void* y;
+  int yt;
+  int64_t ldy;
+  int32_t* acc_out;
+  const float2* partials;
+  int nparts;
+  int flags;
+};
+
+// ---------------------------------------------------------------------------
+// Raw activations of one lane: x[m][k0 .. k0+15], m = mt*16 + r,
+// k0 = kc*64 + g*16.  Rows >= M and columns >= K read as zero.
+// ---------------------------------------------------------------------------
+template <int XT>
+struct XRaw;
+
+template <>
+struct XRaw<XT_F16> {
+  f16x8 a, b;
+  __device__ __forceinline__ void load(const void* x, int64_t ldx, int M, int K, int m, int k0, bool xvec) {
+    const _Float16* p = (const _Float16*)x + (int64_t)m * ldx + k0;
+    if (m < M && xvec && k0 + 16 <= K) {
+      a = *(const f16x8*)p;
+      b = *(const f16x8*)(p + 8);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        a[j] = (m < M && k0 + j < K) ? p[j] : (_Float16)0.0f;
+        b[j] = (m < M && k0 + 8 + j < K) ? p[8 + j] : (_Float16)0.0f;
+      }
+    }
+  }
+  __device__ __forceinline__ float get(int j) const { return j < 8 ? (float)a[j] : (float)b[j - 8]; }
+  __device__ __forceinline__ void load_lds(const uint8_t* xl, int Kp, int M, int m, int k0) {
+    if (m < M) {
+      const _Float16* p = (const _Float16*)xl + m * Kp + k0;
+      a = *(const f16x8*)p;
+      b = *(const f16x8*)(p + 8);
+    } else {
+      a = f16x8{};
+      b = f16x8{};
+    }
+  }
+};
+
+template <>
+struct XRaw<XT_BF16> {
+  bf16x8 a, b;
+  __device__ __forceinline__ void load(const void* x, int64_t ldx, int M, int K, int m, int k0, bool xvec) {
+    const __bf16* p = (const __bf16*)x + (int64_t)m * ldx + k0;
+    if (m < M && xvec && k0 + 16 <= K) {
+      a = *(const bf16x8*)p;
+      b = *(const bf16x8*)(p + 8);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        a[j] = (m < M && k0 + j < K) ? p[j] : (__bf16)0.0f;
+        b[j] = (m < M && k0 + 8 + j < K) ? p[8 + j] : (__bf16)0.0f;
+      }
+    }
+  }
+  __device__ __forceinline__ float get(int j) const { return j < 8 ? (float)a[j] : (float)b[j - 8]; }
+  __device__ __forceinline__ void load_lds(const uint8_t* xl, int Kp, int M, int m, int k0) {
+    if (m < M) {
+      const __bf16* p = (const __bf16*)xl + m * Kp + k0;
+      a = *(const bf16x8*)p;
+      b = *(const bf16x8*)(p + 8);
+    } else {
+      a = bf16x8{};
+      b = bf16x8{};
+    }
+  }
+};
+
+template <>
+struct XRaw<XT_F32> {
+  f32x4 v[4];
+  __device__ __forceinline__ void load(const void* x, int64_t ldx, int M, int K, int m, int k0, bool xvec) {
+    const float* p = (const float*)x + (int64_t)m * ldx + k0;
+    if (m < M && xvec && k0 + 16 <= K) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = *(const f32x4*)(p + 4 * i);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j >> 2][j & 3] = (m < M && k0 + j < K) ? p[j] : 0.0f;
+    }
+  }
+  __device__ __forceinline__ float get(int j) const { return v[j >> 2][j & 3]; }
+  __device__ __forceinline__ void load_lds(const uint8_t* xl, int Kp, int M, int m, int k0) {
+    if (m < M) {
+      const float* p = (const float*)xl + m * Kp + k0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = *(const f32x4*)(p + 4 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = f32x4{};
+    }
+  }
+};
+
+// Element bytes of an activation type.
+template <int XT>
+constexpr int x_bytes() { return XT == XT_F32 ? 4 : 2; }
+
+// Default number of 16-byte chunks of x per thread the LDS staging holds.
+constexpr int kStageChunks = 4;
+
+// Weight tile (16 offset-binary bytes of one lane) x activation fragment ->
+// MFMA into acc.  fp16/bf16 activations are exact operands; fp32 activations
+// run as bf16 hi + bf16 remainder (two passes, remainder first).
+template <int XT>
+__device__ __forceinline__ void tile_mma(u32x4 w, const XRaw<XT>& x, f32x4& acc) {
+  if constexpr (XT == XT_F16) {
+    f16x8 w0, w1;
+    u8x16_to_f16(w, w0, w1);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w0, x.a, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1, x.b, acc, 0, 0, 0);
+  } else if constexpr (XT == XT_BF16) {
+    bf16x8 w0, w1;
+    u8x16_to_bf16(w, w0, w1);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, x.a, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, x.b, acc, 0, 0, 0);
+  } else {
+    bf16x8 w0, w1, h0, h1, l0, l1;
+    u8x16_to_bf16(w, w0, w1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      __bf16 h, l;
+      split_bf16(x.get(j), h, l);
+      h0[j] = h;
+      l0[j] = l;
+      split_bf16(x.get(8 + j), h, l);
+      h1[j] = h;
+      l1[j] = l;
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, l0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, l1, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, h0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, h1, acc, 0, 0, 0);
+  }
+}
+
+// s8 activation fragment (xq - 128) from raw values; columns >= K and rows
+// >= M become 0 (they meet zero weights or are never stored).
+template <int XT>
+__device__ __forceinline__ i32x4 quant_frag(const XRaw<XT>& x, int M, int K, int m, int k0, float inv, float zpf) {
+  uint32_t d[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int jj = 4 * i + j;
+      const int qv = (m < M && k0 + jj < K) ? quant_act_s8(x.get(jj), inv, zpf) : 0;
+      word |= ((uint32_t)qv & 0xffu) << (8 * j);
+    }
+    d[i] = word;
+  }
+  return (i32x4){(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+}
+
+__device__ __forceinline__ i32x4 tile_to_s8(u32x4 w) {
+  return (i32x4){(int)(w.x ^ 0x80808080u), (int)(w.y ^ 0x80808080u), (int)(w.z ^ 0x80808080u),
+                 (int)(w.w ^ 0x80808080u)};
+}
+
+__device__ __forceinline__ u32x4 load_tile_nt(const uint8_t* p) {
+  return __builtin_nontemporal_load((const u32x4*)p);
+}
+
+}  // namespace sbq

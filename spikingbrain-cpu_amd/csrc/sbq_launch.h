@@ -26,6 +26,13 @@ int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t
 // True when the streaming GEMV kernels take this M and K (otherwise the GEMM).
 bool gemv_supports(int64_t M, int64_t K, bool w8a8, int xt);
 
+// Decode fast path (sbq_gemv_fast.hip): M <= 16, K % 64 == 0, aligned x rows.
+// pick_gemv_fast chooses a configuration id and the waves per workgroup;
+// launch_gemv_fast_cfg returns -1 when that configuration cannot run the shape.
+struct GemvArgs;
+bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks);
+int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, hipStream_t st);
+
 // Weight-only linear.  xvec: x and every row of x start 16-byte aligned (vector
 // loads allowed).  yvec: y rows are 16-byte aligned and N % 4 == 0.
 int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,

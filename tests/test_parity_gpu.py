@@ -155,6 +155,32 @@ def test_w8_bias_and_strided_input(dev):
     assert oracle.rel_l2(y2.cpu().numpy(), ref2) <= 1e-5
 
 
+FAST_CASES = [
+    # decode fast path (M <= 16, K % 64 == 0, aligned rows): odd tile counts
+    # with two row tiles per wave, ragged N, M on both sides of 4, long K
+    (1, 6152, 4096), (3, 6160, 4096), (5, 6144, 4096), (8, 4100, 12288), (16, 6152, 2560), (2, 24, 64),
+    (1, 4, 128),
+]
+
+
+@pytest.mark.parametrize("xd", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("M,N,K", FAST_CASES)
+def test_w8_fast_path_bias_strided(dev, M, N, K, xd):
+    announce(f"w8 fast M={M} N={N} K={K} x={xd}")
+    w = make_weights(N, K, 5000 + N + K)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(N))
+    big = make_x(M, K + 64, 6000 + M + K).to(DT[xd])
+    x = big[:, 64:]  # row stride K + 64 elements, rows stay 16-byte aligned
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref = oracle.int8_linear(x.float().numpy(), q, s, b.numpy())
+    lin = quant.Int8Linear(w, b)
+    y = quant.linear_w8(big.to(dev)[:, 64:], lin.packed, lin.scale, lin.bias, N)
+    err = oracle.rel_l2(y.cpu().numpy(), ref)
+    assert err <= (W8_TOL if xd == "f32" else 1e-5), err
+    y16 = quant.linear_w8(big.to(dev)[:, 64:], lin.packed, lin.scale, lin.bias, N, torch.float16)
+    assert oracle.rel_l2(y16.float().cpu().numpy(), ref) <= 4e-3
+
+
 def test_w8_golden_fixture(dev):
     announce("w8 golden fixture")
     d = np.load(GOLD / "int8_linear.npz")
@@ -180,13 +206,19 @@ def test_w8_integer_activations_exact(dev):
     xb = x.float().repeat(8, 1).half()  # M = 96 -> GEMM path
     exact_b = np.tile(exact, (8, 1))
     np.testing.assert_array_equal(lin(xb.to(dev)).cpu().numpy(), exact_b)
+    # rows starting one element off 16-byte alignment -> general GEMV kernel
+    big = torch.zeros((M, K + 8), dtype=torch.float16)
+    big[:, 1:1 + K] = x
+    y_mis = quant.linear_w8(big.to(dev)[:, 1:1 + K], lin.packed, lin.scale, None, N)
+    np.testing.assert_array_equal(y_mis.cpu().numpy(), exact)
 
 
 # ---------------------------------------------------------------------------
 # int8-dyn (W8A8, fbgemm semantics): bit-exact
 # ---------------------------------------------------------------------------
 W8A8_CASES = [(1, 4096, 4096), (1, 4, 2560), (5, 64, 4096), (16, 13, 96), (33, 512, 256), (64, 100, 1000),
-              (65, 64, 4096), (128, 1024, 4096), (300, 130, 200)]
+              (65, 64, 4096), (128, 1024, 4096), (300, 130, 200),
+              (3, 6152, 4096), (8, 4100, 12288), (16, 6144, 4096), (2, 24, 64)]
 
 
 @pytest.mark.parametrize("xd", ["f32", "f16", "bf16"])
