@@ -102,7 +102,7 @@ int sbq_unpack_w8(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_
  *    high part and a bf16 remainder (relative representation error <= 2^-16).
  * packed: from sbq_repack_w8.  scale: device fp32 [N].  bias: device fp32 [N]
  * or NULL.  y: device [M, N] (row stride ldy), dtype F32, F16 or BF16.
- * Accumulation is fp32.  M <= 16 runs the HBM-streaming MFMA GEMV; larger M
+ * Accumulation is fp32.  M <= 32 runs the HBM-streaming MFMA GEMV; larger M
  * runs the LDS-tiled MFMA GEMM.
  * workspace: unused by this entry point (pass NULL, 0). */
 int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
@@ -112,7 +112,9 @@ int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
 
 /* ---- int8-dyn W8A8 linear (DynamicInt8Linear.forward, quant.py:63-66) ---- */
 
-/* Workspace bytes sbq_linear_w8a8 / sbq_act_qparams need for an [M, K] input. */
+/* Workspace bytes sbq_linear_w8a8 / sbq_act_qparams need for an [M, K] input:
+ * 2.5 KiB of activation statistics plus M * ceil(K/64)*64 bytes for the
+ * quantized activations of the tiled (M > 32) path, plus alignment slack. */
 int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K);
 
 /* The activation quantization parameters that fbgemm's dynamic linear chooses

@@ -38,9 +38,16 @@ inline bool y_vec_ok(const void* y, int yt, int64_t ldy, int64_t N) {
   return aligned(y, a) && (ldy * esize(yt)) % a == 0 && N % 4 == 0;
 }
 
+// W8A8 workspace layout (from the first 256-byte boundary): min/max partials
+// (kMinMaxPartials float2), then (s_x, zp) in 256 bytes, then the quantized
+// activations xq [M][Kc*64] (s8) for the GEMM path.
+constexpr int64_t kWsPartialBytes = 256 * 8;
+constexpr int64_t kWsQpBytes = 256;
 inline float2* ws_partials(void* workspace) {
   return (float2*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
 }
+inline float* ws_qp(void* workspace) { return (float*)((uint8_t*)ws_partials(workspace) + kWsPartialBytes); }
+inline int8_t* ws_xq(void* workspace) { return (int8_t*)((uint8_t*)ws_qp(workspace) + kWsQpBytes); }
 
 }  // namespace
 
@@ -111,9 +118,10 @@ int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
 }
 
 int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K) {
-  (void)M;
-  (void)K;
-  return 256 + (int64_t)sbq::kMinMaxPartials * (int64_t)sizeof(float2);
+  static_assert(sbq::kMinMaxPartials * sizeof(float2) <= kWsPartialBytes, "partials fit");
+  if (M < 0 || K < 0) return 0;
+  const int64_t xq = M * (((K + 63) / 64) * 64);
+  return 256 + kWsPartialBytes + kWsQpBytes + ((xq + 255) & ~(int64_t)255);
 }
 
 int sbq_act_qparams(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, float* scale_out,
@@ -140,14 +148,11 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
   const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
   hipStream_t st = (hipStream_t)stream;
   float2* parts = ws_partials(workspace);
-  const int np = sbq::minmax_nparts(M, K);
-  rc = sbq::launch_minmax_partials(x, x_dtype, M, K, ldx, parts, np, st);
-  if (rc) return rc;
   if (sbq::gemv_supports(M, K, true, x_dtype))
     return sbq::launch_gemv_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
-                                 parts, np, st, yv);
+                                 parts, st, yv);
   return sbq::launch_gemm_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
-                               parts, np, st, yv);
+                               parts, ws_xq(workspace), ws_qp(workspace), st, yv);
 }
 
 }  // extern "C"

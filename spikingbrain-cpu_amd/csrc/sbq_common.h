@@ -24,6 +24,7 @@ namespace sbq {
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
@@ -75,6 +76,12 @@ __device__ __forceinline__ void u8x16_to_bf16(u32x4 w, bf16x8& s0, bf16x8& s1) {
   u8x4_to_bf16(w.w, t + 12);
   s0 = (bf16x8){t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7]};
   s1 = (bf16x8){t[8], t[9], t[10], t[11], t[12], t[13], t[14], t[15]};
+}
+
+// 16 offset-binary weight bytes of a packed tile -> s8 MFMA operand (q).
+__device__ __forceinline__ i32x4 tile_to_s8(u32x4 w) {
+  return (i32x4){(int)(w.x ^ 0x80808080u), (int)(w.y ^ 0x80808080u), (int)(w.z ^ 0x80808080u),
+                 (int)(w.w ^ 0x80808080u)};
 }
 
 // ---------------------------------------------------------------------------

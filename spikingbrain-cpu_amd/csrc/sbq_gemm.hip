@@ -12,10 +12,11 @@
 //   W-only: weights are converted int8 -> fp16/bf16 in registers (exact) and
 //           multiplied on v_mfma_f32_16x16x32_{f16,bf16}; fp32 activations run
 //           as bf16 hi + lo planes.  Epilogue: * scale[n] (+ bias[n]).
-//   W8A8:   the activation slab is quantized to s8 (xq - 128) while it is
-//           staged, weights are used as s8, v_mfma_i32_16x16x64_i8 accumulates
-//           exactly; epilogue adds (128 - zp) * colsum[n] and applies
-//           fp32(s_x * scale[n]) (+ bias[n] fused), as fbgemm does.
+//   W8A8:   the activations are quantized to s8 (xq - 128) once, by a
+//           pre-pass into the workspace; weights are used as s8,
+//           v_mfma_i32_16x16x64_i8 accumulates exactly; the epilogue adds
+//           (128 - zp) * colsum[n] and applies fp32(s_x * scale[n]) (+ bias[n]
+//           fused), as fbgemm does.
 #include "sbq_common.h"
 #include "sbq_launch.h"
 
@@ -229,140 +230,6 @@ __global__ __launch_bounds__(WN* WM * 64) void gemm_w8_kernel(const void* __rest
   }
 }
 
-template <int XT, int BN, int BM, int WN, int WM>
-__global__ __launch_bounds__(WN* WM * 64) void gemm_w8a8_kernel(
-    const void* __restrict__ x, int64_t ldx, int M, int K, int Kc, const uint8_t* __restrict__ packed,
-    const float* __restrict__ scale, const int32_t* __restrict__ colsum, const float* __restrict__ bias, int N,
-    int Nt, void* __restrict__ y, int yt, int64_t ldy, int32_t* __restrict__ acc_out,
-    const float2* __restrict__ partials, int nparts, int flags) {
-  constexpr int NT = WN * WM * 64;
-  constexpr int TN = BN / WN, TM = BM / WM;
-  constexpr int FN = TN / 16, FM = TM / 16;
-  constexpr int WCH = BN * 4 / NT;
-  constexpr int XCH = BM * 4 / NT;  // 16-value chunks (16 s8 bytes) per thread
-  static_assert(WCH * NT == BN * 4 && XCH * NT == BM * 4, "tile/thread mismatch");
-
-  __shared__ __attribute__((aligned(16))) uint8_t wl[2][BN * 64];
-  __shared__ __attribute__((aligned(16))) uint8_t xl[2][BM * 64];
-  __shared__ float qred[32];
-
-  const ActQParams qp = block_qparams_from_partials(partials, nparts, qred);
-  const bool xvec = flags & 1, yvec = flags & 2;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int r = lane & 15, g = lane >> 4;
-  const int wn = wave / WM, wm = wave % WM;
-  const int nt0 = blockIdx.x * (BN / 16);
-  const int m0 = blockIdx.y * BM;
-
-  u32x4 wreg[WCH];
-  u32x4 xreg[XCH];
-
-  auto gload = [&](int kc) {
-#pragma unroll
-    for (int i = 0; i < WCH; ++i) {
-      const int c = tid + i * NT;
-      const int j = c >> 6, slot = c & 63;
-      if (nt0 + j < Nt) wreg[i] = *(const u32x4*)(packed + ((int64_t)(nt0 + j) * Kc + kc) * 1024 + slot * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < XCH; ++i) {
-      const int c = tid + i * NT;
-      const int row = c >> 2, ch = c & 3;
-      const int m = m0 + row, k0 = kc * 64 + ch * 16;
-      float t[16];
-      load8_f32<XT>(x, ldx, M, K, m, k0, xvec, t);
-      load8_f32<XT>(x, ldx, M, K, m, k0 + 8, xvec, t + 8);
-      uint32_t d[4];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int jj = 4 * p + j;
-          const int qv = (m < M && k0 + jj < K) ? quant_act_s8(t[jj], qp.inv, qp.zpf) : 0;
-          word |= ((uint32_t)qv & 0xffu) << (8 * j);
-        }
-        d[p] = word;
-      }
-      xreg[i] = (u32x4){d[0], d[1], d[2], d[3]};
-    }
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < WCH; ++i) {
-      const int c = tid + i * NT;
-      *(u32x4*)(&wl[buf][c * 16]) = wreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < XCH; ++i) {
-      const int c = tid + i * NT;
-      *(u32x4*)(&xl[buf][xq_off(c >> 2, c & 3)]) = xreg[i];
-    }
-  };
-
-  i32x4 acc[FN][FM];
-#pragma unroll
-  for (int a = 0; a < FN; ++a)
-#pragma unroll
-    for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
-
-  gload(0);
-  sstore(0);
-  __syncthreads();
-
-  for (int kc = 0; kc < Kc; ++kc) {
-    const int buf = kc & 1;
-    if (kc + 1 < Kc) gload(kc + 1);
-    i32x4 wf[FN];
-#pragma unroll
-    for (int a = 0; a < FN; ++a) {
-      const u32x4 w = *(const u32x4*)(&wl[buf][(wn * FN + a) * 1024 + lane * 16]);
-      wf[a] = (i32x4){(int)(w.x ^ 0x80808080u), (int)(w.y ^ 0x80808080u), (int)(w.z ^ 0x80808080u),
-                      (int)(w.w ^ 0x80808080u)};
-    }
-#pragma unroll
-    for (int b = 0; b < FM; ++b) {
-      const int row = wm * TM + b * 16 + r;
-      const i32x4 xf = *(const i32x4*)(&xl[buf][xq_off(row, g)]);
-#pragma unroll
-      for (int a = 0; a < FN; ++a) acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[a], xf, acc[a][b], 0, 0, 0);
-    }
-    if (kc + 1 < Kc) sstore(buf ^ 1);
-    __syncthreads();
-  }
-
-  const int corr = 128 - qp.zp;
-#pragma unroll
-  for (int a = 0; a < FN; ++a) {
-    const int n = (nt0 + wn * FN + a) * 16 + 4 * g;
-    if (n >= N) continue;
-    const int nvalid = min(4, N - n);
-    int cs[4];
-    f32x4 mult, bi;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int nn = min(n + v, N - 1);
-      cs[v] = colsum[nn];
-      mult[v] = qp.scale * scale[nn];
-      bi[v] = bias ? bias[nn] : 0.0f;
-    }
-#pragma unroll
-    for (int b = 0; b < FM; ++b) {
-      const int m = m0 + wm * TM + b * 16 + r;
-      if (m >= M) continue;
-      f32x4 o;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int av = acc[a][b][v] + corr * cs[v];
-        if (acc_out && v < nvalid) acc_out[(int64_t)m * N + n + v] = av;
-        o[v] = bias ? __builtin_fmaf((float)av, mult[v], bi[v]) : (float)av * mult[v];
-      }
-      store_y4(y, yt, (int64_t)m * ldy + n, o, yvec && nvalid == 4, nvalid);
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Direct-to-LDS pipelined GEMM (weight-only, fp16/bf16 activations, K % 64 == 0)
 //
@@ -518,6 +385,156 @@ __global__ __launch_bounds__(WN* WM * 64) void gemm_w8_dl_kernel(const void* __r
 }
 
 // ---------------------------------------------------------------------------
+// W8A8 prefill: the activations are quantized once, into the caller's
+// workspace, as s8 (xq - 128) rows of Kp = Kc*64 bytes (columns >= K are 0 and
+// meet zero weights); gemm_w8a8_dl_kernel then runs the direct-to-LDS
+// pipeline on s8 operands with v_mfma_i32_16x16x64_i8.
+// ---------------------------------------------------------------------------
+template <int XT>
+__global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restrict__ x, int64_t ldx, int M, int K,
+                                                           int Kp, const float2* __restrict__ partials, int nparts,
+                                                           int8_t* __restrict__ xq, float* __restrict__ qp_out,
+                                                           int flags) {
+  __shared__ float red[16];
+  const ActQParams qp = block_qparams_from_partials(partials, nparts, red);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    qp_out[0] = qp.scale;
+    qp_out[1] = __int_as_float(qp.zp);
+  }
+  const int cpr = Kp / 16;
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= (int64_t)M * cpr) return;
+  const int m = (int)(c / cpr), k0 = (int)(c - (int64_t)m * cpr) * 16;
+  float t[16];
+  load8_f32<XT>(x, ldx, M, K, m, k0, flags & 1, t);
+  load8_f32<XT>(x, ldx, M, K, m, k0 + 8, flags & 1, t + 8);
+  uint32_t d[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int jj = 4 * i + j;
+      const int qv = k0 + jj < K ? quant_act_s8(t[jj], qp.inv, qp.zpf) : 0;
+      word |= ((uint32_t)qv & 0xffu) << (8 * j);
+    }
+    d[i] = word;
+  }
+  *(u32x4*)(xq + (int64_t)m * Kp + k0) = (u32x4){d[0], d[1], d[2], d[3]};
+}
+
+// Block tile BN output channels x BM tokens x 64 K, WN x WM waves, NS LDS
+// stages of BN/16 packed weight tiles + BM s8 activation rows (64 bytes,
+// 16-byte chunks XOR-swizzled by (row >> 2) & 3 on the source side, so that
+// the 16 rows one ds_read_b128 quarter-wave reads cover all 64 banks).
+template <int BN, int BM, int WN, int WM, int NS>
+__global__ __launch_bounds__(WN* WM * 64) void gemm_w8a8_dl_kernel(
+    const int8_t* __restrict__ xq, int Kp, int M, int Kc, const uint8_t* __restrict__ packed,
+    const float* __restrict__ scale, const int32_t* __restrict__ colsum, const float* __restrict__ bias, int N,
+    int Nt, void* __restrict__ y, int yt, int64_t ldy, int32_t* __restrict__ acc_out, const float* __restrict__ qpbuf,
+    int flags) {
+  constexpr int NWAVES = WN * WM;
+  constexpr int TN = BN / WN, TM = BM / WM, FN = TN / 16, FM = TM / 16;
+  constexpr int WT = BN / 16;          // weight tiles per stage
+  constexpr int XR = BM * 64 / 1024;   // 1 KiB activation chunks (16 rows) per stage
+  constexpr int WBYTES = WT * 1024, STAGE = WBYTES + BM * 64;
+  constexpr int LPS = (WT + XR) / NWAVES;
+  static_assert(WT % NWAVES == 0 && XR % NWAVES == 0, "even DMA split");
+  static_assert(NS == 2 || NS == 3, "stages");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int wn = wave / WM, wm = wave % WM;
+  const int nt0 = blockIdx.x * WT;
+  const int m0 = blockIdx.y * BM;
+  const bool yvec = flags & 2;
+
+  auto issue = [&](int kc, int st) {
+    uint8_t* base = lds + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < WT / NWAVES; ++i) {
+      const int j = wave * (WT / NWAVES) + i;
+      const int nt = min(nt0 + j, Nt - 1);
+      lds_dma16(packed + ((int64_t)nt * Kc + kc) * 1024 + lane * 16, base + j * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < XR / NWAVES; ++i) {
+      const int j = wave * (XR / NWAVES) + i;
+      const int row = j * 16 + (lane >> 2);
+      const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+      const int m = min(m0 + row, M - 1);
+      lds_dma16(xq + (int64_t)m * Kp + kc * 64 + chunk * 16, base + WBYTES + j * 1024);
+    }
+  };
+
+  i32x4 acc[FN][FM];
+#pragma unroll
+  for (int a = 0; a < FN; ++a)
+#pragma unroll
+    for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
+
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if (i < Kc) issue(i, i);
+  for (int kc = 0; kc < Kc; ++kc) {
+    const int st = kc % NS;
+    if constexpr (NS == 3) {
+      if (kc + 1 < Kc) wait_vmcnt<LPS>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    barrier_nofence();
+    if (kc + NS - 1 < Kc) issue(kc + NS - 1, (kc + NS - 1) % NS);
+    const uint8_t* wb = lds + st * STAGE;
+    const uint8_t* xs = wb + WBYTES;
+    i32x4 xf[FM];
+#pragma unroll
+    for (int b = 0; b < FM; ++b) xf[b] = *(const i32x4*)(xs + xq_off(wm * TM + b * 16 + r, g));
+#pragma unroll
+    for (int a = 0; a < FN; ++a) {
+      const i32x4 wf = tile_to_s8(*(const u32x4*)(wb + (wn * FN + a) * 1024 + lane * 16));
+#pragma unroll
+      for (int b = 0; b < FM; ++b) acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, xf[b], acc[a][b], 0, 0, 0);
+    }
+    if constexpr (NS == 2) barrier_nofence();  // stage st is overwritten by the next issue
+  }
+
+  const float sx = qpbuf[0];
+  const int corr = 128 - __float_as_int(qpbuf[1]);
+#pragma unroll
+  for (int a = 0; a < FN; ++a) {
+    const int n = (nt0 + wn * FN + a) * 16 + 4 * g;
+    if (n >= N) continue;
+    const int nvalid = min(4, N - n);
+    int cs[4];
+    f32x4 mult, bi;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int nn = min(n + v, N - 1);
+      cs[v] = colsum[nn];
+      mult[v] = sx * scale[nn];
+      bi[v] = bias ? bias[nn] : 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < FM; ++b) {
+      const int m = m0 + wm * TM + b * 16 + r;
+      if (m >= M) continue;
+      f32x4 o;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int av = acc[a][b][v] + corr * cs[v];
+        if (acc_out && v < nvalid) acc_out[(int64_t)m * N + n + v] = av;
+        o[v] = bias ? __builtin_fmaf((float)av, mult[v], bi[v]) : (float)av * mult[v];
+      }
+      store_y4(y, yt, (int64_t)m * ldy + n, o, yvec && nvalid == 4, nvalid);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 constexpr int kBN = 128, kBM = 128, kWN = 2, kWM = 2;
@@ -547,15 +564,40 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
 
 int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                      const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
-                     int64_t ldy, int32_t* acc_out, const float2* partials, int nparts, hipStream_t st, bool yvec) {
-  const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
-  dim3 grid((unsigned)((Nt + kBN / 16 - 1) / (kBN / 16)), (unsigned)((M + kBM - 1) / kBM)), block(kWN * kWM * 64);
+                     int64_t ldy, int32_t* acc_out, float2* partials, int8_t* xq, float* qpbuf, hipStream_t st,
+                     bool yvec) {
+  const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64, Kp = Kc * 64;
+  const int nparts = minmax_nparts(M, K);
+  const int prc = launch_minmax_partials(x, xt, M, K, ldx, partials, nparts, st);
+  if (prc) return prc;
   const int flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
+  const int64_t chunks = M * (Kp / 16);
+  const dim3 qgrid((unsigned)((chunks + 255) / 256));
   switch (xt) {
-    case XT_F16: hipLaunchKernelGGL((gemm_w8a8_kernel<XT_F16, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, partials, nparts, flags); break;
-    case XT_BF16: hipLaunchKernelGGL((gemm_w8a8_kernel<XT_BF16, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, partials, nparts, flags); break;
-    case XT_F32: hipLaunchKernelGGL((gemm_w8a8_kernel<XT_F32, kBN, kBM, kWN, kWM>), grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, partials, nparts, flags); break;
+    case XT_F16: hipLaunchKernelGGL(quantize_act_kernel<XT_F16>, qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp, partials, nparts, xq, qpbuf, flags); break;
+    case XT_BF16: hipLaunchKernelGGL(quantize_act_kernel<XT_BF16>, qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp, partials, nparts, xq, qpbuf, flags); break;
+    case XT_F32: hipLaunchKernelGGL(quantize_act_kernel<XT_F32>, qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp, partials, nparts, xq, qpbuf, flags); break;
     default: return -2;
+  }
+  int rc = check_launch();
+  if (rc) return rc;
+  // Tile choice (measured on MI355X, K = 4096): 256 x 128 blocks with a
+  // 3-stage ring once there are >= 2 blocks per CU, else 128 x 128, else
+  // 128 x 64 (small M: more blocks for the weight stream).
+  const int64_t Mt128 = (M + 127) / 128;
+  const int64_t t256 = ((Nt + 15) / 16) * Mt128, t128 = ((Nt + 7) / 8) * Mt128;
+  if (t256 >= 512) {
+    const dim3 grid((unsigned)((Nt + 15) / 16), (unsigned)Mt128);
+    hipLaunchKernelGGL((gemm_w8a8_dl_kernel<256, 128, 4, 2, 3>), grid, dim3(512), 0, st, xq, (int)Kp, (int)M,
+                       (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, qpbuf, flags);
+  } else if (t128 >= 256) {
+    const dim3 grid((unsigned)((Nt + 7) / 8), (unsigned)Mt128);
+    hipLaunchKernelGGL((gemm_w8a8_dl_kernel<128, 128, 2, 2, 2>), grid, dim3(256), 0, st, xq, (int)Kp, (int)M,
+                       (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, qpbuf, flags);
+  } else {
+    const dim3 grid((unsigned)((Nt + 7) / 8), (unsigned)((M + 63) / 64));
+    hipLaunchKernelGGL((gemm_w8a8_dl_kernel<128, 64, 2, 2, 2>), grid, dim3(256), 0, st, xq, (int)Kp, (int)M,
+                       (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, qpbuf, flags);
   }
   return check_launch();
 }

@@ -521,8 +521,7 @@ int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
 
 int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                      const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
-                     int64_t ldy, int32_t* acc_out, const float2* partials, int nparts, hipStream_t st,
-                     bool yvec) {
+                     int64_t ldy, int32_t* acc_out, float2* partials, hipStream_t st, bool yvec) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
   const GemvCfg c = pick_gemv(M, Nt, Kc, true, xt);
   if (!c.ok) return -1;
@@ -530,11 +529,21 @@ int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
   a.x = x; a.ldx = ldx; a.M = (int)M; a.K = (int)K; a.Kc = (int)Kc;
   a.packed = packed; a.scale = scale; a.bias = bias; a.colsum = colsum;
   a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.acc_out = acc_out;
-  a.partials = partials; a.nparts = nparts;
   a.flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
   int fid, fks;
-  if (pick_gemv_fast(M, K, N, xt, true, xvec, &fid, &fks)) {
+  const bool fast = pick_gemv_fast(M, K, N, xt, true, xvec, &fid, &fks);
+  if (fast) {  // small x: the kernel reduces the activation min/max itself
+    a.nparts = 0;
     const int rc = launch_gemv_fast_cfg(fid, fks, a, xt, true, st);
+    if (rc != -1) return rc;
+  }
+  const int np = minmax_nparts(M, K);
+  int rc = launch_minmax_partials(x, xt, M, K, ldx, partials, np, st);
+  if (rc) return rc;
+  a.partials = partials;
+  a.nparts = np;
+  if (fast) {
+    rc = launch_gemv_fast_cfg(fid, fks, a, xt, true, st);
     if (rc != -1) return rc;
   }
   switch (xt) {

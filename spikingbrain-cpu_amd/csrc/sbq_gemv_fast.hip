@@ -40,6 +40,8 @@ namespace {
 
 constexpr int kFastXLdsBytes = 32768;  // x[M][K] copied to LDS up to this size
 constexpr int kFastMaxWaves = 8;
+constexpr int kFusedChunks = 4;         // QM 2: 16-byte chunks of x per thread
+constexpr int kFusedMinWaves = 4;       // QM 2: x <= kFusedChunks * 16 * 64 * waves bytes
 
 __device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
@@ -94,8 +96,11 @@ __host__ __device__ constexpr int mm_bytes() { return kFastMaxWaves * 8; }
 
 }  // namespace
 
-template <int XT, int D, int G, bool XL, bool W8A8>
+// QM: 0 weight-only; 1 W8A8 with the activation min/max partials of the
+// pre-pass; 2 W8A8 that reduces min/max over the whole (small) x itself.
+template <int XT, int D, int G, bool XL, int QM>
 __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs a, int KW, int xch) {
+  constexpr bool W8A8 = QM != 0;
   typedef typename std::conditional<W8A8, i32x4, f32x4>::type Acc;
   constexpr int EB = x_bytes<XT>();
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -126,9 +131,20 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       if constexpr (W8A8) cs[v] = a.colsum[nn];
     }
   }
-  // W8A8: min/max partials of the activation pre-pass (duplicates are harmless)
+  // W8A8: min/max partials of the activation pre-pass, or (QM 2) up to
+  // kFusedChunks 16-byte chunks of x per thread; duplicates are harmless
   float2 part = {0.f, 0.f};
-  if constexpr (W8A8) part = a.partials[min(tid, a.nparts - 1)];
+  u32x4 xmm[QM == 2 ? kFusedChunks : 1];
+  if constexpr (QM == 1) part = a.partials[min(tid, a.nparts - 1)];
+  if constexpr (QM == 2) {
+    const int cpr = K * EB / 16, nch = M * cpr;
+#pragma unroll
+    for (int i = 0; i < kFusedChunks; ++i) {
+      const int c = min(tid + i * (int)blockDim.x, nch - 1);
+      const int m = c / cpr;
+      xmm[i] = *(const u32x4*)((const uint8_t*)a.x + (int64_t)m * a.ldx * EB + (c - m * cpr) * 16);
+    }
+  }
 
   // x copy into LDS: xch 16-byte chunks per thread, sources clamped
   const uint8_t* xg = (const uint8_t*)a.x;
@@ -159,6 +175,26 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
 
   ActQParams qp = {};
   if constexpr (XL || W8A8) {
+    if constexpr (QM == 2) {
+      float mn = 0.0f, mx = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kFusedChunks; ++i) {
+        constexpr int NE = 16 / EB;
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+          // copy the dword out first: a bit_cast of a vector-element lvalue
+          // reads element 0 with this compiler
+          const uint32_t word = xmm[i][EB == 4 ? j : j / 2];
+          float v;
+          if constexpr (XT == XT_F32) v = __uint_as_float(word);
+          else if constexpr (XT == XT_F16) v = (float)__builtin_bit_cast(f16x2, word)[j & 1];
+          else v = (float)__builtin_bit_cast(bf16x2, word)[j & 1];
+          mn = fminf(mn, v);
+          mx = fmaxf(mx, v);
+        }
+      }
+      part = make_float2(mn, mx);
+    }
     if constexpr (W8A8) {
       const float mn = wave_min(part.x), mx = wave_max(part.y);
       if (lane == 0) mmx[ks] = make_float2(mn, mx);
@@ -273,13 +309,13 @@ constexpr FastCfg kFastCfgs[] = {
 };
 constexpr int kNumFastCfgs = sizeof(kFastCfgs) / sizeof(kFastCfgs[0]);
 
-template <int XT, bool W8A8>
+template <int XT, int QM>
 int launch_fast_typed(int id, const GemvArgs& a, int ks, int KW, int xch, size_t lds, hipStream_t st) {
   const dim3 block(ks * 64);
   switch (id) {
 #define SBQ_FAST_CASE(ID, D, G, XL)                                                                         \
   case ID:                                                                                                  \
-    hipLaunchKernelGGL((gemv_fast_kernel<XT, D, G, XL, W8A8>), dim3((a.Nt + G - 1) / G), block, lds, st, a, KW, \
+    hipLaunchKernelGGL((gemv_fast_kernel<XT, D, G, XL, QM>), dim3((a.Nt + G - 1) / G), block, lds, st, a, KW, \
                        xch);                                                                                \
     return check_launch();
     SBQ_FAST_CONFIGS(SBQ_FAST_CASE)
@@ -291,7 +327,9 @@ int launch_fast_typed(int id, const GemvArgs& a, int ks, int KW, int xch, size_t
 }  // namespace
 
 // Launch of fast-path configuration `id` with `ks` waves per workgroup
-// (returns -1 when the configuration cannot run this shape).
+// (returns -1 when the configuration cannot run this shape).  W8A8 with
+// a.nparts == 0 reduces the activation min/max in the kernel (x must fit
+// kFusedChunks 16-byte chunks per thread, >= kFusedMinWaves waves).
 int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, hipStream_t st) {
   if (id < 0 || id >= kNumFastCfgs || ks < 1 || ks > kFastMaxWaves) return -1;
   const FastCfg c = kFastCfgs[id];
@@ -307,14 +345,20 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   const int T = ks * 64;
   const int xch = c.XL ? (int)((xbytes / 16 + T - 1) / T) : 0;
   const size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
-  switch (xt) {
-    case XT_F16: return w8a8 ? launch_fast_typed<XT_F16, true>(id, a, ks, KW, xch, lds, st)
-                             : launch_fast_typed<XT_F16, false>(id, a, ks, KW, xch, lds, st);
-    case XT_BF16: return w8a8 ? launch_fast_typed<XT_BF16, true>(id, a, ks, KW, xch, lds, st)
-                              : launch_fast_typed<XT_BF16, false>(id, a, ks, KW, xch, lds, st);
-    case XT_F32: return w8a8 ? launch_fast_typed<XT_F32, true>(id, a, ks, KW, xch, lds, st)
-                             : launch_fast_typed<XT_F32, false>(id, a, ks, KW, xch, lds, st);
+  const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
+  if (qm == 2 && (xbytes > (int64_t)kFusedChunks * 16 * T || ks < kFusedMinWaves)) return -1;
+#define SBQ_FAST_QM(XT_)                                                  \
+  switch (qm) {                                                           \
+    case 0: return launch_fast_typed<XT_, 0>(id, a, ks, KW, xch, lds, st); \
+    case 1: return launch_fast_typed<XT_, 1>(id, a, ks, KW, xch, lds, st); \
+    default: return launch_fast_typed<XT_, 2>(id, a, ks, KW, xch, lds, st); \
   }
+  switch (xt) {
+    case XT_F16: SBQ_FAST_QM(XT_F16)
+    case XT_BF16: SBQ_FAST_QM(XT_BF16)
+    case XT_F32: SBQ_FAST_QM(XT_F32)
+  }
+#undef SBQ_FAST_QM
   return -2;
 }
 
@@ -340,7 +384,7 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     *id = wide ? 5 : 3;  // D=8, G=2 | D=8, G=1
     *ks = 2;
   }
-  if (w8a8 && *ks * 64 < std::min<int64_t>(kMinMaxPartials, (M * K + 4095) / 4096)) *ks = 4;
+  if (w8a8 && *ks < kFusedMinWaves) *ks = kFusedMinWaves;  // 256 threads cover the min/max partials / fused x
   return true;
 }
 

@@ -179,10 +179,6 @@ __device__ __forceinline__ i32x4 quant_frag(const XRaw<XT>& x, int M, int K, int
   return (i32x4){(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
 }
 
-__device__ __forceinline__ i32x4 tile_to_s8(u32x4 w) {
-  return (i32x4){(int)(w.x ^ 0x80808080u), (int)(w.y ^ 0x80808080u), (int)(w.z ^ 0x80808080u),
-                 (int)(w.w ^ 0x80808080u)};
-}
 
 __device__ __forceinline__ u32x4 load_tile_nt(const uint8_t* p) {
   return __builtin_nontemporal_load((const u32x4*)p);

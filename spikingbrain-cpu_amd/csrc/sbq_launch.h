@@ -42,14 +42,17 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
                    const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
                    bool yvec);
 
-// W8A8 (fbgemm dynamic semantics); partials from launch_minmax_partials.
+// W8A8 (fbgemm dynamic semantics).  Both launch the activation min/max
+// pre-pass into `partials` (>= kMinMaxPartials float2) when they need it (the
+// decode fast path reduces a small x in the kernel instead).
 int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                      const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
-                     int64_t ldy, int32_t* acc_out, const float2* partials, int nparts, hipStream_t st,
-                     bool yvec);
+                     int64_t ldy, int32_t* acc_out, float2* partials, hipStream_t st, bool yvec);
+// The GEMM quantizes x once into xq (s8 [M][Kc*64]) and writes (s_x, zp) to
+// qpbuf[0..1] (zp as int bits) before the tiled pipeline reads them.
 int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                      const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
-                     int64_t ldy, int32_t* acc_out, const float2* partials, int nparts, hipStream_t st,
+                     int64_t ldy, int32_t* acc_out, float2* partials, int8_t* xq, float* qpbuf, hipStream_t st,
                      bool yvec);
 
 }  // namespace sbq

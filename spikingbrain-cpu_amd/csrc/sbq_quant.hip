@@ -87,29 +87,35 @@ __global__ __launch_bounds__(256) void colsum_kernel(const int8_t* __restrict__ 
 // Per-block (min, max) of x [M, K]; block b covers flat rows/columns
 // b, b + gridDim.x, ... in 256-element strides.
 template <int XT>
-__global__ __launch_bounds__(256) void minmax_partial_kernel(const void* __restrict__ xv, int64_t M, int64_t K,
-                                                             int64_t ldx, float2* __restrict__ partials) {
+__global__ __launch_bounds__(1024) void minmax_partial_kernel(const void* __restrict__ xv, int M, int K, int64_t ldx,
+                                                              float2* __restrict__ partials, int vec) {
   typedef typename XElem<XT>::T T;
-  const T* x = (const T*)xv;
-  float mn = 0.0f, mx = 0.0f;
-  const int64_t total = M * K;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int64_t m = i / K, k = i - m * K;
-    const float v = XElem<XT>::to_f32(x[m * ldx + k]);
-    mn = fminf(mn, v);
-    mx = fmaxf(mx, v);
+  // 8-element chunks, row by row; block b covers chunks b, b + nparts, ...
+  const int cpr = (K + 7) / 8;
+  const int64_t nch = (int64_t)M * cpr;
+  float mn = 0.0f, mx = 0.0f;  // lo <= 0 <= hi after clamping anyway
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < nch; c += (int64_t)gridDim.x * blockDim.x) {
+    const int m = (int)(c / cpr), k0 = (int)(c - (int64_t)m * cpr) * 8;
+    float t[8];
+    load8_f32<XT>(xv, ldx, M, K, m, k0, vec, t);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = k0 + j < K ? t[j] : 0.0f;
+      mn = fminf(mn, v);
+      mx = fmaxf(mx, v);
+    }
   }
-  __shared__ float red[8];
+  __shared__ float red[32];
   mn = wave_min(mn);
   mx = wave_max(mx);
-  const int wid = threadIdx.x >> 6;
+  const int wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     red[2 * wid] = mn;
     red[2 * wid + 1] = mx;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; ++w) {
+    for (int w = 1; w < nw; ++w) {
       mn = fminf(mn, red[2 * w]);
       mx = fmaxf(mx, red[2 * w + 1]);
     }
@@ -172,11 +178,13 @@ int minmax_nparts(int64_t M, int64_t K) {
 
 int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, float2* partials,
                            int nparts, hipStream_t st) {
-  dim3 grid((unsigned)nparts), block(256);
+  const int esz = xt == XT_F32 ? 4 : 2;
+  const int vec = ((uintptr_t)x % 16 == 0) && ((ldx * esz) % 16 == 0);
+  dim3 grid((unsigned)nparts), block(1024);
   switch (xt) {
-    case XT_F32: hipLaunchKernelGGL(minmax_partial_kernel<XT_F32>, grid, block, 0, st, x, M, K, ldx, partials); break;
-    case XT_F16: hipLaunchKernelGGL(minmax_partial_kernel<XT_F16>, grid, block, 0, st, x, M, K, ldx, partials); break;
-    case XT_BF16: hipLaunchKernelGGL(minmax_partial_kernel<XT_BF16>, grid, block, 0, st, x, M, K, ldx, partials); break;
+    case XT_F32: hipLaunchKernelGGL(minmax_partial_kernel<XT_F32>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec); break;
+    case XT_F16: hipLaunchKernelGGL(minmax_partial_kernel<XT_F16>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec); break;
+    case XT_BF16: hipLaunchKernelGGL(minmax_partial_kernel<XT_BF16>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec); break;
     default: return -2;
   }
   return check_launch();
