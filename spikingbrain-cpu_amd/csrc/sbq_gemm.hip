@@ -17,6 +17,8 @@
 //           v_mfma_i32_16x16x64_i8 accumulates exactly; the epilogue adds
 //           (128 - zp) * colsum[n] and applies fp32(s_x * scale[n]) (+ bias[n]
 //           fused), as fbgemm does.
+#include <type_traits>
+
 #include "sbq_common.h"
 #include "sbq_launch.h"
 
@@ -257,6 +259,20 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
+// Wait until only the `younger` most recent stages (LPS DMA instructions each)
+// of this wave are still in flight.
+template <int LPS, int NS>
+__device__ __forceinline__ void wait_stages(int younger) {
+  static_assert(LPS * (NS - 2) < 64, "vmcnt range");
+  if constexpr (NS > 7) { if (younger >= 6) { wait_vmcnt<(NS > 7 ? 6 * LPS : 0)>(); return; } }
+  if constexpr (NS > 6) { if (younger == 5) { wait_vmcnt<(NS > 6 ? 5 * LPS : 0)>(); return; } }
+  if constexpr (NS > 5) { if (younger == 4) { wait_vmcnt<(NS > 5 ? 4 * LPS : 0)>(); return; } }
+  if constexpr (NS > 4) { if (younger == 3) { wait_vmcnt<(NS > 4 ? 3 * LPS : 0)>(); return; } }
+  if constexpr (NS > 3) { if (younger == 2) { wait_vmcnt<(NS > 3 ? 2 * LPS : 0)>(); return; } }
+  if constexpr (NS > 2) { if (younger == 1) { wait_vmcnt<(NS > 2 ? LPS : 0)>(); return; } }
+  wait_vmcnt<0>();
+}
+
 // Workgroup barrier without the release/acquire fence of __syncthreads():
 // the fence would wait for every outstanding load, including the LDS DMA of
 // the stages still in flight.  Each wave waits for its own DMA of the stage it
@@ -270,103 +286,173 @@ __device__ __forceinline__ void barrier_nofence() {
 
 __device__ __forceinline__ int xsw_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
-template <int XT, int BN, int BM, int WN, int WM, int NS>
-__global__ __launch_bounds__(WN* WM * 64) void gemm_w8_dl_kernel(const void* __restrict__ x, int64_t ldx, int M,
-                                                                 int Kc, const uint8_t* __restrict__ packed,
-                                                                 const float* __restrict__ scale,
-                                                                 const float* __restrict__ bias, int N, int Nt,
-                                                                 void* __restrict__ y, int yt, int64_t ldy,
-                                                                 int flags) {
+// Arguments of the direct-to-LDS GEMM (one struct, passed by value).
+struct GemmArgs {
+  const void* x;  // W-only: fp16/bf16 activations; I8: s8 quantized activations
+  int64_t ldx;    // row stride: elements (W-only) or bytes (I8)
+  int M, Kc;
+  const uint8_t* packed;
+  const float* scale;
+  const float* bias;
+  const int32_t* colsum;  // I8 only
+  int N, Nt;
+  void* y;
+  int yt;
+  int64_t ldy;
+  int32_t* acc_out;     // I8 only, may be null
+  const float* qpbuf;   // I8 only: (s_x, zp as int bits)
+  int flags;            // bit 1: y rows 4-element vector stores
+};
+
+// KG groups of WN x WM waves: group kg streams the K tiles
+// [kg*KW, kg*KW + KW), KW = ceil(Kc/KG), through its own NS-stage ring; the
+// groups step in lockstep (one barrier per stage) and their partial tiles are
+// summed through LDS in group order at the end.  Splitting K inside the
+// workgroup multiplies the waves per SIMD (latency hiding) for grids too small
+// to fill the chip, without extra HBM traffic.
+template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG>
+__global__ __launch_bounds__(KG* WN* WM * 64, 4) void gemm_dl_kernel(const GemmArgs a) {
   typedef GemmOp<XT> Op;
   typedef typename Op::V V;
-  constexpr int NWAVES = WN * WM;
+  typedef typename std::conditional<I8, i32x4, f32x4>::type Acc;
+  constexpr int GW = WN * WM;
   constexpr int TN = BN / WN, TM = BM / WM, FN = TN / 16, FM = TM / 16;
-  constexpr int WT = BN / 16;          // weight tiles per stage
-  constexpr int XR = BM * 128 / 1024;  // 1 KiB activation chunks (8 rows) per stage
-  constexpr int WBYTES = WT * 1024, STAGE = WBYTES + BM * 128;
-  constexpr int LPS = (WT + XR) / NWAVES;  // DMA instructions per wave per stage
-  static_assert(WT % NWAVES == 0 && XR % NWAVES == 0, "even DMA split");
-  static_assert(NS == 2 || NS == 3, "stages");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE];
+  constexpr int XB = I8 ? 64 : 128;     // bytes of one activation row per stage
+  constexpr int WT = BN / 16;           // weight tiles per stage
+  constexpr int XR = BM * XB / 1024;    // 1 KiB activation chunks per stage
+  constexpr int WBYTES = WT * 1024, STAGE = WBYTES + BM * XB;
+  constexpr int LPS = (WT + XR) / GW;   // DMA instructions per wave per stage
+  constexpr int RED = (KG - 1) * GW * FN * FM * 1024;
+  constexpr int LDSB = KG * NS * STAGE > RED ? KG * NS * STAGE : RED;
+  static_assert(WT % GW == 0 && XR % GW == 0, "even DMA split");
+  static_assert(NS >= 2 && NS <= 8, "stages");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDSB];
 
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r = lane & 15, g = lane >> 4;
-  const int wn = wave / WM, wm = wave % WM;
-  const int nt0 = blockIdx.x * WT;
-  const int m0 = blockIdx.y * BM;
-  const bool yvec = flags & 2;
-  const uint8_t* xb = (const uint8_t*)x;
+  const int kg = wave / GW, w = wave % GW;
+  const int wn = w / WM, wm = w % WM;
+  const int nt0 = blockIdx.x * WT, m0 = blockIdx.y * BM;
+  const int M = a.M, Kc = a.Kc, Nt = a.Nt;
+  const int KW = (Kc + KG - 1) / KG;
+  const int kbeg = kg * KW;
+  const int cnt = min(KW, Kc - kbeg);  // tiles of this group (<= 0: none)
+  const uint8_t* xg = (const uint8_t*)a.x;
+  const int64_t xrow = I8 ? a.ldx : a.ldx * 2;  // bytes per activation row
 
-  auto issue = [&](int kc, int st) {
-    uint8_t* base = lds + st * STAGE;
+  auto issue = [&](int i, int st) {
+    // clamped: the surplus stages of a short last group are never multiplied
+    const int kc = KG == 1 ? i : max(0, min(kbeg + min(i, cnt - 1), Kc - 1));
+    uint8_t* base = lds + (kg * NS + st) * STAGE;
 #pragma unroll
-    for (int i = 0; i < WT / NWAVES; ++i) {
-      const int j = wave * (WT / NWAVES) + i;
+    for (int i2 = 0; i2 < WT / GW; ++i2) {
+      const int j = w * (WT / GW) + i2;
       const int nt = min(nt0 + j, Nt - 1);
-      lds_dma16(packed + ((int64_t)nt * Kc + kc) * 1024 + lane * 16, base + j * 1024);
+      lds_dma16(a.packed + ((int64_t)nt * Kc + kc) * 1024 + lane * 16, base + j * 1024);
     }
 #pragma unroll
-    for (int i = 0; i < XR / NWAVES; ++i) {
-      const int j = wave * (XR / NWAVES) + i;
-      const int row = j * 8 + (lane >> 3);
-      const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-      const int m = min(m0 + row, M - 1);
-      lds_dma16(xb + ((int64_t)m * ldx + kc * 64 + chunk * 8) * 2, base + WBYTES + j * 1024);
+    for (int i2 = 0; i2 < XR / GW; ++i2) {
+      const int j = w * (XR / GW) + i2;
+      if constexpr (I8) {
+        const int row = j * 16 + (lane >> 2);
+        const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+        const int m = min(m0 + row, M - 1);
+        lds_dma16(xg + (int64_t)m * xrow + kc * 64 + chunk * 16, base + WBYTES + j * 1024);
+      } else {
+        const int row = j * 8 + (lane >> 3);
+        const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+        const int m = min(m0 + row, M - 1);
+        lds_dma16(xg + (int64_t)m * xrow + (kc * 64 + chunk * 8) * 2, base + WBYTES + j * 1024);
+      }
     }
   };
 
-  f32x4 acc[FN][FM];
+  Acc acc[FN][FM];
 #pragma unroll
-  for (int a = 0; a < FN; ++a)
+  for (int i = 0; i < FN; ++i)
 #pragma unroll
-    for (int b = 0; b < FM; ++b) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < FM; ++b) acc[i][b] = Acc{0, 0, 0, 0};
 
 #pragma unroll
   for (int i = 0; i < NS - 1; ++i)
-    if (i < Kc) issue(i, i);
-  for (int kc = 0; kc < Kc; ++kc) {
-    const int st = kc % NS;
-    // this wave's DMA of stage kc is complete once at most the younger
-    // in-flight stages (NS - 2 of them, fewer at the end) remain outstanding
-    if constexpr (NS == 3) {
-      if (kc + 1 < Kc) wait_vmcnt<LPS>();
-      else wait_vmcnt<0>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    if (i < KW) issue(i, i);
+  for (int i = 0; i < KW; ++i) {
+    // stage i has landed once only the younger in-flight stages remain
+    wait_stages<LPS, NS>(min(NS - 2, KW - 1 - i));
     barrier_nofence();
-    if (kc + NS - 1 < Kc) issue(kc + NS - 1, (kc + NS - 1) % NS);
-    const uint8_t* wb = lds + st * STAGE;
-    const uint8_t* xs = wb + WBYTES;
+    if (i + NS - 1 < KW) issue(i + NS - 1, (i + NS - 1) % NS);
+    if (KG == 1 || i < cnt) {
+      const uint8_t* wb = lds + (kg * NS + i % NS) * STAGE;
+      const uint8_t* xs = wb + WBYTES;
+      if constexpr (I8) {
+        i32x4 xf[FM];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      V xf[FM];
+        for (int b = 0; b < FM; ++b) xf[b] = *(const i32x4*)(xs + xq_off(wm * TM + b * 16 + r, g));
 #pragma unroll
-      for (int b = 0; b < FM; ++b) xf[b] = *(const V*)(xs + xsw_off(wm * TM + b * 16 + r, 2 * g + s));
+        for (int t = 0; t < FN; ++t) {
+          const i32x4 wf = tile_to_s8(*(const u32x4*)(wb + (wn * FN + t) * 1024 + lane * 16));
 #pragma unroll
-      for (int a = 0; a < FN; ++a) {
-        const u32x2 raw = *(const u32x2*)(wb + (wn * FN + a) * 1024 + lane * 16 + s * 8);
-        V wf0, wf1;
-        Op::wconv((u32x4){raw.x, raw.y, 0u, 0u}, wf0, wf1);
+          for (int b = 0; b < FM; ++b) acc[t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, xf[b], acc[t][b], 0, 0, 0);
+        }
+      } else {
 #pragma unroll
-        for (int b = 0; b < FM; ++b) acc[a][b] = Op::mma(wf0, xf[b], acc[a][b]);
+        for (int s2 = 0; s2 < 2; ++s2) {
+          V xf[FM];
+#pragma unroll
+          for (int b = 0; b < FM; ++b) xf[b] = *(const V*)(xs + xsw_off(wm * TM + b * 16 + r, 2 * g + s2));
+#pragma unroll
+          for (int t = 0; t < FN; ++t) {
+            const u32x2 raw = *(const u32x2*)(wb + (wn * FN + t) * 1024 + lane * 16 + s2 * 8);
+            V wf0, wf1;
+            Op::wconv((u32x4){raw.x, raw.y, 0u, 0u}, wf0, wf1);
+#pragma unroll
+            for (int b = 0; b < FM; ++b) acc[t][b] = Op::mma(wf0, xf[b], acc[t][b]);
+          }
+        }
       }
     }
-    if constexpr (NS == 2) barrier_nofence();  // stage st is overwritten by the next issue
+    if constexpr (NS == 2) barrier_nofence();  // stage i % 2 is overwritten by the next issue
   }
 
+  if constexpr (KG > 1) {
+    if constexpr (NS > 2) barrier_nofence();  // every group is done with its stages
+    Acc* red = (Acc*)lds;
+    if (kg > 0) {
 #pragma unroll
-  for (int a = 0; a < FN; ++a) {
-    const int n = (nt0 + wn * FN + a) * 16 + 4 * g;
-    if (n >= N) continue;
-    const int nvalid = min(4, N - n);
+      for (int t = 0; t < FN; ++t)
+#pragma unroll
+        for (int b = 0; b < FM; ++b) red[(((kg - 1) * GW + w) * FN * FM + t * FM + b) * 64 + lane] = acc[t][b];
+    }
+    __syncthreads();  // no DMA is in flight any more: the fence costs nothing here
+    if (kg > 0) return;
+#pragma unroll 1
+    for (int k = 1; k < KG; ++k)
+#pragma unroll
+      for (int t = 0; t < FN; ++t)
+#pragma unroll
+        for (int b = 0; b < FM; ++b) acc[t][b] += red[(((k - 1) * GW + w) * FN * FM + t * FM + b) * 64 + lane];
+  }
+
+  const bool yvec = a.flags & 2;
+  float sx = 0.0f;
+  int corr = 0;
+  if constexpr (I8) {
+    sx = a.qpbuf[0];
+    corr = 128 - __float_as_int(a.qpbuf[1]);
+  }
+#pragma unroll
+  for (int t = 0; t < FN; ++t) {
+    const int n = (nt0 + wn * FN + t) * 16 + 4 * g;
+    if (n >= a.N) continue;
+    const int nvalid = min(4, a.N - n);
     f32x4 sc, bi;
+    int cs[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int nn = min(n + v, N - 1);
-      sc[v] = scale[nn];
-      bi[v] = bias ? bias[nn] : 0.0f;
+      const int nn = min(n + v, a.N - 1);
+      sc[v] = I8 ? sx * a.scale[nn] : a.scale[nn];
+      bi[v] = a.bias ? a.bias[nn] : 0.0f;
+      cs[v] = I8 ? a.colsum[nn] : 0;
     }
 #pragma unroll
     for (int b = 0; b < FM; ++b) {
@@ -375,13 +461,26 @@ __global__ __launch_bounds__(WN* WM * 64) void gemm_w8_dl_kernel(const void* __r
       f32x4 o;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        float out = acc[a][b][v] * sc[v];
-        if (bias) out = out + bi[v];
-        o[v] = out;
+        if constexpr (I8) {
+          const int av = acc[t][b][v] + corr * cs[v];
+          if (a.acc_out && v < nvalid) a.acc_out[(int64_t)m * a.N + n + v] = av;
+          o[v] = a.bias ? __builtin_fmaf((float)av, sc[v], bi[v]) : (float)av * sc[v];
+        } else {
+          float out = acc[t][b][v] * sc[v];
+          if (a.bias) out = out + bi[v];
+          o[v] = out;
+        }
       }
-      store_y4(y, yt, (int64_t)m * ldy + n, o, yvec && nvalid == 4, nvalid);
+      store_y4(a.y, a.yt, (int64_t)m * a.ldy + n, o, yvec && nvalid == 4, nvalid);
     }
   }
+}
+
+template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG>
+int launch_dl(const GemmArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)((a.Nt + BN / 16 - 1) / (BN / 16)), (unsigned)((a.M + BM - 1) / BM));
+  hipLaunchKernelGGL((gemm_dl_kernel<I8, XT, BN, BM, WN, WM, NS, KG>), grid, dim3(KG * WN * WM * 64), 0, st, a);
+  return check_launch();
 }
 
 // ---------------------------------------------------------------------------
@@ -423,115 +522,56 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restric
   *(u32x4*)(xq + (int64_t)m * Kp + k0) = (u32x4){d[0], d[1], d[2], d[3]};
 }
 
-// Block tile BN output channels x BM tokens x 64 K, WN x WM waves, NS LDS
-// stages of BN/16 packed weight tiles + BM s8 activation rows (64 bytes,
-// 16-byte chunks XOR-swizzled by (row >> 2) & 3 on the source side, so that
-// the 16 rows one ds_read_b128 quarter-wave reads cover all 64 banks).
-template <int BN, int BM, int WN, int WM, int NS>
-__global__ __launch_bounds__(WN* WM * 64) void gemm_w8a8_dl_kernel(
-    const int8_t* __restrict__ xq, int Kp, int M, int Kc, const uint8_t* __restrict__ packed,
-    const float* __restrict__ scale, const int32_t* __restrict__ colsum, const float* __restrict__ bias, int N,
-    int Nt, void* __restrict__ y, int yt, int64_t ldy, int32_t* __restrict__ acc_out, const float* __restrict__ qpbuf,
-    int flags) {
-  constexpr int NWAVES = WN * WM;
-  constexpr int TN = BN / WN, TM = BM / WM, FN = TN / 16, FM = TM / 16;
-  constexpr int WT = BN / 16;          // weight tiles per stage
-  constexpr int XR = BM * 64 / 1024;   // 1 KiB activation chunks (16 rows) per stage
-  constexpr int WBYTES = WT * 1024, STAGE = WBYTES + BM * 64;
-  constexpr int LPS = (WT + XR) / NWAVES;
-  static_assert(WT % NWAVES == 0 && XR % NWAVES == 0, "even DMA split");
-  static_assert(NS == 2 || NS == 3, "stages");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE];
 
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int r = lane & 15, g = lane >> 4;
-  const int wn = wave / WM, wm = wave % WM;
-  const int nt0 = blockIdx.x * WT;
-  const int m0 = blockIdx.y * BM;
-  const bool yvec = flags & 2;
+// Direct-to-LDS configurations (BN, BM, WN, WM, NS, KG), indexed by id.
+#define SBQ_DL_CONFIGS(X) \
+  X(0, 256, 128, 4, 2, 2, 1) \
+  X(1, 256, 128, 4, 2, 3, 1) \
+  X(2, 128, 128, 2, 2, 2, 1) \
+  X(3, 128, 64, 2, 2, 2, 1)  \
+  X(4, 128, 64, 2, 2, 2, 2)  \
+  X(5, 128, 64, 2, 2, 2, 4)  \
+  X(6, 128, 128, 2, 2, 2, 2) \
+  X(7, 256, 128, 4, 2, 2, 2) \
+  X(8, 64, 64, 1, 2, 2, 4)   \
+  X(9, 128, 64, 2, 2, 3, 2)
 
-  auto issue = [&](int kc, int st) {
-    uint8_t* base = lds + st * STAGE;
-#pragma unroll
-    for (int i = 0; i < WT / NWAVES; ++i) {
-      const int j = wave * (WT / NWAVES) + i;
-      const int nt = min(nt0 + j, Nt - 1);
-      lds_dma16(packed + ((int64_t)nt * Kc + kc) * 1024 + lane * 16, base + j * 1024);
-    }
-#pragma unroll
-    for (int i = 0; i < XR / NWAVES; ++i) {
-      const int j = wave * (XR / NWAVES) + i;
-      const int row = j * 16 + (lane >> 2);
-      const int chunk = (lane & 3) ^ ((row >> 2) & 3);
-      const int m = min(m0 + row, M - 1);
-      lds_dma16(xq + (int64_t)m * Kp + kc * 64 + chunk * 16, base + WBYTES + j * 1024);
-    }
-  };
-
-  i32x4 acc[FN][FM];
-#pragma unroll
-  for (int a = 0; a < FN; ++a)
-#pragma unroll
-    for (int b = 0; b < FM; ++b) acc[a][b] = (i32x4){0, 0, 0, 0};
-
-#pragma unroll
-  for (int i = 0; i < NS - 1; ++i)
-    if (i < Kc) issue(i, i);
-  for (int kc = 0; kc < Kc; ++kc) {
-    const int st = kc % NS;
-    if constexpr (NS == 3) {
-      if (kc + 1 < Kc) wait_vmcnt<LPS>();
-      else wait_vmcnt<0>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    barrier_nofence();
-    if (kc + NS - 1 < Kc) issue(kc + NS - 1, (kc + NS - 1) % NS);
-    const uint8_t* wb = lds + st * STAGE;
-    const uint8_t* xs = wb + WBYTES;
-    i32x4 xf[FM];
-#pragma unroll
-    for (int b = 0; b < FM; ++b) xf[b] = *(const i32x4*)(xs + xq_off(wm * TM + b * 16 + r, g));
-#pragma unroll
-    for (int a = 0; a < FN; ++a) {
-      const i32x4 wf = tile_to_s8(*(const u32x4*)(wb + (wn * FN + a) * 1024 + lane * 16));
-#pragma unroll
-      for (int b = 0; b < FM; ++b) acc[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, xf[b], acc[a][b], 0, 0, 0);
-    }
-    if constexpr (NS == 2) barrier_nofence();  // stage st is overwritten by the next issue
+template <bool I8, int XT>
+int launch_dl_id(int id, const GemmArgs& a, hipStream_t st) {
+  switch (id) {
+#define SBQ_DL_CASE(ID, BN, BM, WN, WM, NS, KG) \
+  case ID: return launch_dl<I8, XT, BN, BM, WN, WM, NS, KG>(a, st);
+    SBQ_DL_CONFIGS(SBQ_DL_CASE)
+#undef SBQ_DL_CASE
   }
+  return -1;
+}
 
-  const float sx = qpbuf[0];
-  const int corr = 128 - __float_as_int(qpbuf[1]);
-#pragma unroll
-  for (int a = 0; a < FN; ++a) {
-    const int n = (nt0 + wn * FN + a) * 16 + 4 * g;
-    if (n >= N) continue;
-    const int nvalid = min(4, N - n);
-    int cs[4];
-    f32x4 mult, bi;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int nn = min(n + v, N - 1);
-      cs[v] = colsum[nn];
-      mult[v] = sx * scale[nn];
-      bi[v] = bias ? bias[nn] : 0.0f;
-    }
-#pragma unroll
-    for (int b = 0; b < FM; ++b) {
-      const int m = m0 + wm * TM + b * 16 + r;
-      if (m >= M) continue;
-      f32x4 o;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int av = acc[a][b][v] + corr * cs[v];
-        if (acc_out && v < nvalid) acc_out[(int64_t)m * N + n + v] = av;
-        o[v] = bias ? __builtin_fmaf((float)av, mult[v], bi[v]) : (float)av * mult[v];
-      }
-      store_y4(y, yt, (int64_t)m * ldy + n, o, yvec && nvalid == 4, nvalid);
-    }
+// Launch of direct-to-LDS configuration `id` (tuning entry; -1: no such id).
+int launch_gemm_dl_cfg(int id, bool i8, int xt, const GemmArgs& a, hipStream_t st) {
+  if (i8) return launch_dl_id<true, XT_F16>(id, a, st);
+  if (xt == XT_F16) return launch_dl_id<false, XT_F16>(id, a, st);
+  if (xt == XT_BF16) return launch_dl_id<false, XT_BF16>(id, a, st);
+  return -2;
+}
+
+// Configuration for a shape (measured on MI355X, K = 4096, M 128..8192,
+// N 1024..12288): big grids take 256 x 128 blocks (W8A8 also 128 x 128 for
+// mid-size grids); grids that leave CUs short of waves take 128 x 64 or
+// 64 x 64 blocks with K split over 4 wave groups inside the workgroup.
+int pick_gemm_dl(bool i8, int64_t M, int64_t Nt) {
+  const int64_t t256 = ((Nt + 15) / 16) * ((M + 127) / 128);
+  const int64_t t128 = ((Nt + 7) / 8) * ((M + 127) / 128);
+  const int64_t t128x64 = ((Nt + 7) / 8) * ((M + 63) / 64);
+  if (i8) {
+    if (t256 >= 512) return 0;
+    if (t128 >= 256) return 2;
+    if (t128x64 >= 256) return 5;
+    return 8;
   }
+  if (t256 >= 256 || t128x64 >= 512) return 0;
+  if (t128x64 >= 128) return 5;
+  return 8;
 }
 
 // ---------------------------------------------------------------------------
@@ -545,12 +585,11 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
   const int flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
   if (xvec && K % 64 == 0 && xt != XT_F32) {
-    dim3 g2((unsigned)((Nt + 15) / 16), (unsigned)((M + 127) / 128));
-    if (xt == XT_F16)
-      hipLaunchKernelGGL((gemm_w8_dl_kernel<XT_F16, 256, 128, 4, 2, 2>), g2, dim3(512), 0, st, x, ldx, (int)M, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, flags);
-    else
-      hipLaunchKernelGGL((gemm_w8_dl_kernel<XT_BF16, 256, 128, 4, 2, 2>), g2, dim3(512), 0, st, x, ldx, (int)M, (int)Kc, packed, scale, bias, (int)N, (int)Nt, y, yt, ldy, flags);
-    return check_launch();
+    GemmArgs a{};
+    a.x = x; a.ldx = ldx; a.M = (int)M; a.Kc = (int)Kc;
+    a.packed = packed; a.scale = scale; a.bias = bias;
+    a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.flags = flags;
+    return launch_gemm_dl_cfg(pick_gemm_dl(false, M, Nt), false, xt, a, st);
   }
   dim3 grid((unsigned)((Nt + kBN / 16 - 1) / (kBN / 16)), (unsigned)((M + kBM - 1) / kBM)), block(kWN * kWM * 64);
   switch (xt) {
@@ -581,25 +620,12 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
   }
   int rc = check_launch();
   if (rc) return rc;
-  // Tile choice (measured on MI355X, K = 4096): 256 x 128 blocks with a
-  // 3-stage ring once there are >= 2 blocks per CU, else 128 x 128, else
-  // 128 x 64 (small M: more blocks for the weight stream).
-  const int64_t Mt128 = (M + 127) / 128;
-  const int64_t t256 = ((Nt + 15) / 16) * Mt128, t128 = ((Nt + 7) / 8) * Mt128;
-  if (t256 >= 512) {
-    const dim3 grid((unsigned)((Nt + 15) / 16), (unsigned)Mt128);
-    hipLaunchKernelGGL((gemm_w8a8_dl_kernel<256, 128, 4, 2, 3>), grid, dim3(512), 0, st, xq, (int)Kp, (int)M,
-                       (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, qpbuf, flags);
-  } else if (t128 >= 256) {
-    const dim3 grid((unsigned)((Nt + 7) / 8), (unsigned)Mt128);
-    hipLaunchKernelGGL((gemm_w8a8_dl_kernel<128, 128, 2, 2, 2>), grid, dim3(256), 0, st, xq, (int)Kp, (int)M,
-                       (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, qpbuf, flags);
-  } else {
-    const dim3 grid((unsigned)((Nt + 7) / 8), (unsigned)((M + 63) / 64));
-    hipLaunchKernelGGL((gemm_w8a8_dl_kernel<128, 64, 2, 2, 2>), grid, dim3(256), 0, st, xq, (int)Kp, (int)M,
-                       (int)Kc, packed, scale, colsum, bias, (int)N, (int)Nt, y, yt, ldy, acc_out, qpbuf, flags);
-  }
-  return check_launch();
+  GemmArgs a{};
+  a.x = xq; a.ldx = Kp; a.M = (int)M; a.Kc = (int)Kc;
+  a.packed = packed; a.scale = scale; a.bias = bias; a.colsum = colsum;
+  a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.acc_out = acc_out; a.qpbuf = qpbuf;
+  a.flags = flags;
+  return launch_gemm_dl_cfg(pick_gemm_dl(true, M, Nt), true, XT_F16, a, st);
 }
 
 }  // namespace sbq
