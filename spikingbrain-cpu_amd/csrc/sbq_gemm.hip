@@ -310,8 +310,13 @@ struct GemmArgs {
 // summed through LDS in group order at the end.  Splitting K inside the
 // workgroup multiplies the waves per SIMD (latency hiding) for grids too small
 // to fill the chip, without extra HBM traffic.
+// Occupancy hint: 4 waves per SIMD (128 VGPRs) unless a wave's accumulator
+// tile exceeds 64 x 64 (then 2 waves per SIMD, 256 VGPRs).
+template <int BN, int BM, int WN, int WM>
+constexpr int dl_min_waves() { return (BN / WN) * (BM / WM) > 64 * 64 ? 2 : 4; }
+
 template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG>
-__global__ __launch_bounds__(KG* WN* WM * 64, 4) void gemm_dl_kernel(const GemmArgs a) {
+__global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) void gemm_dl_kernel(const GemmArgs a) {
   typedef GemmOp<XT> Op;
   typedef typename Op::V V;
   typedef typename std::conditional<I8, i32x4, f32x4>::type Acc;
@@ -534,7 +539,10 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restric
   X(6, 128, 128, 2, 2, 2, 2) \
   X(7, 256, 128, 4, 2, 2, 2) \
   X(8, 64, 64, 1, 2, 2, 4)   \
-  X(9, 128, 64, 2, 2, 3, 2)
+  X(9, 128, 64, 2, 2, 3, 2)  \
+  X(10, 256, 128, 4, 1, 2, 1) \
+  X(11, 128, 256, 2, 2, 2, 1) \
+  X(12, 256, 256, 4, 2, 2, 1)
 
 template <bool I8, int XT>
 int launch_dl_id(int id, const GemmArgs& a, hipStream_t st) {
@@ -569,6 +577,7 @@ int pick_gemm_dl(bool i8, int64_t M, int64_t Nt) {
     if (t128x64 >= 256) return 5;
     return 8;
   }
+  if (t256 >= 1536) return 10;  // 64 x 128 wave tiles: half the conversion work per MFMA
   if (t256 >= 256 || t128x64 >= 512) return 0;
   if (t128x64 >= 128) return 5;
   return 8;
