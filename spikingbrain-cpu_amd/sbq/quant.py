@@ -209,6 +209,11 @@ class Int8Linear(nn.Module):
         packed, _ = repack(q, with_colsum=False)
         self.register_buffer("packed", packed, persistent=False)
         self.out_dtype = torch.float32
+        # a loaded state_dict replaces qweight in place: rebuild the tiles from it
+        self.register_load_state_dict_post_hook(lambda module, incompatible: module._repack())
+
+    def _repack(self):
+        self.packed = repack(self.qweight.contiguous(), with_colsum=False)[0]
 
     @property
     def in_features(self) -> int:
@@ -221,7 +226,7 @@ class Int8Linear(nn.Module):
     def _refresh(self):
         # packed follows qweight across .to()/.cuda(); rebuild if it was lost
         if self.packed.device != self.qweight.device or self.packed.numel() == 0:
-            self.packed = repack(self.qweight, with_colsum=False)[0]
+            self._repack()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not self.qweight.is_cuda:

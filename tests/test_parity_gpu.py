@@ -282,7 +282,8 @@ def test_w8a8_bias_fused(dev):
 # ---------------------------------------------------------------------------
 # full-size shapes (sampled rows)
 # ---------------------------------------------------------------------------
-FULL_W8 = [(1, 4096, 4096), (1, 6144, 4096), (4, 24576, 4096), (16, 4096, 12288), (2048, 12288, 4096)]
+FULL_W8 = [(1, 4096, 4096), (1, 6144, 4096), (4, 24576, 4096), (16, 4096, 12288), (2048, 12288, 4096),
+           (2048, 24576, 4096), (512, 4096, 4096)]
 
 
 @pytest.mark.parametrize("M,N,K", FULL_W8)
@@ -316,3 +317,76 @@ def test_w8a8_full_size_sampled(dev, M, N):
     acc_ref = ((xq.astype(np.int64) - zp) @ q.astype(np.int64).T).astype(np.int32)
     np.testing.assert_array_equal(acc.cpu().numpy()[rows], acc_ref)
     np.testing.assert_array_equal(y.cpu().numpy()[rows], oracle.dyn_epilogue(acc_ref, sx, s))
+
+
+# ---------------------------------------------------------------------------
+# the reference module API as the loader and the model use it
+# ---------------------------------------------------------------------------
+def test_int8_state_dict_roundtrip(dev):
+    """quant.py:36-38: the state_dict holds qweight / scale (/ bias); loading
+    one into another module must make it compute with the loaded weights."""
+    announce("state_dict roundtrip")
+    N, K = 96, 512
+    w1, w2 = make_weights(N, K, 31), make_weights(N, K, 32)
+    b = torch.randn(N)
+    lin1, lin2 = quant.Int8Linear(w1, b), quant.Int8Linear(w2, torch.zeros(N))
+    sd = lin1.state_dict()
+    assert set(sd) == {"qweight", "scale", "bias"}
+    assert sd["qweight"].dtype == torch.int8 and sd["scale"].dtype == torch.float32
+    assert set(quant.Int8Linear(w1, None).state_dict()) == {"qweight", "scale"}
+    lin2.load_state_dict(sd)
+    x = make_x(3, K, 33)
+    np.testing.assert_array_equal(lin2(x.to(dev)).cpu().numpy(), lin1(x.to(dev)).cpu().numpy())
+
+
+def test_cpu_tensors_in_and_out(dev):
+    """The reference model feeds CPU fp32 [T, B, K] tensors and views the
+    fp32 contiguous result (model.py:262-264): same contract here."""
+    announce("cpu in / cpu out")
+    N, K = 64, 256
+    w = make_weights(N, K, 41)
+    x = make_x(6, K, 42).reshape(2, 3, K)
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref = oracle.int8_linear(x.reshape(-1, K).numpy(), q, s).reshape(2, 3, N)
+    for fmt in ("int8", "int8-dyn"):
+        y = quant.make_linear(fmt, w, None)(x)
+        assert y.device.type == "cpu" and y.dtype == torch.float32 and y.shape == (2, 3, N) and y.is_contiguous()
+        tol = 1e-5 if fmt == "int8" else 2e-2  # int8-dyn quantizes the activations too
+        assert oracle.rel_l2(y.numpy(), ref) <= tol, fmt
+
+
+@pytest.mark.parametrize("fmt", list(quant.FORMATS))
+def test_make_linear_every_format(dev, fmt):
+    announce(f"make_linear {fmt}")
+    N, K = 48, 320
+    w = make_weights(N, K, 51)
+    b = torch.randn(N)
+    x = make_x(5, K, 52)
+    ref = x.double() @ w.double().t() + b.double()
+    y = quant.make_linear(fmt, w, b)(x.to(dev))
+    assert y.dtype == torch.float32 and y.shape == (5, N)
+    tol = {"float32": 1e-6, "bfloat16": 2e-2, "float16": 2e-3, "int8": 2e-2, "int8-dyn": 3e-2}[fmt]
+    assert oracle.rel_l2(y.cpu().double().numpy(), ref.numpy()) <= tol
+
+
+def test_loader_style_swap(dev):
+    """loader.py:43-51 replaces every nn.Linear (including nn.Sequential
+    children) by make_linear(fmt, weight, None) in place."""
+    announce("loader-style swap")
+    torch.manual_seed(61)
+    model = torch.nn.ModuleDict({
+        "q_proj": torch.nn.Linear(256, 128, bias=False),
+        "lora": torch.nn.Sequential(torch.nn.Linear(256, 32, bias=False), torch.nn.Linear(32, 128, bias=False)),
+    })
+    x = torch.randn(4, 256)
+    ref_q = model["q_proj"](x).detach()
+    ref_l = model["lora"](x).detach()
+    for name, mod in list(model.named_modules()):
+        if isinstance(mod, torch.nn.Linear):
+            parent_name, _, child = name.rpartition(".")
+            parent = model.get_submodule(parent_name) if parent_name else model
+            setattr(parent, child, quant.make_linear("int8", mod.weight.detach(), None))
+    assert not any(isinstance(m, torch.nn.Linear) for m in model.modules())
+    with torch.inference_mode():
+        assert oracle.rel_l2(model["q_proj"](x).numpy(), ref_q.numpy()) <= 2e-2
+        assert oracle.rel_l2(model["lora"](x).numpy(), ref_l.numpy()) <= 3e-2
