@@ -42,6 +42,7 @@ constexpr int kFastXLdsBytes = 32768;  // x[M][K] copied to LDS up to this size
 constexpr int kFastMaxWaves = 8;
 constexpr int kFusedChunks = 4;         // QM 2: 16-byte chunks of x per thread
 constexpr int kFusedMinWaves = 4;       // QM 2: x <= kFusedChunks * 16 * 64 * waves bytes
+constexpr int kFastSplitBytes = 24576;  // fp32 x split into bf16 planes in LDS up to this size
 
 __device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
@@ -116,6 +117,9 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   float2* mmx = (float2*)(smem + red_bytes<G>(KS));
   uint8_t* xs = smem + red_bytes<G>(KS) + mm_bytes();
   const int xrow = K * EB;  // bytes of one x row in LDS
+  constexpr bool kSplitX = XL && XT == XT_F32 && !W8A8;
+  uint8_t* xhi = xs + xch * (int)blockDim.x * 16;  // kSplitX: bf16 planes [M][K] after the raw copy
+  uint8_t* xlo = xhi + M * K * 2;
 
   // epilogue operands of row tile `ks` (wave ks < G finishes tile ks)
   const int nte = min(nt0 + min(ks, G - 1), a.Nt - 1);
@@ -201,6 +205,25 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
     }
     if constexpr (XL) wait_vm<D * G>();  // this wave's x copies are in LDS; weights stay in flight
     lds_barrier();
+    if constexpr (kSplitX) {
+      // fp32 x: split once into bf16 high / remainder planes (the per-tile
+      // split would cost ~48 VALU per lane per tile)
+      const int nel = M * K;
+      for (int e = tid * 4; e < nel; e += (int)blockDim.x * 4) {
+        const f32x4 v = *(const f32x4*)(xs + e * 4);
+        bf16x4 h, l;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          __bf16 hh, ll;
+          split_bf16(v[j], hh, ll);
+          h[j] = hh;
+          l[j] = ll;
+        }
+        *(bf16x4*)(xhi + e * 2) = h;
+        *(bf16x4*)(xlo + e * 2) = l;
+      }
+      lds_barrier();
+    }
     if constexpr (W8A8) {
       float mn = 0.0f, mx = 0.0f;
       for (int i = 0; i < KS; ++i) {
@@ -217,6 +240,22 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   for (int j = 0; j < G; ++j) acc[j] = Acc{0, 0, 0, 0};
   const uint8_t* xl = xs + mr * xrow + g * 16 * EB;
   auto step = [&](int p, int kt) {  // kt: tile index within this wave's range
+    if constexpr (kSplitX) {
+      const int e = mr * K + (kbeg + kt) * 64 + g * 16;
+      const bf16x8 h0 = *(const bf16x8*)(xhi + e * 2), h1 = *(const bf16x8*)(xhi + e * 2 + 16);
+      const bf16x8 l0 = *(const bf16x8*)(xlo + e * 2), l1 = *(const bf16x8*)(xlo + e * 2 + 16);
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        bf16x8 w0, w1;
+        u8x16_to_bf16(w[p][j], w0, w1);
+        // same order as tile_mma<XT_F32>: remainder first, then the high part
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, l0, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, l1, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, h0, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, h1, acc[j], 0, 0, 0);
+      }
+      return;
+    }
     XRaw<XT> f;
     if constexpr (XL) load_frag<XT>(f, xl + (kbeg + kt) * 64 * EB);
     else f = xd[p];
@@ -344,7 +383,11 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   if (c.D * c.G > 32) return -1;
   const int T = ks * 64;
   const int xch = c.XL ? (int)((xbytes / 16 + T - 1) / T) : 0;
-  const size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
+  size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
+  if (c.XL && xt == XT_F32 && !w8a8) {  // bf16 high / remainder planes
+    if (xbytes > kFastSplitBytes) return -1;
+    lds += (size_t)a.M * a.K * 4;
+  }
   const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
   if (qm == 2 && (xbytes > (int64_t)kFusedChunks * 16 * T || ks < kFusedMinWaves)) return -1;
 #define SBQ_FAST_QM(XT_)                                                  \
@@ -366,15 +409,17 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
 // MI355X over the decode shapes (M = 1, 4, 16; K = 4096, 12288; N = 4096 ..
 // 151936): 4-tile steps over two row tiles per wave for wide K = 4096 layers,
 // 8-tile steps over one row tile for long K or narrow N, two waves per row tile
-// once M > 4 (the activation fragments then dominate the registers), and
-// 4-tile single-row-tile steps for fp32 / bf16 activations (costlier
-// conversion, larger fragments).
+// once M > 4 (the activation fragments then dominate the registers).  bf16
+// activations follow the fp16 rules; fp32 activations are copied to LDS and
+// split once into bf16 high / remainder planes when x fits.
 bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks) {
   if (M < 1 || M > 16 || K % 64 != 0 || !xvec) return false;
   const int64_t Kc = K / 64, Nt = (N + 15) / 16;
-  if (xt != XT_F16) {
-    *id = 2;  // D=4, G=1
-    *ks = Kc >= 128 ? 8 : 4;
+  if (xt == XT_F32) {
+    // x in LDS, split once into bf16 planes, when it fits; else 8- or 4-tile
+    // direct steps
+    *id = M * K * 4 <= kFastSplitBytes ? 0 : (Kc >= 128 ? 3 : 2);
+    *ks = 4;
   } else if (M <= 4) {
     const bool wide = Kc < 128 && Nt >= 384;
     *id = wide ? 4 : 3;  // D=4, G=2 | D=8, G=1
