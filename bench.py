@@ -14,7 +14,8 @@ Also reported (``extra``): M=4/16 decode, the 4096x4096 single GEMV (fp32 and
 fp16 activations), the prefill GEMM at M=512/2048/8192 (N=12288, K=4096,
 TFLOP/s vs the 2.5 PFLOP/s dense fp16 peak), int8-dyn at M=1/128/2048, and
 one decode step through all 539 linears of a random-init 36-layer hybrid
-model (hidden 4096, FFN 12288, vocab 151936) at M=1 and M=8.
+model (hidden 4096, FFN 12288, vocab 151936) at M=1 and M=8, unfused and with
+the layers that read the same input fused (223 launches, same weight bytes).
 
 ``roofline`` covers the dominant kernel (the gate+up GEMV launch): its average
 duration is measured with HIP events around a graph of back-to-back launches
@@ -231,25 +232,35 @@ def w8a8_bench(ctx, M, N, K=4096, steps=10, warmup=3):
 # ---------------------------------------------------------------------------
 # one decode step through every quantized linear of the 36-layer hybrid model
 # ---------------------------------------------------------------------------
-def hybrid_stack_shapes(H=4096, F=12288, heads=32, kv_heads=8, d=128, routers=4, vocab=151936, layers=36):
+def hybrid_stack_shapes(H=4096, F=12288, heads=32, kv_heads=8, d=128, routers=4, vocab=151936, layers=36,
+                        fused=False):
+    """(N, K) of every quantized linear of one decode step.  fused=True
+    concatenates the layers that read the same input (FusedLinear): per hybrid
+    block sse_q/k/v + lora_q[0]/lora_k[0] + sse_a/b/e + swa_q/k/v (N=18820),
+    and gate+up; per softmax block q/k/v and gate+up.  Same weight bytes."""
     shapes = []
     for i in range(layers):
         if i in SOFTMAX_LAYERS:
-            shapes += [(heads * d, H), (kv_heads * d, H), (kv_heads * d, H), (H, heads * d)]
+            qkv = [(heads * d, H), (kv_heads * d, H), (kv_heads * d, H)]
+            shapes += [(sum(n for n, _ in qkv), H)] if fused else qkv
+            shapes += [(H, heads * d)]
         else:
-            shapes += [(heads * d, H)] * 3                      # sse_q, sse_k, sse_v
-            shapes += [(d, H), (d, H), (heads * d, d), (heads * d, d)]  # lora_q/k [0], [1]
-            shapes += [(2 * heads, H), (2 * heads, H), (routers, H)]   # sse_a, sse_b, sse_e
-            shapes += [(H, heads * d)]                          # sse_o
-            shapes += [(heads * d, H), (kv_heads * d, H), (kv_heads * d, H), (H, heads * d)]  # swa q,k,v,o
-        shapes += [(F, H), (F, H), (H, F)]                      # gate, up, down
+            reads_x = [(heads * d, H)] * 3                      # sse_q, sse_k, sse_v
+            reads_x += [(d, H), (d, H)]                         # lora_q[0], lora_k[0]
+            reads_x += [(2 * heads, H), (2 * heads, H), (routers, H)]  # sse_a, sse_b, sse_e
+            reads_x += [(heads * d, H), (kv_heads * d, H), (kv_heads * d, H)]  # swa q, k, v
+            shapes += [(sum(n for n, _ in reads_x), H)] if fused else reads_x
+            shapes += [(heads * d, d), (heads * d, d)]          # lora_q[1], lora_k[1]
+            shapes += [(H, heads * d), (H, heads * d)]          # sse_o, swa_o
+        shapes += [(2 * F, H)] if fused else [(F, H), (F, H)]   # gate, up
+        shapes += [(H, F)]                                      # down
     shapes.append((vocab, H))                                   # lm_head
     return shapes
 
 
-def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3):
+def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False):
     torch, quant = ctx.torch, ctx.quant
-    shapes = hybrid_stack_shapes()
+    shapes = hybrid_stack_shapes(fused=fused)
     layers = [ctx.weights(N, K, 2000 + i) for i, (N, K) in enumerate(shapes)]
     wbytes = sum(N * K for N, K in shapes)
     res = {"linears": len(shapes), "weight_bytes": wbytes}
@@ -489,6 +500,8 @@ def main():
         extra["w8a8"] = [w8a8_bench(ctx, M, N) for M in (1, 128, 2048) for N in (4096, 12288)]
         log("36-layer linear stack")
         extra["stack"] = stack_bench(ctx)
+        log("36-layer linear stack, layers reading the same input fused")
+        extra["stack_fused"] = stack_bench(ctx, fused=True)
         torch.cuda.empty_cache()
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)

@@ -3,10 +3,10 @@
 ``sbq.quant`` is the drop-in for ``spikingbrain_cpu/quant.py``; ``sbq._lib`` is
 the ctypes binding of libsbq.so (C ABI: include/sbq.h).
 """
-from .quant import (FORMATS, BF16Linear, DynamicInt8Linear, FloatLinear, FP16Linear, Int8Linear, make_linear,
-                    quantize_per_channel)
+from .quant import (FORMATS, BF16Linear, DynamicInt8Linear, FloatLinear, FP16Linear, FusedLinear, Int8Linear,
+                    fuse_linears, make_linear, quantize_per_channel)
 
 __version__ = "0.1.0"
 
-__all__ = ["FORMATS", "BF16Linear", "DynamicInt8Linear", "FloatLinear", "FP16Linear", "Int8Linear", "make_linear",
-           "quantize_per_channel"]
+__all__ = ["FORMATS", "BF16Linear", "DynamicInt8Linear", "FloatLinear", "FP16Linear", "FusedLinear", "Int8Linear",
+           "fuse_linears", "make_linear", "quantize_per_channel"]

@@ -27,6 +27,7 @@ ROCm GPU every entry point raises: there is no CPU implementation here.
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 import torch.nn as nn
@@ -318,6 +319,96 @@ class FloatLinear(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return _run_on_device(x, self.weight.device, lambda xd: F.linear(xd.float(), self.weight, self.bias))
+
+
+class FusedLinear(nn.Module):
+    """Quantized linears that read the same input, run as one launch over their
+    row-concatenated weights (the q/k/v and gate/up projections of model.py
+    call their modules back to back on one x: model.py:262-264, 363-365).
+    quant.py:25-29 quantizes every output row on its own, so the concatenated
+    qweight / scale rows are exactly the parts' rows; int8-dyn outputs are
+    bit-identical to the separate layers' (one activation quantization for the
+    same x, exact int32 sums), int8 outputs agree to fp32 summation order.
+
+    forward(x) returns one tensor per part (contiguous, like the parts').
+    part(i) is a drop-in module for part i: the parts share the result of one
+    launch for the same input tensor (identity and in-place version checked)."""
+
+    def __init__(self, parts: list[nn.Module]):
+        super().__init__()
+        parts = list(parts)
+        kinds = {type(p) for p in parts}
+        if not parts or len(kinds) != 1 or not kinds <= {Int8Linear, DynamicInt8Linear}:
+            raise ValueError("fuse_linears: the parts must all be Int8Linear or all DynamicInt8Linear")
+        if len({p.in_features for p in parts}) != 1:
+            raise ValueError("fuse_linears: the parts must share in_features")
+        self.w8a8 = kinds == {DynamicInt8Linear}
+        device = parts[0].packed.device
+        self.sizes = [p.out_features for p in parts]
+        self.in_features = parts[0].in_features
+        self.out_features = sum(self.sizes)
+        if self.w8a8:
+            q = torch.cat([unpack(p.packed, p.out_features, p.in_features) for p in parts])
+        else:
+            q = torch.cat([p.qweight.to(device) for p in parts])
+        scale = torch.cat([p.scale.to(device).float() for p in parts])
+        bias = None
+        if any(p.bias is not None for p in parts):
+            bias = torch.cat([p.bias.to(device).float() if p.bias is not None
+                              else torch.zeros(p.out_features, device=device) for p in parts])
+        packed, colsum = repack(q, with_colsum=self.w8a8)
+        self.register_buffer("packed", packed, persistent=False)
+        self.register_buffer("scale", scale, persistent=False)
+        self.register_buffer("colsum", colsum, persistent=False)
+        self.register_buffer("bias", bias, persistent=False)
+        self.out_dtype = torch.float32
+        self._memo_ref = None
+        self._memo_version = -1
+        self._memo_out = None
+
+    def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, ...]:
+        shape = x.shape
+
+        def run(xd):
+            x2 = xd.reshape(-1, shape[-1])
+            if self.w8a8:
+                return linear_w8a8(x2, self.packed, self.scale, self.colsum, self.bias, self.out_features,
+                                   self.out_dtype)
+            return linear_w8(x2, self.packed, self.scale, self.bias, self.out_features, self.out_dtype)
+
+        y = _run_on_device(x, self.packed.device, run)
+        outs = torch.split(y, self.sizes, dim=-1)
+        return tuple(o.contiguous().reshape(*shape[:-1], -1) for o in outs)
+
+    def _shared(self, x: torch.Tensor) -> tuple[torch.Tensor, ...]:
+        ref = self._memo_ref() if self._memo_ref is not None else None
+        if ref is not x or x._version != self._memo_version:
+            out = self.forward(x)
+            self._memo_ref, self._memo_version, self._memo_out = weakref.ref(x), x._version, out
+        return self._memo_out
+
+    def part(self, i: int) -> nn.Module:
+        return _FusedPart(self, i)
+
+
+class _FusedPart(nn.Module):
+    """Part i of a FusedLinear as a module with the part's own forward."""
+
+    def __init__(self, fused: FusedLinear, i: int):
+        super().__init__()
+        self._fused = (fused,)  # not a registered child: the fused weights belong to the FusedLinear
+        self.index = i
+        self.in_features = fused.in_features
+        self.out_features = fused.sizes[i]
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self._fused[0]._shared(x)[self.index]
+
+
+def fuse_linears(parts: list[nn.Module]) -> FusedLinear:
+    """One launch for several Int8Linear (or DynamicInt8Linear) layers that
+    read the same input; see FusedLinear."""
+    return FusedLinear(parts)
 
 
 def make_linear(fmt: str, weight: torch.Tensor, bias: torch.Tensor | None = None) -> nn.Module:

@@ -20,7 +20,7 @@ def test_unknown_format_raises_value_error_like_reference():
 
 def test_public_names():
     for name in ("quantize_per_channel", "Int8Linear", "DynamicInt8Linear", "FP16Linear", "BF16Linear",
-                 "FloatLinear", "make_linear"):
+                 "FloatLinear", "make_linear", "fuse_linears", "FusedLinear"):
         assert hasattr(quant, name)
 
 
@@ -32,3 +32,10 @@ def test_no_cpu_fallback(fmt):
         quant.make_linear(fmt, torch.randn(8, 64))
     with pytest.raises(RuntimeError, match="no ROCm GPU"):
         quant.quantize_per_channel(torch.randn(8, 64))
+
+
+def test_fuse_linears_needs_quantized_parts():
+    with pytest.raises(ValueError):
+        quant.fuse_linears([])
+    with pytest.raises(ValueError):
+        quant.fuse_linears([torch.nn.Linear(4, 4)])

@@ -390,3 +390,55 @@ def test_loader_style_swap(dev):
     with torch.inference_mode():
         assert oracle.rel_l2(model["q_proj"](x).numpy(), ref_q.numpy()) <= 2e-2
         assert oracle.rel_l2(model["lora"](x).numpy(), ref_l.numpy()) <= 3e-2
+
+
+# ---------------------------------------------------------------------------
+# exact N-fusion of layers that read the same input
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M", [1, 5, 70])
+def test_fused_w8a8_bitexact_and_parts(dev, M):
+    """int8-dyn: one activation quantization for the same x and exact int32
+    sums, so the fused layer must equal the separate layers bit for bit."""
+    announce(f"fused w8a8 M={M}")
+    K = 512
+    sizes = (256, 64, 64, 4)
+    ws = [make_weights(n, K, 70 + i) for i, n in enumerate(sizes)]
+    bs = [torch.randn(n) if i == 1 else None for i, n in enumerate(sizes)]
+    mods = [quant.DynamicInt8Linear(w, b) for w, b in zip(ws, bs)]
+    fused = quant.fuse_linears(mods)
+    assert fused.out_features == sum(sizes)
+    x = make_x(M, K, 80, outliers=True).to(dev)
+    outs = fused(x)
+    for m, o in zip(mods, outs):
+        assert o.is_contiguous() and o.shape == (M, m.out_features)
+        np.testing.assert_array_equal(o.cpu().numpy(), m(x).cpu().numpy())
+    parts = [fused.part(i) for i in range(len(sizes))]
+    for m, pmod in zip(mods, parts):
+        np.testing.assert_array_equal(pmod(x).cpu().numpy(), m(x).cpu().numpy())
+    x.mul_(0.5)  # in-place change: the parts must not reuse the earlier launch
+    for m, pmod in zip(mods, parts):
+        np.testing.assert_array_equal(pmod(x).cpu().numpy(), m(x).cpu().numpy())
+
+
+@pytest.mark.parametrize("M", [1, 3, 40])
+def test_fused_w8_matches_parts(dev, M):
+    announce(f"fused w8 M={M}")
+    K = 1024
+    sizes = (512, 128, 128)
+    ws = [make_weights(n, K, 90 + i) for i, n in enumerate(sizes)]
+    mods = [quant.Int8Linear(w, None) for w in ws]
+    fused = quant.fuse_linears(mods)
+    x = make_x(M, K, 99).reshape(1, M, K)
+    outs = fused(x)  # CPU in, CPU out, [1, M, n]
+    for w, m, o in zip(ws, mods, outs):
+        assert o.device.type == "cpu" and o.shape == (1, M, m.out_features)
+        q, s = oracle.quantize_per_channel(w.numpy())
+        assert oracle.rel_l2(o.reshape(M, -1).numpy(), oracle.int8_linear(x.reshape(M, K).numpy(), q, s)) <= 1e-5
+
+
+def test_fuse_linears_rejects_mixed_parts(dev):
+    a = quant.Int8Linear(make_weights(16, 64, 1), None)
+    with pytest.raises(ValueError):
+        quant.fuse_linears([a, quant.DynamicInt8Linear(make_weights(16, 64, 2), None)])
+    with pytest.raises(ValueError):
+        quant.fuse_linears([a, quant.Int8Linear(make_weights(16, 128, 3), None)])
