@@ -26,6 +26,9 @@
  *                                quantization parameters chosen inside
  *                                torch.ops.quantized.linear_dynamic)
  *   sbq_linear_w8a8           <- spikingbrain_cpu/quant.py:63-66 DynamicInt8Linear.forward
+ *   sbq_argmax_rows           <- spikingbrain_cpu/engine.py:30-31 (greedy sampling,
+ *                                int(logits.argmax()) over the lm_head output of
+ *                                model.py:447), so the logits need not leave the GPU
  */
 #ifndef SBQ_H_
 #define SBQ_H_
@@ -142,6 +145,13 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
                     const float* bias, int64_t N,
                     void* y, int y_dtype, int64_t ldy, int32_t* acc_out,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- greedy token selection (engine.py:30-31) ---- */
+
+/* idx[m] = the first n with y[m, n] maximal over row m of fp32 y [M, N] (row
+ * stride ldy); NaN ranks above every number (torch.argmax semantics).
+ * idx: device int64 [M]. */
+int sbq_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* idx, void* stream);
 
 #ifdef __cplusplus
 }

@@ -155,4 +155,11 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
                                parts, ws_xq(workspace), ws_qp(workspace), st, yv);
 }
 
+int sbq_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* idx, void* stream) {
+  if (M < 0 || N < 1 || ldy < N || N > kIntMax || M > kIntMax) return SBQ_ERR_ARG;
+  if (M == 0) return SBQ_OK;
+  if (!y || !idx) return SBQ_ERR_ARG;
+  return sbq::launch_argmax_rows(y, M, N, ldy, idx, (hipStream_t)stream);
+}
+
 }  // extern "C"

@@ -22,6 +22,7 @@ int minmax_nparts(int64_t M, int64_t K);
 int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, float2* partials,
                            int nparts, hipStream_t st);
 int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t* zp_out, hipStream_t st);
+int launch_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* out, hipStream_t st);
 
 // True when the streaming GEMV kernels take this M and K (otherwise the GEMM).
 bool gemv_supports(int64_t M, int64_t K, bool w8a8, int xt);

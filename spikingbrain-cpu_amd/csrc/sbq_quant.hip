@@ -134,6 +134,78 @@ __global__ __launch_bounds__(256) void qparams_kernel(const float2* __restrict__
 }
 
 // ---------------------------------------------------------------------------
+// Row argmax of fp32 logits (greedy sampling, engine.py:30-31
+// `int(logits.argmax())` over the lm_head output): the first index of the
+// largest value, NaN above every number, as torch.argmax.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn != bn) return vn;
+  if (vn) return i < bi;
+  return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void arg_take(float v, int i, float& bv, int& bi) {
+  if (arg_better(v, i, bv, bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+// One workgroup per row; each thread keeps four independent running bests so
+// that four vector loads are in flight at a time.
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restrict__ y, int N, int64_t ldy,
+                                                           int64_t* __restrict__ out, int vec) {
+  const float* row = y + (int64_t)blockIdx.x * ldy;
+  float bv[4];
+  int bi[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    bv[u] = -__builtin_inff();
+    bi[u] = 0x7fffffff;
+  }
+  const int T = blockDim.x, t = threadIdx.x;
+  int i0 = 0;
+  if (vec) {
+    const int n4 = N / 4;
+    int c = t;
+    for (; c + 3 * T < n4; c += 4 * T) {
+      f32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = *(const f32x4*)(row + 4 * (c + u * T));
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) arg_take(v[u][j], 4 * (c + u * T) + j, bv[u], bi[u]);
+    }
+    for (; c < n4; c += T) {
+      const f32x4 v = *(const f32x4*)(row + 4 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) arg_take(v[j], 4 * c + j, bv[0], bi[0]);
+    }
+    i0 = n4 * 4;
+  }
+  for (int i = i0 + t; i < N; i += T) arg_take(row[i], i, bv[0], bi[0]);
+#pragma unroll
+  for (int u = 1; u < 4; ++u) arg_take(bv[u], bi[u], bv[0], bi[0]);
+  float v = bv[0];
+  int i = bi[0];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) arg_take(__shfl_xor(v, o, 64), __shfl_xor(i, o, 64), v, i);
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  if ((t & 63) == 0) {
+    sv[t >> 6] = v;
+    si[t >> 6] = i;
+  }
+  __syncthreads();
+  if (t == 0) {
+    for (int w = 1; w < (T >> 6); ++w) arg_take(sv[w], si[w], v, i);
+    out[blockIdx.x] = i;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
 int launch_quantize_per_channel(const void* w, int wt, int64_t N, int64_t K, int64_t ldw, int8_t* q,
@@ -192,6 +264,12 @@ int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t 
 
 int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t* zp_out, hipStream_t st) {
   hipLaunchKernelGGL(qparams_kernel, dim3(1), dim3(256), 0, st, partials, nparts, scale_out, zp_out);
+  return check_launch();
+}
+
+int launch_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* out, hipStream_t st) {
+  const int vec = ((uintptr_t)y % 16 == 0) && (ldy % 4 == 0);
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)M), dim3(1024), 0, st, y, (int)N, ldy, out, vec);
   return check_launch();
 }
 

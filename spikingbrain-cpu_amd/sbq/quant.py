@@ -158,6 +158,22 @@ def linear_w8a8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, col
     return y
 
 
+def greedy_tokens(logits: torch.Tensor) -> torch.Tensor:
+    """engine.py:30-31 on the GPU: int64 [...] of row argmaxes of fp32 logits
+    [..., V] (first index of the maximum, NaN above every number)."""
+    if logits.dtype != torch.float32 or not logits.is_cuda:
+        raise ValueError("greedy_tokens expects fp32 GPU logits")
+    shape = logits.shape
+    y = logits.reshape(-1, shape[-1])
+    if y.stride(-1) != 1:
+        y = y.contiguous()
+    out = torch.empty((y.shape[0],), dtype=torch.int64, device=y.device)
+    with torch.cuda.device(y.device):
+        _lib.check(_lib.load().sbq_argmax_rows(_ptr(y), y.shape[0], y.shape[1], y.stride(0), _ptr(out),
+                                               _stream(y.device)), "sbq_argmax_rows")
+    return out.reshape(shape[:-1])
+
+
 def act_qparams(x2: torch.Tensor) -> tuple[float, int]:
     """The per-tensor (scale, zero_point) the int8-dyn path uses for x2 [M, K]."""
     x2 = _as_activation(x2)
@@ -215,6 +231,25 @@ class Int8Linear(nn.Module):
 
     def _repack(self):
         self.packed = repack(self.qweight.contiguous(), with_colsum=False)[0]
+
+    @classmethod
+    def from_quantized(cls, qweight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None = None,
+                       block: int = 128) -> "Int8Linear":
+        """An Int8Linear from an already quantized int8 [N,K] / fp32 [N] pair (the
+        state_dict entries of quant.py:36-37): no re-quantization at load."""
+        if qweight.dtype != torch.int8 or qweight.dim() != 2 or scale.shape != (qweight.shape[0],):
+            raise ValueError("from_quantized expects int8 qweight [N, K] and scale [N]")
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        device = _gpu_for(qweight)
+        self.register_buffer("qweight", qweight.to(device).contiguous())
+        self.register_buffer("scale", scale.to(device=device, dtype=torch.float32).contiguous())
+        self.bias = None if bias is None else nn.Parameter(bias.to(device).float(), requires_grad=False)
+        self.block = block
+        self.register_buffer("packed", repack(self.qweight, with_colsum=False)[0], persistent=False)
+        self.out_dtype = torch.float32
+        self.register_load_state_dict_post_hook(lambda module, incompatible: module._repack())
+        return self
 
     @property
     def in_features(self) -> int:
@@ -276,6 +311,66 @@ class DynamicInt8Linear(nn.Module):
 
         out = _run_on_device(x, self.packed.device, run)
         return out.reshape(*shape[:-1], -1)
+
+
+def _dyn_from_quantized(qweight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None) -> "DynamicInt8Linear":
+    if qweight.dtype != torch.int8 or qweight.dim() != 2 or scale.shape != (qweight.shape[0],):
+        raise ValueError("from_quantized expects int8 qweight [N, K] and scale [N]")
+    self = DynamicInt8Linear.__new__(DynamicInt8Linear)
+    nn.Module.__init__(self)
+    device = _gpu_for(qweight)
+    packed, colsum = repack(qweight.to(device).contiguous(), with_colsum=True)
+    self.register_buffer("packed", packed, persistent=False)
+    self.register_buffer("scale", scale.to(device=device, dtype=torch.float32).contiguous(), persistent=False)
+    self.register_buffer("colsum", colsum, persistent=False)
+    self.register_buffer("bias", None if bias is None else bias.to(device).float(), persistent=False)
+    self.in_features = qweight.shape[1]
+    self.out_features = qweight.shape[0]
+    self.out_dtype = torch.float32
+    return self
+
+
+DynamicInt8Linear.from_quantized = staticmethod(_dyn_from_quantized)
+
+
+def save_quantized(layers: dict[str, nn.Module], path: str) -> None:
+    """Write the int8 rows and fp32 scales (and biases) of Int8Linear /
+    DynamicInt8Linear layers to a safetensors file (keys <name>.qweight,
+    <name>.scale, <name>.bias), so a later load skips quant.py:25-29."""
+    from safetensors.torch import save_file
+
+    tensors = {}
+    for name, mod in layers.items():
+        if isinstance(mod, Int8Linear):
+            q = mod.qweight
+        elif isinstance(mod, DynamicInt8Linear):
+            q = unpack(mod.packed, mod.out_features, mod.in_features)
+        else:
+            raise ValueError(f"save_quantized: {name} is not an int8 layer")
+        tensors[name + ".qweight"] = q.contiguous().cpu()
+        tensors[name + ".scale"] = mod.scale.float().contiguous().cpu()
+        if mod.bias is not None:
+            tensors[name + ".bias"] = mod.bias.detach().float().contiguous().cpu()
+    save_file(tensors, path, metadata={"format": "sbq-int8-per-channel"})
+
+
+def load_quantized(path: str, fmt: str = "int8", device: torch.device | None = None) -> dict[str, nn.Module]:
+    """Layers of a save_quantized file as Int8Linear (fmt "int8") or
+    DynamicInt8Linear (fmt "int8-dyn") on the GPU, without re-quantizing."""
+    from safetensors.torch import load_file
+
+    if fmt not in ("int8", "int8-dyn"):
+        raise ValueError("unknown weight format " + fmt)
+    t = load_file(path, device="cpu")
+    out = {}
+    for key in sorted(k for k in t if k.endswith(".qweight")):
+        name = key[: -len(".qweight")]
+        q, s, b = t[key], t[name + ".scale"], t.get(name + ".bias")
+        if device is not None:
+            q = q.to(device)
+        out[name] = (Int8Linear.from_quantized(q, s, b) if fmt == "int8"
+                     else DynamicInt8Linear.from_quantized(q, s, b))
+    return out
 
 
 class FP16Linear(nn.Module):

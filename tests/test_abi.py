@@ -25,7 +25,8 @@ def lib():
 
 def test_header_declares_the_expected_entry_points():
     syms = declared_symbols()
-    for s in ("sbq_quantize_per_channel", "sbq_repack_w8", "sbq_linear_w8", "sbq_linear_w8a8", "sbq_act_qparams"):
+    for s in ("sbq_quantize_per_channel", "sbq_repack_w8", "sbq_linear_w8", "sbq_linear_w8a8", "sbq_act_qparams",
+              "sbq_argmax_rows"):
         assert s in syms
 
 
@@ -78,6 +79,11 @@ def test_argument_validation_without_gpu(lib):
     assert lib.sbq_quantize_per_channel(dummy, 5, 4, 4, 4, dummy, 4, dummy, None) == -2
     assert lib.sbq_repack_w8(dummy, 4, 64, 32, dummy, None, None) == -1
     assert lib.sbq_act_qparams(dummy, 0, 1, 64, 64, dummy, dummy, None, 0, None) == -4
+    # argmax: N < 1, ldy < N, null pointers; M == 0 is a no-op
+    assert lib.sbq_argmax_rows(dummy, 1, 0, 0, dummy, None) == -1
+    assert lib.sbq_argmax_rows(dummy, 1, 8, 4, dummy, None) == -1
+    assert lib.sbq_argmax_rows(None, 1, 8, 8, dummy, None) == -1
+    assert lib.sbq_argmax_rows(None, 0, 8, 8, None, None) == 0
 
 
 def test_python_binding_maps_status_to_exceptions():

@@ -442,3 +442,61 @@ def test_fuse_linears_rejects_mixed_parts(dev):
         quant.fuse_linears([a, quant.DynamicInt8Linear(make_weights(16, 64, 2), None)])
     with pytest.raises(ValueError):
         quant.fuse_linears([a, quant.Int8Linear(make_weights(16, 128, 3), None)])
+
+
+# ---------------------------------------------------------------------------
+# greedy token selection on the GPU (engine.py:30-31)
+# ---------------------------------------------------------------------------
+def test_greedy_tokens_match_torch_argmax(dev):
+    announce("greedy tokens")
+    g = torch.Generator().manual_seed(3)
+    V = 151936
+    logits = torch.randn(3, V, generator=g)
+    logits[1, 5] = logits[1, 100] = 50.0           # tie: the first index wins
+    logits[2, 7] = float("nan")                     # NaN ranks above numbers
+    logits[2, 9] = float("nan")
+    got = quant.greedy_tokens(logits.to(dev)).cpu()
+    np.testing.assert_array_equal(got.numpy(), torch.argmax(logits, dim=-1).numpy())
+    assert got.tolist()[1:] == [5, 7]
+    neg = torch.full((2, 1000), float("-inf"))
+    assert quant.greedy_tokens(neg.to(dev)).tolist() == [0, 0]
+    # rows that do not start 16-byte aligned take the scalar path
+    wide = torch.randn(4, 1003, generator=g)
+    sub = wide.to(dev)[:, 1:]
+    np.testing.assert_array_equal(quant.greedy_tokens(sub).cpu().numpy(),
+                                  torch.argmax(wide[:, 1:], dim=-1).numpy())
+
+
+def test_greedy_tokens_after_lm_head(dev):
+    """lm_head (model.py:447) then greedy sampling: the token equals torch's
+    argmax of the same fp32 logits."""
+    announce("lm_head + greedy")
+    V, H = 32000, 1024
+    lm = quant.Int8Linear(make_weights(V, H, 123), None)
+    x = make_x(2, H, 124).to(dev)
+    logits = lm(x)
+    np.testing.assert_array_equal(quant.greedy_tokens(logits).cpu().numpy(),
+                                  torch.argmax(logits.cpu(), dim=-1).numpy())
+
+
+# ---------------------------------------------------------------------------
+# pre-quantized weights: no re-quantization at load
+# ---------------------------------------------------------------------------
+def test_from_quantized_and_safetensors_roundtrip(dev, tmp_path):
+    announce("prequantized load")
+    N, K = 80, 384
+    w = make_weights(N, K, 131)
+    b = torch.randn(N)
+    lin = quant.Int8Linear(w, b)
+    dyn = quant.DynamicInt8Linear(w, None)
+    x = make_x(4, K, 132).to(dev)
+    same = quant.Int8Linear.from_quantized(lin.qweight, lin.scale, lin.bias)
+    np.testing.assert_array_equal(same(x).cpu().numpy(), lin(x).cpu().numpy())
+    path = str(tmp_path / "layers.safetensors")
+    quant.save_quantized({"mlp.up": lin, "attn.q": dyn}, path)
+    w8 = quant.load_quantized(path, "int8")
+    np.testing.assert_array_equal(w8["mlp.up"](x).cpu().numpy(), lin(x).cpu().numpy())
+    dy = quant.load_quantized(path, "int8-dyn")
+    np.testing.assert_array_equal(dy["attn.q"](x).cpu().numpy(), dyn(x).cpu().numpy())
+    with pytest.raises(ValueError):
+        quant.load_quantized(path, "float8")
