@@ -416,11 +416,13 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
         }
       }
     }
-    if constexpr (NS == 2) barrier_nofence();  // stage i % 2 is overwritten by the next issue
+    // No barrier here: the stage this step read is overwritten only by the
+    // issue after the next step's barrier, which every wave reaches after its
+    // reads of this stage have returned (their MFMAs consumed them).
   }
 
   if constexpr (KG > 1) {
-    if constexpr (NS > 2) barrier_nofence();  // every group is done with its stages
+    barrier_nofence();  // every group is done with its stages before they become the reduction buffer
     Acc* red = (Acc*)lds;
     if (kg > 0) {
 #pragma unroll
