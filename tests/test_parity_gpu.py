@@ -500,3 +500,52 @@ def test_from_quantized_and_safetensors_roundtrip(dev, tmp_path):
     np.testing.assert_array_equal(dy["attn.q"](x).cpu().numpy(), dyn(x).cpu().numpy())
     with pytest.raises(ValueError):
         quant.load_quantized(path, "float8")
+
+
+# ---------------------------------------------------------------------------
+# HIP graph capture: every entry point replays correctly with eager work between
+# ---------------------------------------------------------------------------
+def test_graph_replays_match_eager(dev):
+    announce("graph replays")
+    K = 1024
+    w = make_weights(320, K, 141)
+    lin = quant.Int8Linear(w, torch.randn(320))
+    dyn = quant.DynamicInt8Linear(w, None)
+    shapes = [(1, True), (3, False), (96, True)]  # fast GEMV, general GEMV (misaligned rows), GEMM
+    xs = []
+    for M, aligned in shapes:
+        big = make_x(M, K + 8, 142 + M).to(dev)
+        xs.append(big[:, :K] if aligned else big[:, 1:1 + K])
+    ws_dyn = [quant.w8a8_workspace(x.shape[0], K, dev) for x in xs]
+    outs = {}
+
+    def body():
+        for i, x in enumerate(xs):
+            outs[("w8", i)] = quant.linear_w8(x, lin.packed, lin.scale, lin.bias, 320)
+            outs[("dyn", i)] = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, 320,
+                                                 workspace=ws_dyn[i])
+        outs["tok"] = quant.greedy_tokens(outs[("w8", 0)])
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        body()
+    for rep in range(3):
+        for x in xs:  # eager work between replays: new activations in place
+            x.mul_(-1.25).add_(0.5 * rep)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, x in enumerate(xs):
+            eager_w8 = quant.linear_w8(x, lin.packed, lin.scale, lin.bias, 320)
+            eager_dyn = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, 320)
+            np.testing.assert_array_equal(outs[("w8", i)].cpu().numpy(), eager_w8.cpu().numpy(),
+                                          err_msg=f"w8 replay {rep} M={x.shape[0]}")
+            np.testing.assert_array_equal(outs[("dyn", i)].cpu().numpy(), eager_dyn.cpu().numpy(),
+                                          err_msg=f"w8a8 replay {rep} M={x.shape[0]}")
+        assert outs["tok"].item() == int(torch.argmax(outs[("w8", 0)][0]).item())
