@@ -319,6 +319,40 @@ def traffic_probe(ctx, launches=24, cal_reps=4):
     log(f"traffic probe: {launches} gate+up launches, {cal_reps} copies of {CAL_BYTES >> 20} MiB")
 
 
+def prefill_probe(ctx, M=2048, N=12288, K=4096, launches=4):
+    """The prefill GEMM alone (int8 weights, fp16 x and y), for counter passes."""
+    torch, quant = ctx.torch, ctx.quant
+    packed, s, _ = ctx.weights(N, K, 900)
+    x = ctx.act(M, K, 901)
+    y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
+    torch.cuda.synchronize()
+    for _ in range(launches):
+        quant.linear_w8(x, packed, s, None, N, out=y)
+    torch.cuda.synchronize()
+    log(f"prefill probe: {launches} launches of M={M} N={N} K={K}")
+
+
+def summarize_counters(dirs, match, command):
+    """Markdown table: per-dispatch averages of every counter collected in the
+    rocprofv3 --pmc output directories, for kernels whose name contains match."""
+    rows = []
+    for d in dirs:
+        acc = {}
+        for r in _csv_rows(d, "counter_collection.csv"):
+            if match not in r["Kernel_Name"]:
+                continue
+            k = (r["Dispatch_Id"], r["Counter_Name"])
+            acc[k] = acc.get(k, 0.0) + float(r["Counter_Value"])
+        per = {}
+        for (_, c), v in acc.items():
+            per.setdefault(c, []).append(v)
+        rows += [(c, sum(v) / len(v), len(v)) for c, v in sorted(per.items())]
+    out = [f"# rocprofv3 counters of `{match}`", "", "Command:", "", "```", command, "```", "",
+           "| counter | average per dispatch | dispatches |", "|---|---|---|"]
+    out += [f"| {c} | {v:.6g} | {n} |" for c, v, n in rows]
+    return "\n".join(out) + "\n"
+
+
 def _csv_rows(d, suffix):
     import csv
 
@@ -459,6 +493,11 @@ def main():
     ap.add_argument("--summarize-trace", metavar="DIR", help="print a markdown summary of a rocprofv3 kernel trace")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the traffic JSON from FETCH_SIZE and WRITE_SIZE passes over --traffic-probe")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="only run the M=2048 prefill GEMM (workload of the prefill counter passes)")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
+                    help="print per-dispatch counter averages from rocprofv3 --pmc directories")
+    ap.add_argument("--match", default="gemm_dl_kernel", help="kernel-name filter for --summarize-counters")
     ap.add_argument("--command", default="", help="the profiling command(s), recorded in the summary")
     args = ap.parse_args()
     if args.summarize_trace:
@@ -466,6 +505,9 @@ def main():
         return
     if args.summarize_pmc:
         print(summarize_pmc(*args.summarize_pmc, args.command), end="")
+        return
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters, args.match, args.command), end="")
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported in this build "
@@ -479,6 +521,9 @@ def main():
     torch = ctx.torch
     if args.traffic_probe:
         traffic_probe(ctx)
+        return
+    if args.prefill_probe:
+        prefill_probe(ctx)
         return
     log("decode M=1 (headline)")
     head = decode_bench(ctx, 1, args.steps, args.warmup)
