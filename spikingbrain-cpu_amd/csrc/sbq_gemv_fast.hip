@@ -409,7 +409,7 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
 // MI355X over the decode shapes (M = 1, 4, 16; K = 4096, 12288; N = 4096 ..
 // 151936): 4-tile steps over two row tiles per wave for wide K = 4096 layers,
 // 8-tile steps over one row tile for long K or narrow N, two waves per row tile
-// once M > 4 (the activation fragments then dominate the registers).  bf16
+// once M > 8 (the activation fragments then dominate the registers).  bf16
 // activations follow the fp16 rules; fp32 activations are copied to LDS and
 // split once into bf16 high / remainder planes when x fits.
 bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks) {
@@ -420,7 +420,7 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     // direct steps
     *id = M * K * 4 <= kFastSplitBytes ? 0 : (Kc >= 128 ? 3 : 2);
     *ks = 4;
-  } else if (M <= 4) {
+  } else if (M <= 8) {
     const bool wide = Kc < 128 && Nt >= 384;
     *id = wide ? 4 : 3;  // D=4, G=2 | D=8, G=1
     *ks = 4;
