@@ -107,11 +107,19 @@ int sbq_unpack_w8(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_
  * or NULL.  y: device [M, N] (row stride ldy), dtype F32, F16 or BF16.
  * Accumulation is fp32.  M <= 32 runs the HBM-streaming MFMA GEMV; larger M
  * runs the LDS-tiled MFMA GEMM.
- * workspace: unused by this entry point (pass NULL, 0). */
+ * workspace: optional (NULL, 0 is valid).  With >= sbq_w8_workspace_bytes(M, K)
+ * bytes, the F16 prefill GEMM takes its per-row activation sums from a
+ * pre-pass instead of accumulating them in its K loop (faster; results agree
+ * to fp32 rounding).  Other dtypes and the GEMV ignore it. */
 int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   const uint8_t* packed, const float* scale, const float* bias, int64_t N,
                   void* y, int y_dtype, int64_t ldy,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes that let sbq_linear_w8 run its fast fp16 prefill path for
+ * an [M, K] input: M floats plus alignment slack.  No counterpart in the
+ * reference (its CPU matmul needs no scratch). */
+int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K);
 
 /* ---- int8-dyn W8A8 linear (DynamicInt8Linear.forward, quant.py:63-66) ---- */
 

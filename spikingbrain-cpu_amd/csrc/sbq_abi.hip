@@ -104,17 +104,25 @@ int sbq_unpack_w8(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_
   return sbq::launch_unpack(packed, N, K, q, ldq, (hipStream_t)stream);
 }
 
+int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K) {
+  (void)K;
+  if (M < 0) return 0;
+  return 256 + ((M * 4 + 255) & ~(int64_t)255);
+}
+
 int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
                   const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
                   void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   int rc = check_linear(x, x_dtype, M, K, ldx, packed, scale, N, y, y_dtype, ldy);
   if (rc || M == 0) return rc;
   const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
   hipStream_t st = (hipStream_t)stream;
   if (sbq::gemv_supports(M, K, false, x_dtype)) return sbq::launch_gemv_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
-  return sbq::launch_gemm_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
+  // optional: row-sum scratch for the fp16 prefill GEMM (256-byte aligned)
+  float* rsum = nullptr;
+  if (workspace && (int64_t)workspace_bytes >= sbq_w8_workspace_bytes(M, K))
+    rsum = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  return sbq::launch_gemm_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, rsum, st, yv);
 }
 
 int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K) {

@@ -48,6 +48,15 @@ __device__ __forceinline__ void u8x4_to_f16(uint32_t w, f16x2& lo, f16x2& hi) {
   hi = __builtin_bit_cast(f16x2, b) - bias;
 }
 
+// 8 offset-binary bytes u = q + 128 -> 8 fp16 subnormals u * 2^-24 (exact,
+// one v_perm per pair of values).  The caller removes the offset:
+// sum_k u_k x_k = 2^24 * sum_k (q_k x_k) * 2^-24 + 128 * sum_k x_k.
+__device__ __forceinline__ f16x8 u8x8_to_f16_sub(uint32_t lo, uint32_t hi) {
+  const u32x4 d = {__builtin_amdgcn_perm(0u, lo, 0x0c010c00u), __builtin_amdgcn_perm(0u, lo, 0x0c030c02u),
+                   __builtin_amdgcn_perm(0u, hi, 0x0c010c00u), __builtin_amdgcn_perm(0u, hi, 0x0c030c02u)};
+  return __builtin_bit_cast(f16x8, d);
+}
+
 // 16 offset-binary bytes (one lane slot of a tile) -> two fp16 MFMA operands:
 // s0 = columns 0..7, s1 = columns 8..15 of the slot.
 __device__ __forceinline__ void u8x16_to_f16(u32x4 w, f16x8& s0, f16x8& s1) {

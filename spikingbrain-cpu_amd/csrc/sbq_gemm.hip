@@ -252,6 +252,17 @@ __device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 
+// Raw buffer over [base, base + bytes): loads outside it return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes per lane from buffer offset voff + soff straight into LDS at
+// lds + 16 * lane (lds wave-uniform).
+__device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff, void* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
 // s_waitcnt vmcnt(n) (n < 64) leaving the other counters unconstrained.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -301,6 +312,7 @@ struct GemmArgs {
   int64_t ldy;
   int32_t* acc_out;     // I8 only, may be null
   const float* qpbuf;   // I8 only: (s_x, zp as int bits)
+  const float* rsum;    // fp16 W-only with RSP: per-row sums of x [M]
   int flags;            // bit 1: y rows 4-element vector stores
 };
 
@@ -315,7 +327,9 @@ struct GemmArgs {
 template <int BN, int BM, int WN, int WM>
 constexpr int dl_min_waves() { return (BN / WN) * (BM / WM) > 64 * 64 ? 2 : 4; }
 
-template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG>
+// RSP (fp16 W-only): the per-row sums of x come precomputed in a.rsum instead
+// of being accumulated in the K loop.
+template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false>
 __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) void gemm_dl_kernel(const GemmArgs a) {
   typedef GemmOp<XT> Op;
   typedef typename Op::V V;
@@ -329,13 +343,22 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   constexpr int LPS = (WT + XR) / GW;   // DMA instructions per wave per stage
   constexpr int RED = (KG - 1) * GW * FN * FM * 1024;
   constexpr int LDSB = KG * NS * STAGE > RED ? KG * NS * STAGE : RED;
+  // fp16 activations: weights enter the MFMA as subnormals u * 2^-24 (u = q + 128,
+  // one v_perm per pair); the 128 * rowsum(x) offset is removed in the epilogue.
+  constexpr bool OFS = !I8 && XT == XT_F16;
+  constexpr bool RSK = OFS && !RSP;  // row sums accumulated here
+  constexpr int RF = FM / WN;        // activation fragments whose row sums each wave keeps
   static_assert(WT % GW == 0 && XR % GW == 0, "even DMA split");
   static_assert(NS >= 2 && NS <= 8, "stages");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDSB];
+  static_assert(FM % WN == 0, "row-sum split");
+  // one LDS object: with a second one the compiler waits for every stage DMA in
+  // flight before any LDS read of the main loop (it cannot tell them apart)
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDSB + (RSK ? KG * BM * 4 : 0)];
+  float* const rsum_lds = (float*)(lds + LDSB);
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r = lane & 15, g = lane >> 4;
-  const int kg = wave / GW, w = wave % GW;
+  const int kg = wave / GW, w = __builtin_amdgcn_readfirstlane(wave % GW);  // wave-uniform: LDS targets stay scalar
   const int wn = w / WM, wm = w % WM;
   const int nt0 = blockIdx.x * WT, m0 = blockIdx.y * BM;
   const int M = a.M, Kc = a.Kc, Nt = a.Nt;
@@ -345,31 +368,46 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   const uint8_t* xg = (const uint8_t*)a.x;
   const int64_t xrow = I8 ? a.ldx : a.ldx * 2;  // bytes per activation row
 
+  // Per-lane byte offsets of this wave's DMA slots from the block's first
+  // weight tile / activation row; fixed over the K loop, so each stage issues
+  // from a wave-uniform base (scalar registers) plus these offsets.  The
+  // launcher keeps them below 2^31.
+  uint32_t woff[WT / GW], xoff[XR / GW];
+#pragma unroll
+  for (int i2 = 0; i2 < WT / GW; ++i2) {
+    const int j = w * (WT / GW) + i2;
+    woff[i2] = (uint32_t)(min(nt0 + j, Nt - 1) - nt0) * (uint32_t)Kc * 1024u + lane * 16;
+  }
+#pragma unroll
+  for (int i2 = 0; i2 < XR / GW; ++i2) {
+    const int j = w * (XR / GW) + i2;
+    if constexpr (I8) {
+      const int row = j * 16 + (lane >> 2);
+      const int chunk = (lane & 3) ^ ((row >> 2) & 3);
+      xoff[i2] = (uint32_t)((int64_t)(min(m0 + row, M - 1) - m0) * xrow) + chunk * 16;
+    } else {
+      const int row = j * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+      xoff[i2] = (uint32_t)((int64_t)(min(m0 + row, M - 1) - m0) * xrow) + chunk * 16;
+    }
+  }
+  const __amdgpu_buffer_rsrc_t wrs =
+      raw_rsrc(a.packed + (int64_t)nt0 * Kc * 1024, (uint32_t)min((int64_t)(Nt - nt0) * Kc * 1024, (int64_t)0xffffffff));
+  const __amdgpu_buffer_rsrc_t xrs =
+      raw_rsrc(xg + (int64_t)m0 * xrow, (uint32_t)min((int64_t)(M - m0) * xrow, (int64_t)0xffffffff));
+
+  // this wave's LDS slots within a stage (scalar)
+  const int wslot = __builtin_amdgcn_readfirstlane(w * (WT / GW) * 1024);
+  const int xslot = __builtin_amdgcn_readfirstlane(WBYTES + w * (XR / GW) * 1024);
   auto issue = [&](int i, int st) {
     // clamped: the surplus stages of a short last group are never multiplied
     const int kc = KG == 1 ? i : max(0, min(kbeg + min(i, cnt - 1), Kc - 1));
-    uint8_t* base = lds + (kg * NS + st) * STAGE;
+    const int sb = __builtin_amdgcn_readfirstlane((kg * NS + st) * STAGE);
 #pragma unroll
-    for (int i2 = 0; i2 < WT / GW; ++i2) {
-      const int j = w * (WT / GW) + i2;
-      const int nt = min(nt0 + j, Nt - 1);
-      lds_dma16(a.packed + ((int64_t)nt * Kc + kc) * 1024 + lane * 16, base + j * 1024);
-    }
+    for (int i2 = 0; i2 < WT / GW; ++i2) lds_dma16_buf(wrs, woff[i2], kc * 1024, lds + sb + wslot + i2 * 1024);
 #pragma unroll
-    for (int i2 = 0; i2 < XR / GW; ++i2) {
-      const int j = w * (XR / GW) + i2;
-      if constexpr (I8) {
-        const int row = j * 16 + (lane >> 2);
-        const int chunk = (lane & 3) ^ ((row >> 2) & 3);
-        const int m = min(m0 + row, M - 1);
-        lds_dma16(xg + (int64_t)m * xrow + kc * 64 + chunk * 16, base + WBYTES + j * 1024);
-      } else {
-        const int row = j * 8 + (lane >> 3);
-        const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-        const int m = min(m0 + row, M - 1);
-        lds_dma16(xg + (int64_t)m * xrow + (kc * 64 + chunk * 8) * 2, base + WBYTES + j * 1024);
-      }
-    }
+    for (int i2 = 0; i2 < XR / GW; ++i2)
+      lds_dma16_buf(xrs, xoff[i2], kc * (I8 ? 64 : 128), lds + sb + xslot + i2 * 1024);
   };
 
   Acc acc[FN][FM];
@@ -377,6 +415,12 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   for (int i = 0; i < FN; ++i)
 #pragma unroll
     for (int b = 0; b < FM; ++b) acc[i][b] = Acc{0, 0, 0, 0};
+  // OFS: wave (wn, wm) sums the activation rows of fragments b = wn + j*WN
+  // (each row of the block once over the WN waves); lane (g, r) holds row r of
+  // the fragment over its K columns
+  float rs[RF];
+#pragma unroll
+  for (int j = 0; j < RF; ++j) rs[j] = 0.0f;
 
 #pragma unroll
   for (int i = 0; i < NS - 1; ++i)
@@ -405,11 +449,25 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
           V xf[FM];
 #pragma unroll
           for (int b = 0; b < FM; ++b) xf[b] = *(const V*)(xs + xsw_off(wm * TM + b * 16 + r, 2 * g + s2));
+          if constexpr (RSK) {
+#pragma unroll
+            for (int j = 0; j < RF; ++j) {
+              const u32x4 xv = *(const u32x4*)(xs + xsw_off(wm * TM + (wn + j * WN) * 16 + r, 2 * g + s2));
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t word = xv[e];  // bit_cast of a vector element reads element 0: copy first
+                rs[j] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, word), (f16x2){1.0f16, 1.0f16}, rs[j], false);
+              }
+            }
+          }
 #pragma unroll
           for (int t = 0; t < FN; ++t) {
             const u32x2 raw = *(const u32x2*)(wb + (wn * FN + t) * 1024 + lane * 16 + s2 * 8);
             V wf0, wf1;
-            Op::wconv((u32x4){raw.x, raw.y, 0u, 0u}, wf0, wf1);
+            if constexpr (OFS)
+              wf0 = u8x8_to_f16_sub(raw.x, raw.y);
+            else
+              Op::wconv((u32x4){raw.x, raw.y, 0u, 0u}, wf0, wf1);
 #pragma unroll
             for (int b = 0; b < FM; ++b) acc[t][b] = Op::mma(wf0, xf[b], acc[t][b]);
           }
@@ -421,6 +479,16 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
     // reads of this stage have returned (their MFMAs consumed them).
   }
 
+  if constexpr (RSK) {
+    // sum the 4 K-column groups of each row, then publish the block's row sums
+#pragma unroll
+    for (int j = 0; j < RF; ++j) {
+      rs[j] += __shfl_xor(rs[j], 16);
+      rs[j] += __shfl_xor(rs[j], 32);
+      if (g == 0) rsum_lds[kg * BM + wm * TM + (wn + j * WN) * 16 + r] = rs[j];
+    }
+    if constexpr (KG == 1) __syncthreads();  // every stage has landed: the fence costs nothing here
+  }
   if constexpr (KG > 1) {
     barrier_nofence();  // every group is done with its stages before they become the reduction buffer
     Acc* red = (Acc*)lds;
@@ -447,6 +515,20 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
     sx = a.qpbuf[0];
     corr = 128 - __float_as_int(a.qpbuf[1]);
   }
+  // OFS: acc = 2^-24 * sum (q + 128) x, so y = (acc - 2^-17 * rowsum) * (scale * 2^24)
+  float rc[FM];
+#pragma unroll
+  for (int b = 0; b < FM; ++b) {
+    rc[b] = 0.0f;
+    if constexpr (RSK) {
+      float t2 = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KG; ++k) t2 += rsum_lds[k * BM + wm * TM + b * 16 + r];
+      rc[b] = t2 * 0x1p-17f;
+    } else if constexpr (OFS) {
+      rc[b] = a.rsum[min(m0 + wm * TM + b * 16 + r, M - 1)] * 0x1p-17f;
+    }
+  }
 #pragma unroll
   for (int t = 0; t < FN; ++t) {
     const int n = (nt0 + wn * FN + t) * 16 + 4 * g;
@@ -457,7 +539,7 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int nn = min(n + v, a.N - 1);
-      sc[v] = I8 ? sx * a.scale[nn] : a.scale[nn];
+      sc[v] = I8 ? sx * a.scale[nn] : (OFS ? a.scale[nn] * 0x1p24f : a.scale[nn]);
       bi[v] = a.bias ? a.bias[nn] : 0.0f;
       cs[v] = I8 ? a.colsum[nn] : 0;
     }
@@ -473,7 +555,7 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
           if (a.acc_out && v < nvalid) a.acc_out[(int64_t)m * a.N + n + v] = av;
           o[v] = a.bias ? __builtin_fmaf((float)av, sc[v], bi[v]) : (float)av * sc[v];
         } else {
-          float out = acc[t][b][v] * sc[v];
+          float out = (OFS ? acc[t][b][v] - rc[b] : acc[t][b][v]) * sc[v];
           if (a.bias) out = out + bi[v];
           o[v] = out;
         }
@@ -483,10 +565,10 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   }
 }
 
-template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG>
+template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false>
 int launch_dl(const GemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((a.Nt + BN / 16 - 1) / (BN / 16)), (unsigned)((a.M + BM - 1) / BM));
-  hipLaunchKernelGGL((gemm_dl_kernel<I8, XT, BN, BM, WN, WM, NS, KG>), grid, dim3(KG * WN * WM * 64), 0, st, a);
+  hipLaunchKernelGGL((gemm_dl_kernel<I8, XT, BN, BM, WN, WM, NS, KG, RSP>), grid, dim3(KG * WN * WM * 64), 0, st, a);
   return check_launch();
 }
 
@@ -557,19 +639,36 @@ int launch_dl_id(int id, const GemmArgs& a, hipStream_t st) {
   return -1;
 }
 
+// fp16 W-only with precomputed row sums: the configurations pick_gemm_dl
+// chooses for W-only (the others run with the sums accumulated in the loop).
+int launch_dl_rsp(int id, const GemmArgs& a, hipStream_t st) {
+  switch (id) {
+    case 0: return launch_dl<false, XT_F16, 256, 128, 4, 2, 2, 1, true>(a, st);
+    case 2: return launch_dl<false, XT_F16, 128, 128, 2, 2, 2, 1, true>(a, st);
+    case 5: return launch_dl<false, XT_F16, 128, 64, 2, 2, 2, 4, true>(a, st);
+    case 8: return launch_dl<false, XT_F16, 64, 64, 1, 2, 2, 4, true>(a, st);
+    case 10: return launch_dl<false, XT_F16, 256, 128, 4, 1, 2, 1, true>(a, st);
+  }
+  GemmArgs b = a;
+  b.rsum = nullptr;
+  return launch_dl_id<false, XT_F16>(id, b, st);
+}
+
 // Launch of direct-to-LDS configuration `id` (tuning entry; -1: no such id).
 int launch_gemm_dl_cfg(int id, bool i8, int xt, const GemmArgs& a, hipStream_t st) {
   if (i8) return launch_dl_id<true, XT_F16>(id, a, st);
-  if (xt == XT_F16) return launch_dl_id<false, XT_F16>(id, a, st);
+  if (xt == XT_F16) return a.rsum ? launch_dl_rsp(id, a, st) : launch_dl_id<false, XT_F16>(id, a, st);
   if (xt == XT_BF16) return launch_dl_id<false, XT_BF16>(id, a, st);
   return -2;
 }
 
 // Configuration for a shape (measured on MI355X, K = 4096, M 128..8192,
-// N 1024..12288): big grids take 256 x 128 blocks (W8A8 also 128 x 128 for
-// mid-size grids); grids that leave CUs short of waves take 128 x 64 or
-// 64 x 64 blocks with K split over 4 wave groups inside the workgroup.
-int pick_gemm_dl(bool i8, int64_t M, int64_t Nt) {
+// N 1024..24576): big grids take 256 x 128 blocks (W8A8 and fp16 also
+// 128 x 128 for mid-size grids); grids that leave CUs short of waves take
+// 128 x 64 or 64 x 64 blocks with K split over 4 wave groups inside the
+// workgroup.  bf16 W-only keeps 64 x 128 wave tiles on the largest grids
+// (half the conversion work per MFMA).
+int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt) {
   const int64_t t256 = ((Nt + 15) / 16) * ((M + 127) / 128);
   const int64_t t128 = ((Nt + 7) / 8) * ((M + 127) / 128);
   const int64_t t128x64 = ((Nt + 7) / 8) * ((M + 63) / 64);
@@ -579,7 +678,13 @@ int pick_gemm_dl(bool i8, int64_t M, int64_t Nt) {
     if (t128x64 >= 256) return 5;
     return 8;
   }
-  if (t256 >= 1536) return 10;  // 64 x 128 wave tiles: half the conversion work per MFMA
+  if (xt == XT_F16) {
+    if (t256 >= 384) return 0;
+    if (t128 >= 256) return 2;
+    if (t128x64 >= 128) return 5;
+    return 8;
+  }
+  if (t256 >= 1536) return 10;
   if (t256 >= 256 || t128x64 >= 512) return 0;
   if (t128x64 >= 128) return 5;
   return 8;
@@ -591,16 +696,22 @@ int pick_gemm_dl(bool i8, int64_t M, int64_t Nt) {
 constexpr int kBN = 128, kBM = 128, kWN = 2, kWM = 2;
 
 int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
-                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
-                   bool yvec) {
+                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, float* rsum,
+                   hipStream_t st, bool yvec) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
   const int flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
-  if (xvec && K % 64 == 0 && xt != XT_F32) {
+  // the direct-to-LDS path addresses a block's rows and tiles with 32-bit offsets
+  if (xvec && K % 64 == 0 && xt != XT_F32 && ldx <= ((int64_t)1 << 21) && K <= ((int64_t)1 << 21)) {
     GemmArgs a{};
     a.x = x; a.ldx = ldx; a.M = (int)M; a.Kc = (int)Kc;
     a.packed = packed; a.scale = scale; a.bias = bias;
     a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.flags = flags;
-    return launch_gemm_dl_cfg(pick_gemm_dl(false, M, Nt), false, xt, a, st);
+    if (xt == XT_F16 && rsum) {
+      const int rc = launch_rowsum_f16(x, ldx, M, K, rsum, st);
+      if (rc) return rc;
+      a.rsum = rsum;
+    }
+    return launch_gemm_dl_cfg(pick_gemm_dl(false, xt, M, Nt), false, xt, a, st);
   }
   dim3 grid((unsigned)((Nt + kBN / 16 - 1) / (kBN / 16)), (unsigned)((M + kBM - 1) / kBM)), block(kWN * kWM * 64);
   switch (xt) {
@@ -617,6 +728,7 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
                      int64_t ldy, int32_t* acc_out, float2* partials, int8_t* xq, float* qpbuf, hipStream_t st,
                      bool yvec) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64, Kp = Kc * 64;
+  if (Kp > ((int64_t)1 << 21)) return -1;  // 32-bit block offsets of the direct-to-LDS GEMM
   const int nparts = minmax_nparts(M, K);
   const int prc = launch_minmax_partials(x, xt, M, K, ldx, partials, nparts, st);
   if (prc) return prc;
@@ -636,7 +748,7 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
   a.packed = packed; a.scale = scale; a.bias = bias; a.colsum = colsum;
   a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.acc_out = acc_out; a.qpbuf = qpbuf;
   a.flags = flags;
-  return launch_gemm_dl_cfg(pick_gemm_dl(true, M, Nt), true, XT_F16, a, st);
+  return launch_gemm_dl_cfg(pick_gemm_dl(true, XT_F16, M, Nt), true, XT_F16, a, st);
 }
 
 }  // namespace sbq

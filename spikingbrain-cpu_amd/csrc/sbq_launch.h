@@ -39,9 +39,13 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
 int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                    const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
                    bool yvec);
+// rsum: device scratch of M floats (nullable).  With fp16 x it receives the
+// per-row sums of x from a pre-pass, which the GEMM then skips.
 int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
-                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
-                   bool yvec);
+                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, float* rsum,
+                   hipStream_t st, bool yvec);
+// Per-row sums in fp32 of fp16 x [M, K] (K % 8 == 0, 16-byte aligned rows).
+int launch_rowsum_f16(const void* x, int64_t ldx, int64_t M, int64_t K, float* out, hipStream_t st);
 
 // W8A8 (fbgemm dynamic semantics).  Both launch the activation min/max
 // pre-pass into `partials` (>= kMinMaxPartials float2) when they need it (the

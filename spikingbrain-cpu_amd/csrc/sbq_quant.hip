@@ -152,6 +152,31 @@ __device__ __forceinline__ void arg_take(float v, int i, float& bv, int& bi) {
   }
 }
 
+// Per-row sums of fp16 activations in fp32 (the offset the prefill GEMM's
+// subnormal weight encoding adds: sum_k (q + 128) x_k = sum_k q x_k + 128 * rowsum).
+// One wave per row, 16-byte loads, two accumulators; rows are 16-byte aligned
+// and K % 8 == 0 on this path.
+__global__ __launch_bounds__(256) void rowsum_f16_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, int K,
+                                                         float* __restrict__ out) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const _Float16* p = x + (int64_t)row * ldx;
+  float s0 = 0.0f, s1 = 0.0f;
+  for (int k = lane * 8; k < K; k += 512) {
+    const u32x4 v = *(const u32x4*)(p + k);
+    const uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
+    const f16x2 one = {1.0f16, 1.0f16};
+    s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w0), one, s0, false);
+    s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w1), one, s1, false);
+    s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one, s0, false);
+    s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w3), one, s1, false);
+  }
+  float s = s0 + s1;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if (lane == 0) out[row] = s;
+}
+
 // One workgroup per row; each thread keeps four independent running bests so
 // that four vector loads are in flight at a time.
 __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restrict__ y, int N, int64_t ldy,
@@ -264,6 +289,12 @@ int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t 
 
 int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t* zp_out, hipStream_t st) {
   hipLaunchKernelGGL(qparams_kernel, dim3(1), dim3(256), 0, st, partials, nparts, scale_out, zp_out);
+  return check_launch();
+}
+
+int launch_rowsum_f16(const void* x, int64_t ldx, int64_t M, int64_t K, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(rowsum_f16_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, (const _Float16*)x, ldx, (int)M,
+                     (int)K, out);
   return check_launch();
 }
 

@@ -118,16 +118,28 @@ def unpack(packed: torch.Tensor, N: int, K: int) -> torch.Tensor:
     return q
 
 
+def w8_workspace(M: int, K: int, device: torch.device) -> torch.Tensor:
+    n = _lib.load().sbq_w8_workspace_bytes(M, K)
+    return torch.empty((n,), dtype=torch.uint8, device=device)
+
+
 def linear_w8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None, N: int,
-              out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None) -> torch.Tensor:
-    """y = (x2 @ q^T) * scale (+ bias) for x2 [M, K] on the GPU."""
+              out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None,
+              workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """y = (x2 @ q^T) * scale (+ bias) for x2 [M, K] on the GPU.
+
+    fp16 prefill inputs (M > 32) get a small row-sum scratch (M floats) unless
+    the caller passes one; the library itself never allocates."""
     x2 = _as_activation(x2)
     M, K = x2.shape
     y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x2.device)
+    ws = workspace
+    if ws is None and x2.dtype == torch.float16 and M > 16:  # decode sizes run the GEMV, which needs none
+        ws = w8_workspace(M, K, x2.device)
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
                                              _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype), y.stride(0),
-                                             None, 0, _stream(x2.device)),
+                                             _ptr(ws), 0 if ws is None else ws.numel(), _stream(x2.device)),
                    "sbq_linear_w8")
     return y
 
