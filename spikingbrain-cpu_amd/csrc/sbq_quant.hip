@@ -154,23 +154,32 @@ __device__ __forceinline__ void arg_take(float v, int i, float& bv, int& bi) {
 
 // Per-row sums of fp16 activations in fp32 (the offset the prefill GEMM's
 // subnormal weight encoding adds: sum_k (q + 128) x_k = sum_k q x_k + 128 * rowsum).
-// One wave per row, 16-byte loads, two accumulators; rows are 16-byte aligned
-// and K % 8 == 0 on this path.
+// One wave per row, 16-byte loads (four in flight per lane), two accumulators;
+// rows are 16-byte aligned and K % 8 == 0 on this path.
+__device__ __forceinline__ void rowsum_acc(u32x4 v, float& s0, float& s1) {
+  const uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
+  const f16x2 one = {1.0f16, 1.0f16};
+  s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w0), one, s0, false);
+  s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w1), one, s1, false);
+  s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one, s0, false);
+  s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w3), one, s1, false);
+}
+
 __global__ __launch_bounds__(256) void rowsum_f16_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, int K,
                                                          float* __restrict__ out) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= M) return;
   const _Float16* p = x + (int64_t)row * ldx;
   float s0 = 0.0f, s1 = 0.0f;
-  for (int k = lane * 8; k < K; k += 512) {
-    const u32x4 v = *(const u32x4*)(p + k);
-    const uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
-    const f16x2 one = {1.0f16, 1.0f16};
-    s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w0), one, s0, false);
-    s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w1), one, s1, false);
-    s0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w2), one, s0, false);
-    s1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w3), one, s1, false);
+  int k = lane * 8;
+  for (; k + 3 * 512 < K; k += 4 * 512) {
+    u32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = *(const u32x4*)(p + k + j * 512);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rowsum_acc(v[j], s0, s1);
   }
+  for (; k < K; k += 512) rowsum_acc(*(const u32x4*)(p + k), s0, s1);
   float s = s0 + s1;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
