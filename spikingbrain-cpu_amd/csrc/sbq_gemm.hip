@@ -6,12 +6,15 @@
 //
 // Block tile BN (output channels) x BM (tokens) x 64 (K per stage), WN x WM
 // waves.  Each stage copies BN/16 packed weight tiles verbatim into LDS and the
-// BM x 64 activation slab into an XOR-swizzled LDS tile; the next stage is
-// prefetched into registers while MFMAs run on the current one (two LDS
-// buffers, one barrier per stage).
-//   W-only: weights are converted int8 -> fp16/bf16 in registers (exact) and
-//           multiplied on v_mfma_f32_16x16x32_{f16,bf16}; fp32 activations run
-//           as bf16 hi + lo planes.  Epilogue: * scale[n] (+ bias[n]).
+// BM x 64 activation slab into an XOR-swizzled LDS tile, straight from global
+// memory (LDS DMA); later stages land while MFMAs run on the current one (one
+// barrier per stage).
+//   W-only: fp16 activations meet the weights as fp16 subnormals
+//           (q + 128) * 2^-24 (one v_perm per pair) and the epilogue removes
+//           128 * rowsum(x); bf16 activations meet exact bf16 weights.  Both
+//           run v_mfma_f32_16x16x32_{f16,bf16}; fp32 activations run as bf16
+//           hi + lo planes (register-staged kernel).  Epilogue: * scale[n]
+//           (+ bias[n]).
 //   W8A8:   the activations are quantized to s8 (xq - 128) once, by a
 //           pre-pass into the workspace; weights are used as s8,
 //           v_mfma_i32_16x16x64_i8 accumulates exactly; the epilogue adds
