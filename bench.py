@@ -203,7 +203,7 @@ def prefill_bench(ctx, M, N=12288, K=4096, steps=10, warmup=3):
     packed, s, _ = ctx.weights(N, K, 900)
     x = ctx.act(M, K, 901)
     y = ctx.torch.empty((M, N), dtype=ctx.torch.float16, device=ctx.dev)
-    ws = quant.w8_workspace(M, K, ctx.dev)  # row-sum scratch: the pre-pass is part of each timed step
+    ws = quant.w8_workspace(M, K, ctx.dev, x.dtype)  # row-sum scratch: the pre-pass is part of each timed step
     ms = ctx.time_steps(lambda c: quant.linear_w8(x, packed, s, None, N, out=y, workspace=ws), 1, steps, warmup)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     return {"M": M, "N": N, "K": K, "ms": ms, "TFLOPs": tflops, "mfma_frac": tflops / F16_PEAK_TFLOPS}
@@ -326,7 +326,7 @@ def prefill_probe(ctx, M=2048, N=12288, K=4096, launches=4):
     packed, s, _ = ctx.weights(N, K, 900)
     x = ctx.act(M, K, 901)
     y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
-    ws = quant.w8_workspace(M, K, ctx.dev)
+    ws = quant.w8_workspace(M, K, ctx.dev, x.dtype)
     torch.cuda.synchronize()
     for _ in range(launches):
         quant.linear_w8(x, packed, s, None, N, out=y, workspace=ws)

@@ -107,19 +107,23 @@ int sbq_unpack_w8(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_
  * or NULL.  y: device [M, N] (row stride ldy), dtype F32, F16 or BF16.
  * Accumulation is fp32.  M <= 32 runs the HBM-streaming MFMA GEMV; larger M
  * runs the LDS-tiled MFMA GEMM.
- * workspace: optional (NULL, 0 is valid).  With >= sbq_w8_workspace_bytes(M, K)
- * bytes, the F16 prefill GEMM takes its per-row activation sums from a
- * pre-pass instead of accumulating them in its K loop (faster; results agree
- * to fp32 rounding).  Other dtypes and the GEMV ignore it. */
+ * workspace: optional (NULL, 0 is valid).  With >= sbq_w8_workspace_bytes(M,
+ * K, x_dtype) bytes the prefill GEMM (M > 32, K % 64 == 0, aligned rows) runs
+ * its fastest path: F16 x with per-row sums from a pre-pass; BF16 / F32 x
+ * staged as power-of-two scaled fp16 planes (BF16: exact; F32: hi + lo, 22
+ * significant bits) for the same fp16 MFMA kernel.  Without it, F16 / BF16 run
+ * a slower tiled GEMM and F32 the register-staged bf16 hi + lo GEMM. */
 int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   const uint8_t* packed, const float* scale, const float* bias, int64_t N,
                   void* y, int y_dtype, int64_t ldy,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes that let sbq_linear_w8 run its fast fp16 prefill path for
- * an [M, K] input: M floats plus alignment slack.  No counterpart in the
- * reference (its CPU matmul needs no scratch). */
-int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K);
+/* Workspace bytes that let sbq_linear_w8 run its fastest prefill path for an
+ * [M, K] input of x_dtype: 2 * M floats (F16), plus M * K * 2 bytes (BF16) or
+ * M * K * 4 bytes (F32) of staged activations, plus alignment slack.  0 for a
+ * bad argument.  No counterpart in the reference (its CPU matmul needs no
+ * scratch). */
+int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K, int x_dtype);
 
 /* ---- int8-dyn W8A8 linear (DynamicInt8Linear.forward, quant.py:63-66) ---- */
 

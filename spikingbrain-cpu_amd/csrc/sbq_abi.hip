@@ -104,10 +104,9 @@ int sbq_unpack_w8(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_
   return sbq::launch_unpack(packed, N, K, q, ldq, (hipStream_t)stream);
 }
 
-int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K) {
-  (void)K;
-  if (M < 0) return 0;
-  return 256 + ((M * 4 + 255) & ~(int64_t)255);
+int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K, int x_dtype) {
+  if (M < 0 || K < 0 || M > kIntMax || K > kIntMax || !valid_dtype(x_dtype)) return 0;
+  return 256 + sbq::w8_ws_layout(M, ((K + 63) / 64) * 64, x_dtype).bytes;
 }
 
 int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
@@ -118,11 +117,15 @@ int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
   const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
   hipStream_t st = (hipStream_t)stream;
   if (sbq::gemv_supports(M, K, false, x_dtype)) return sbq::launch_gemv_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
-  // optional: row-sum scratch for the fp16 prefill GEMM (256-byte aligned)
-  float* rsum = nullptr;
-  if (workspace && (int64_t)workspace_bytes >= sbq_w8_workspace_bytes(M, K))
-    rsum = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
-  return sbq::launch_gemm_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, rsum, st, yv);
+  // optional scratch of the prefill GEMM (row sums, staged activations), 256-byte aligned
+  void* ws = nullptr;
+  int64_t ws_bytes = 0;
+  if (workspace && (int64_t)workspace_bytes >= sbq_w8_workspace_bytes(M, K, x_dtype)) {
+    ws = (void*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+    ws_bytes = (int64_t)workspace_bytes - (int64_t)((uintptr_t)ws - (uintptr_t)workspace);
+  }
+  return sbq::launch_gemm_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, ws, ws_bytes, st,
+                             yv);
 }
 
 int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K) {

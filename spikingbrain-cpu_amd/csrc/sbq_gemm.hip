@@ -316,6 +316,8 @@ struct GemmArgs {
   int32_t* acc_out;     // I8 only, may be null
   const float* qpbuf;   // I8 only: (s_x, zp as int bits)
   const float* rsum;    // fp16 W-only with RSP: per-row sums of x [M]
+  const float* rscale;  // fp16 W-only with RSP, nullable: per-row output scale [M]
+  int kx;               // activation K tiles (0: Kc); 2 * Kc = two planes over the same weights
   int flags;            // bit 1: y rows 4-element vector stores
 };
 
@@ -365,9 +367,10 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   const int wn = w / WM, wm = w % WM;
   const int nt0 = blockIdx.x * WT, m0 = blockIdx.y * BM;
   const int M = a.M, Kc = a.Kc, Nt = a.Nt;
-  const int KW = (Kc + KG - 1) / KG;
+  const int KX = a.kx > 0 ? a.kx : Kc;  // activation K tiles: x tile kc meets weight tile kc mod Kc
+  const int KW = (KX + KG - 1) / KG;
   const int kbeg = kg * KW;
-  const int cnt = min(KW, Kc - kbeg);  // tiles of this group (<= 0: none)
+  const int cnt = min(KW, KX - kbeg);  // tiles of this group (<= 0: none)
   const uint8_t* xg = (const uint8_t*)a.x;
   const int64_t xrow = I8 ? a.ldx : a.ldx * 2;  // bytes per activation row
 
@@ -404,10 +407,11 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   const int xslot = __builtin_amdgcn_readfirstlane(WBYTES + w * (XR / GW) * 1024);
   auto issue = [&](int i, int st) {
     // clamped: the surplus stages of a short last group are never multiplied
-    const int kc = KG == 1 ? i : max(0, min(kbeg + min(i, cnt - 1), Kc - 1));
+    const int kc = KG == 1 ? i : max(0, min(kbeg + min(i, cnt - 1), KX - 1));
+    const int kw = kc >= Kc ? kc - Kc : kc;
     const int sb = __builtin_amdgcn_readfirstlane((kg * NS + st) * STAGE);
 #pragma unroll
-    for (int i2 = 0; i2 < WT / GW; ++i2) lds_dma16_buf(wrs, woff[i2], kc * 1024, lds + sb + wslot + i2 * 1024);
+    for (int i2 = 0; i2 < WT / GW; ++i2) lds_dma16_buf(wrs, woff[i2], kw * 1024, lds + sb + wslot + i2 * 1024);
 #pragma unroll
     for (int i2 = 0; i2 < XR / GW; ++i2)
       lds_dma16_buf(xrs, xoff[i2], kc * (I8 ? 64 : 128), lds + sb + xslot + i2 * 1024);
@@ -519,10 +523,14 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
     corr = 128 - __float_as_int(a.qpbuf[1]);
   }
   // OFS: acc = 2^-24 * sum (q + 128) x, so y = (acc - 2^-17 * rowsum) * (scale * 2^24)
-  float rc[FM];
+  // (* rscale[m] for staged fp32 / bf16 activations)
+  float rc[FM], rf[FM];
 #pragma unroll
   for (int b = 0; b < FM; ++b) {
     rc[b] = 0.0f;
+    rf[b] = 1.0f;
+    if constexpr (RSP)
+      if (a.rscale) rf[b] = a.rscale[min(m0 + wm * TM + b * 16 + r, M - 1)];
     if constexpr (RSK) {
       float t2 = 0.0f;
 #pragma unroll
@@ -558,7 +566,7 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
           if (a.acc_out && v < nvalid) a.acc_out[(int64_t)m * a.N + n + v] = av;
           o[v] = a.bias ? __builtin_fmaf((float)av, sc[v], bi[v]) : (float)av * sc[v];
         } else {
-          float out = (OFS ? acc[t][b][v] - rc[b] : acc[t][b][v]) * sc[v];
+          float out = OFS ? ((acc[t][b][v] - rc[b]) * sc[v]) * rf[b] : acc[t][b][v] * sc[v];
           if (a.bias) out = out + bi[v];
           o[v] = out;
         }
@@ -652,6 +660,7 @@ int launch_dl_rsp(int id, const GemmArgs& a, hipStream_t st) {
     case 8: return launch_dl<false, XT_F16, 64, 64, 1, 2, 2, 4, true>(a, st);
     case 10: return launch_dl<false, XT_F16, 256, 128, 4, 1, 2, 1, true>(a, st);
   }
+  if (a.rscale) return -1;  // staged activations need the row scale: only the configurations above apply it
   GemmArgs b = a;
   b.rsum = nullptr;
   return launch_dl_id<false, XT_F16>(id, b, st);
@@ -698,23 +707,52 @@ int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt) {
 // ---------------------------------------------------------------------------
 constexpr int kBN = 128, kBM = 128, kWN = 2, kWM = 2;
 
+W8Ws w8_ws_layout(int64_t M, int64_t K, int xt) {
+  auto r256 = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+  const int np = xt == XT_F32 ? 2 : (xt == XT_BF16 ? 1 : 0);
+  W8Ws l;
+  l.rowsum = 0;
+  l.rscale = r256(M * 4);
+  l.planes = l.rscale + r256(M * 4);
+  l.bytes = l.planes + r256(M * np * K * 2);
+  return l;
+}
+
 int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
-                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, float* rsum,
-                   hipStream_t st, bool yvec) {
+                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, void* ws,
+                   int64_t ws_bytes, hipStream_t st, bool yvec) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
   const int flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
   // the direct-to-LDS path addresses a block's rows and tiles with 32-bit offsets
-  if (xvec && K % 64 == 0 && xt != XT_F32 && ldx <= ((int64_t)1 << 21) && K <= ((int64_t)1 << 21)) {
+  const bool dl = xvec && K % 64 == 0 && ldx <= ((int64_t)1 << 21) && K <= ((int64_t)1 << 21);
+  const W8Ws l = w8_ws_layout(M, K, xt);
+  const bool staged = dl && ws && ws_bytes >= l.bytes;
+  if (dl && (xt != XT_F32 || staged)) {
     GemmArgs a{};
     a.x = x; a.ldx = ldx; a.M = (int)M; a.Kc = (int)Kc;
     a.packed = packed; a.scale = scale; a.bias = bias;
     a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.flags = flags;
-    if (xt == XT_F16 && rsum) {
-      const int rc = launch_rowsum_f16(x, ldx, M, K, rsum, st);
-      if (rc) return rc;
-      a.rsum = rsum;
+    int gxt = xt;
+    if (staged) {
+      uint8_t* w = (uint8_t*)ws;
+      float* rowsum = (float*)(w + l.rowsum);
+      a.rsum = rowsum;
+      if (xt == XT_F16) {
+        const int rc = launch_rowsum_f16(x, ldx, M, K, rowsum, st);
+        if (rc) return rc;
+      } else {
+        // fp32 / bf16: scaled fp16 planes [hi | lo] per row, then the fp16 GEMM
+        const int np = xt == XT_F32 ? 2 : 1;
+        _Float16* planes = (_Float16*)(w + l.planes);
+        float* rscale = (float*)(w + l.rscale);
+        const int rc = launch_stage_act(x, xt, ldx, M, K, planes, rowsum, rscale, st);
+        if (rc) return rc;
+        a.x = planes; a.ldx = np * K; a.kx = (int)(np * Kc); a.rscale = rscale;
+        a.flags = flags | 1;
+        gxt = XT_F16;
+      }
     }
-    return launch_gemm_dl_cfg(pick_gemm_dl(false, xt, M, Nt), false, xt, a, st);
+    return launch_gemm_dl_cfg(pick_gemm_dl(false, gxt, M, Nt), false, gxt, a, st);
   }
   dim3 grid((unsigned)((Nt + kBN / 16 - 1) / (kBN / 16)), (unsigned)((M + kBM - 1) / kBM)), block(kWN * kWM * 64);
   switch (xt) {

@@ -39,13 +39,24 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
 int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                    const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
                    bool yvec);
-// rsum: device scratch of M floats (nullable).  With fp16 x it receives the
-// per-row sums of x from a pre-pass, which the GEMM then skips.
+// ws: device scratch (nullable, 256-byte aligned) of ws_bytes bytes, laid out
+// by w8_ws_layout.  With enough of it the fp16 GEMM takes its per-row sums of x
+// from a pre-pass, and fp32 / bf16 activations are staged as scaled fp16 planes
+// for the same GEMM.
 int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
-                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, float* rsum,
-                   hipStream_t st, bool yvec);
+                   const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, void* ws,
+                   int64_t ws_bytes, hipStream_t st, bool yvec);
+// W-only prefill scratch: [rowsum: M floats][rscale: M floats][fp16 planes: M x NP x K],
+// each part 256-byte aligned; NP = 2 for fp32 x, 1 for bf16, 0 for fp16.
+struct W8Ws {
+  int64_t rowsum, rscale, planes, bytes;
+};
+W8Ws w8_ws_layout(int64_t M, int64_t K, int xt);
 // Per-row sums in fp32 of fp16 x [M, K] (K % 8 == 0, 16-byte aligned rows).
 int launch_rowsum_f16(const void* x, int64_t ldx, int64_t M, int64_t K, float* out, hipStream_t st);
+// fp32 / bf16 x [M, K] -> scaled fp16 planes, row sums and row scales.
+int launch_stage_act(const void* x, int xt, int64_t ldx, int64_t M, int64_t K, _Float16* xs, float* rowsum,
+                     float* rscale, hipStream_t st);
 
 // W8A8 (fbgemm dynamic semantics).  Both launch the activation min/max
 // pre-pass into `partials` (>= kMinMaxPartials float2) when they need it (the

@@ -186,6 +186,61 @@ __global__ __launch_bounds__(256) void rowsum_f16_kernel(const _Float16* __restr
   if (lane == 0) out[row] = s;
 }
 
+// fp32 / bf16 activations -> power-of-two scaled fp16 planes for the fp16
+// prefill GEMM.  Row m is scaled by 2^e (max|x| * 2^e in [2^14, 2^15), an
+// exact scaling); plane 0 is hi = rn16(x * 2^e), plane 1 (fp32 only) is
+// lo = rn16(x * 2^e - hi).  bf16 values (8 significant bits) are exact in
+// plane 0 down to 2^28 below the row maximum; fp32 values keep 22 bits.
+// Output row m: [hi (K) | lo (K)] fp16 at xs + m * NP * K; rowsum[m] = the fp32
+// sum of every plane's fp16 values; rscale[m] = 2^-e.  One wave per row; rows
+// are 16-byte aligned and K % 64 == 0 on this path.
+template <int XT, int NP>
+__global__ __launch_bounds__(256) void stage_act_kernel(const void* __restrict__ xv, int64_t ldx, int M, int K,
+                                                        _Float16* __restrict__ xs, float* __restrict__ rowsum,
+                                                        float* __restrict__ rscale) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  float mx = 0.0f;
+  for (int k = lane * 8; k < K; k += 512) {
+    float t[8];
+    load8_f32<XT>(xv, ldx, M, K, row, k, true, t);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(t[j]));
+  }
+  mx = wave_max(mx);
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.4028235e38f) {
+    int ex;
+    (void)frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+    e = min(max(15 - ex, -112), 120);
+  }
+  const float sc = ldexpf(1.0f, e);
+  _Float16* out = xs + (int64_t)row * NP * K;
+  float s0 = 0.0f, s1 = 0.0f;
+  for (int k = lane * 8; k < K; k += 512) {
+    float t[8];
+    load8_f32<XT>(xv, ldx, M, K, row, k, true, t);
+    f16x8 hi, lo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = t[j] * sc;
+      hi[j] = (_Float16)v;
+      lo[j] = (_Float16)(v - (float)hi[j]);
+      s0 += (float)hi[j];
+      if constexpr (NP == 2) s1 += (float)lo[j];
+    }
+    *(f16x8*)(out + k) = hi;
+    if constexpr (NP == 2) *(f16x8*)(out + K + k) = lo;
+  }
+  float s = s0 + s1;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if (lane == 0) {
+    rowsum[row] = s;
+    rscale[row] = ldexpf(1.0f, -e);
+  }
+}
+
 // One workgroup per row; each thread keeps four independent running bests so
 // that four vector loads are in flight at a time.
 __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restrict__ y, int N, int64_t ldy,
@@ -304,6 +359,18 @@ int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t
 int launch_rowsum_f16(const void* x, int64_t ldx, int64_t M, int64_t K, float* out, hipStream_t st) {
   hipLaunchKernelGGL(rowsum_f16_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, (const _Float16*)x, ldx, (int)M,
                      (int)K, out);
+  return check_launch();
+}
+
+int launch_stage_act(const void* x, int xt, int64_t ldx, int64_t M, int64_t K, _Float16* xs, float* rowsum,
+                     float* rscale, hipStream_t st) {
+  const dim3 grid((unsigned)((M + 3) / 4)), block(256);
+  if (xt == XT_F32)
+    hipLaunchKernelGGL((stage_act_kernel<XT_F32, 2>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale);
+  else if (xt == XT_BF16)
+    hipLaunchKernelGGL((stage_act_kernel<XT_BF16, 1>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale);
+  else
+    return -2;
   return check_launch();
 }
 

@@ -27,7 +27,7 @@ SIGNATURES = {
     "sbq_repack_w8": (_I, [_P, _L, _L, _L, _P, _P, _P]),
     "sbq_unpack_w8": (_I, [_P, _L, _L, _P, _L, _P]),
     "sbq_linear_w8": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _L, _P, _I, _L, _P, _S, _P]),
-    "sbq_w8_workspace_bytes": (_L, [_L, _L]),
+    "sbq_w8_workspace_bytes": (_L, [_L, _L, _I]),
     "sbq_w8a8_workspace_bytes": (_L, [_L, _L]),
     "sbq_act_qparams": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _S, _P]),
     "sbq_linear_w8a8": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _L, _P, _I, _L, _P, _P, _S, _P]),

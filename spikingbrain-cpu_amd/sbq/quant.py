@@ -118,8 +118,9 @@ def unpack(packed: torch.Tensor, N: int, K: int) -> torch.Tensor:
     return q
 
 
-def w8_workspace(M: int, K: int, device: torch.device) -> torch.Tensor:
-    n = _lib.load().sbq_w8_workspace_bytes(M, K)
+def w8_workspace(M: int, K: int, device: torch.device, dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """Scratch for linear_w8's prefill path with [M, K] activations of `dtype`."""
+    n = _lib.load().sbq_w8_workspace_bytes(M, K, _code(dtype))
     return torch.empty((n,), dtype=torch.uint8, device=device)
 
 
@@ -128,14 +129,15 @@ def linear_w8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias:
               workspace: torch.Tensor | None = None) -> torch.Tensor:
     """y = (x2 @ q^T) * scale (+ bias) for x2 [M, K] on the GPU.
 
-    fp16 prefill inputs (M > 32) get a small row-sum scratch (M floats) unless
-    the caller passes one; the library itself never allocates."""
+    Prefill-sized inputs (M > 16) get the scratch of the fastest GEMM path
+    (row sums; staged fp16 planes for fp32 / bf16 activations) unless the
+    caller passes one; the library itself never allocates."""
     x2 = _as_activation(x2)
     M, K = x2.shape
     y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x2.device)
     ws = workspace
-    if ws is None and x2.dtype == torch.float16 and M > 16:  # decode sizes run the GEMV, which needs none
-        ws = w8_workspace(M, K, x2.device)
+    if ws is None and M > 16:  # decode sizes run the GEMV, which needs none
+        ws = w8_workspace(M, K, x2.device, x2.dtype)
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
                                              _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype), y.stride(0),

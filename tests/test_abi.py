@@ -53,8 +53,11 @@ def test_packed_bytes(lib):
     assert lib.sbq_packed_bytes(13, 200) == 16 * 256
     assert lib.sbq_packed_bytes(0, 5) == 0
     assert lib.sbq_w8a8_workspace_bytes(1, 4096) >= 256 * 8
-    assert lib.sbq_w8_workspace_bytes(2048, 4096) >= 2048 * 4 + 255
-    assert lib.sbq_w8_workspace_bytes(-1, 4096) == 0
+    assert lib.sbq_w8_workspace_bytes(2048, 4096, 1) >= 2 * 2048 * 4 + 255  # fp16: row sums and scales
+    assert lib.sbq_w8_workspace_bytes(2048, 4096, 2) >= 2048 * 4096 * 2     # bf16: one staged plane
+    assert lib.sbq_w8_workspace_bytes(2048, 4096, 0) >= 2048 * 4096 * 4     # fp32: two staged planes
+    assert lib.sbq_w8_workspace_bytes(-1, 4096, 1) == 0
+    assert lib.sbq_w8_workspace_bytes(16, 64, 7) == 0
 
 
 def test_argument_validation_without_gpu(lib):

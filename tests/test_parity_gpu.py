@@ -150,6 +150,30 @@ def test_w8_f16_prefill_row_sum_paths(dev, M, N, K):
         assert e_pre <= bound and e_loop <= bound, (positive, e_pre, e_loop)
 
 
+@pytest.mark.parametrize("xd", ["f32", "bf16"])
+@pytest.mark.parametrize("M,N,K", [(64, 512, 2560), (200, 130, 4096), (512, 2048, 512), (300, 4096, 4096)])
+def test_w8_staged_prefill_rows(dev, M, N, K, xd):
+    """fp32 / bf16 prefill activations are staged as power-of-two scaled fp16
+    planes (fp32: hi + lo) for the fp16 GEMM when a workspace is given; rows
+    span 1e-30 .. 1e30, and each row must match the oracle on its own.  The
+    paths without a workspace are held to the same bar."""
+    announce(f"w8 staged M={M} N={N} K={K} x={xd}")
+    w = make_weights(N, K, 9000 + N + K)
+    q, s = oracle.quantize_per_channel(w.numpy())
+    lin = quant.Int8Linear(w, None)
+    mags = torch.pow(10.0, torch.linspace(-30.0, 30.0, M, dtype=torch.float64)).float()
+    x = (make_x(M, K, 9100 + M + K) * mags[:, None]).to(DT[xd])
+    ref = oracle.int8_linear(x.float().numpy(), q, s).astype(np.float64)
+    xd_dev = x.to(dev)
+    none = torch.empty(0, dtype=torch.uint8, device=dev)
+    for ws in (None, none):
+        y = quant.linear_w8(xd_dev, lin.packed, lin.scale, None, N, workspace=ws).cpu().numpy().astype(np.float64)
+        row_err = np.linalg.norm(y - ref, axis=1) / np.linalg.norm(ref, axis=1)
+        # staged fp32 keeps 22 significant bits, staged bf16 is exact: both far inside the tolerance
+        bar = (2e-5 if xd == "f32" else 2e-6) if ws is None else W8_TOL
+        assert row_err.max() <= bar, (ws is None, float(row_err.max()), int(row_err.argmax()))
+
+
 @pytest.mark.parametrize("yd", ["f16", "bf16"])
 @pytest.mark.parametrize("M", [1, 9, 100])
 def test_w8_low_precision_output(dev, M, yd):
