@@ -101,8 +101,11 @@ int sbq_unpack_w8(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_
 
 /* y[m,n] = (sum_k x[m,k] * q[n,k]) * scale[n] (+ bias[n])
  * x: device [M, K] (row stride ldx), dtype F32, F16 or BF16.
- *    F16/BF16 inputs are used exactly; F32 inputs are split into a bf16
- *    high part and a bf16 remainder (relative representation error <= 2^-16).
+ *    F16/BF16 inputs are used exactly (BF16 staged for the prefill GEMM: exact
+ *    down to 2^28 below each row's maximum).  F32 inputs are split into two
+ *    parts: fp16 hi + lo of the row scaled by a power of two on the staged
+ *    prefill path (22 significant bits), bf16 hi + remainder elsewhere
+ *    (relative representation error <= 2^-16).
  * packed: from sbq_repack_w8.  scale: device fp32 [N].  bias: device fp32 [N]
  * or NULL.  y: device [M, N] (row stride ldy), dtype F32, F16 or BF16.
  * Accumulation is fp32.  M <= 32 runs the HBM-streaming MFMA GEMV; larger M
