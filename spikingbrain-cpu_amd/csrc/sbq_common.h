@@ -259,6 +259,18 @@ __device__ __forceinline__ int quant_act_s8(float x, float inv, float zpf) {
   return (int)t - 128;
 }
 
+// Four pre-rounding values t = fma(x, inv, zp) -> four packed s8 (xq - 128).
+// v_cvt_pk_u8_f32 computes clamp(rint(t), 0, 255) (ties to even, NaN -> 0,
+// as quant_act_s8 does; checked on MI355X) and packs the byte; ^ 0x80 maps
+// u8 to s8 - 128 for four values at once.
+__device__ __forceinline__ uint32_t pack_act_s8x4(float t0, float t1, float t2, float t3) {
+  uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(t0, 0, 0u);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(t1, 1, w);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(t2, 2, w);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(t3, 3, w);
+  return w ^ 0x80808080u;
+}
+
 // Number of min/max partials the activation pre-pass writes (upper bound).
 constexpr int kMinMaxPartials = 256;
 

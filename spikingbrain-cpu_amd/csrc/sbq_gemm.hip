@@ -589,37 +589,77 @@ int launch_dl(const GemmArgs& a, hipStream_t st) {
 // meet zero weights); gemm_w8a8_dl_kernel then runs the direct-to-LDS
 // pipeline on s8 operands with v_mfma_i32_16x16x64_i8.
 // ---------------------------------------------------------------------------
-template <int XT>
+constexpr int kQuantChunks = 4;
+
+// VEC: 16-byte aligned rows and K % 16 == 0 (every chunk is whole, branch-free loads)
+template <int XT, bool VEC>
 __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restrict__ x, int64_t ldx, int M, int K,
                                                            int Kp, const float2* __restrict__ partials, int nparts,
                                                            int8_t* __restrict__ xq, float* __restrict__ qp_out,
                                                            int flags) {
+  // kQuantChunks 16-element chunks per thread, chunk i of the block at
+  // (block * kQuantChunks + i) * 256 + thread.  The activation loads go out
+  // first; the (latency-bound) reduction of the partials and fbgemm's
+  // double-precision parameter choice run while they are in flight.
+  const int cpr = Kp / 16;
+  const int64_t nch = (int64_t)M * cpr;
+  float t[kQuantChunks][16];
+  int64_t cc[kQuantChunks];
+#pragma unroll
+  for (int i = 0; i < kQuantChunks; ++i) {
+    cc[i] = ((int64_t)blockIdx.x * kQuantChunks + i) * blockDim.x + threadIdx.x;
+    const int64_t c = min(cc[i], nch - 1);  // clamped: surplus chunks are loaded but not stored
+    const int m = (int)(c / cpr), k0 = (int)(c - (int64_t)m * cpr) * 16;
+    if constexpr (VEC) {
+      typedef typename XElem<XT>::T T;
+      typedef T v8 __attribute__((ext_vector_type(8)));
+      const T* p = (const T*)x + (int64_t)m * ldx + k0;
+      if constexpr (XT == XT_F32) {
+        const f32x4 a0 = *(const f32x4*)p, a1 = *(const f32x4*)(p + 4);
+        const f32x4 a2 = *(const f32x4*)(p + 8), a3 = *(const f32x4*)(p + 12);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          t[i][j] = a0[j];
+          t[i][4 + j] = a1[j];
+          t[i][8 + j] = a2[j];
+          t[i][12 + j] = a3[j];
+        }
+      } else {
+        const v8 a0 = *(const v8*)p, a1 = *(const v8*)(p + 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          t[i][j] = XElem<XT>::to_f32(a0[j]);
+          t[i][8 + j] = XElem<XT>::to_f32(a1[j]);
+        }
+      }
+    } else {
+      load8_f32<XT>(x, ldx, M, K, m, k0, flags & 1, t[i]);
+      load8_f32<XT>(x, ldx, M, K, m, k0 + 8, flags & 1, t[i] + 8);
+    }
+  }
   __shared__ float red[16];
   const ActQParams qp = block_qparams_from_partials(partials, nparts, red);
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     qp_out[0] = qp.scale;
     qp_out[1] = __int_as_float(qp.zp);
   }
-  const int cpr = Kp / 16;
-  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= (int64_t)M * cpr) return;
-  const int m = (int)(c / cpr), k0 = (int)(c - (int64_t)m * cpr) * 16;
-  float t[16];
-  load8_f32<XT>(x, ldx, M, K, m, k0, flags & 1, t);
-  load8_f32<XT>(x, ldx, M, K, m, k0 + 8, flags & 1, t + 8);
-  uint32_t d[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t word = 0;
+  for (int i = 0; i < kQuantChunks; ++i) {
+    if (cc[i] >= nch) break;
+    const int m = (int)(cc[i] / cpr), k0 = (int)(cc[i] - (int64_t)m * cpr) * 16;
+    uint32_t d[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int jj = 4 * i + j;
-      const int qv = k0 + jj < K ? quant_act_s8(t[jj], qp.inv, qp.zpf) : 0;
-      word |= ((uint32_t)qv & 0xffu) << (8 * j);
+    for (int w = 0; w < 4; ++w) {
+      float u[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int jj = 4 * w + j;
+        u[j] = k0 + jj < K ? __builtin_fmaf(t[i][jj], qp.inv, qp.zpf) : 128.0f;  // padding columns: s8 0
+      }
+      d[w] = pack_act_s8x4(u[0], u[1], u[2], u[3]);
     }
-    d[i] = word;
+    *(u32x4*)(xq + (int64_t)m * Kp + k0) = (u32x4){d[0], d[1], d[2], d[3]};
   }
-  *(u32x4*)(xq + (int64_t)m * Kp + k0) = (u32x4){d[0], d[1], d[2], d[3]};
 }
 
 
@@ -775,13 +815,22 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
   if (prc) return prc;
   const int flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
   const int64_t chunks = M * (Kp / 16);
-  const dim3 qgrid((unsigned)((chunks + 255) / 256));
+  const dim3 qgrid((unsigned)((chunks + 256 * kQuantChunks - 1) / (256 * kQuantChunks)));
+  const bool qvec = xvec && K % 16 == 0;
+#define SBQ_QUANT_LAUNCH(XT_)                                                                                       \
+  if (qvec)                                                                                                           \
+    hipLaunchKernelGGL((quantize_act_kernel<XT_, true>), qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp,    \
+                       partials, nparts, xq, qpbuf, flags);                                                          \
+  else                                                                                                                \
+    hipLaunchKernelGGL((quantize_act_kernel<XT_, false>), qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp,   \
+                       partials, nparts, xq, qpbuf, flags);
   switch (xt) {
-    case XT_F16: hipLaunchKernelGGL(quantize_act_kernel<XT_F16>, qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp, partials, nparts, xq, qpbuf, flags); break;
-    case XT_BF16: hipLaunchKernelGGL(quantize_act_kernel<XT_BF16>, qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp, partials, nparts, xq, qpbuf, flags); break;
-    case XT_F32: hipLaunchKernelGGL(quantize_act_kernel<XT_F32>, qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp, partials, nparts, xq, qpbuf, flags); break;
+    case XT_F16: SBQ_QUANT_LAUNCH(XT_F16) break;
+    case XT_BF16: SBQ_QUANT_LAUNCH(XT_BF16) break;
+    case XT_F32: SBQ_QUANT_LAUNCH(XT_F32) break;
     default: return -2;
   }
+#undef SBQ_QUANT_LAUNCH
   int rc = check_launch();
   if (rc) return rc;
   GemmArgs a{};

@@ -80,12 +80,9 @@ template <int XT>
 __device__ __forceinline__ i32x4 quant16(const XRaw<XT>& f, float inv, float zpf) {
   uint32_t d[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) word |= ((uint32_t)quant_act_s8(f.get(4 * i + j), inv, zpf) & 0xffu) << (8 * j);
-    d[i] = word;
-  }
+  for (int i = 0; i < 4; ++i)
+    d[i] = pack_act_s8x4(__builtin_fmaf(f.get(4 * i), inv, zpf), __builtin_fmaf(f.get(4 * i + 1), inv, zpf),
+                         __builtin_fmaf(f.get(4 * i + 2), inv, zpf), __builtin_fmaf(f.get(4 * i + 3), inv, zpf));
   return (i32x4){(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
 }
 

@@ -167,14 +167,14 @@ __device__ __forceinline__ i32x4 quant_frag(const XRaw<XT>& x, int M, int K, int
   uint32_t d[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    uint32_t word = 0;
+    float t[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int jj = 4 * i + j;
-      const int qv = (m < M && k0 + jj < K) ? quant_act_s8(x.get(jj), inv, zpf) : 0;
-      word |= ((uint32_t)qv & 0xffu) << (8 * j);
+      // outside x: xq = 128, i.e. s8 0
+      t[j] = (m < M && k0 + jj < K) ? __builtin_fmaf(x.get(jj), inv, zpf) : 128.0f;
     }
-    d[i] = word;
+    d[i] = pack_act_s8x4(t[0], t[1], t[2], t[3]);
   }
   return (i32x4){(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
 }

@@ -93,17 +93,35 @@ __global__ __launch_bounds__(1024) void minmax_partial_kernel(const void* __rest
   // 8-element chunks, row by row; block b covers chunks b, b + nparts, ...
   const int cpr = (K + 7) / 8;
   const int64_t nch = (int64_t)M * cpr;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   float mn = 0.0f, mx = 0.0f;  // lo <= 0 <= hi after clamping anyway
-  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < nch; c += (int64_t)gridDim.x * blockDim.x) {
-    const int m = (int)(c / cpr), k0 = (int)(c - (int64_t)m * cpr) * 8;
-    float t[8];
-    load8_f32<XT>(xv, ldx, M, K, m, k0, vec, t);
+  auto fold = [&](const float* t, int k0) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float v = k0 + j < K ? t[j] : 0.0f;
       mn = fminf(mn, v);
       mx = fmaxf(mx, v);
     }
+  };
+  int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; c + 3 * stride < nch; c += 4 * stride) {  // four chunks in flight
+    float t[4][8];
+    int k0[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t ci = c + i * stride;
+      const int m = (int)(ci / cpr);
+      k0[i] = (int)(ci - (int64_t)m * cpr) * 8;
+      load8_f32<XT>(xv, ldx, M, K, m, k0[i], vec, t[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fold(t[i], k0[i]);
+  }
+  for (; c < nch; c += stride) {
+    const int m = (int)(c / cpr), k0 = (int)(c - (int64_t)m * cpr) * 8;
+    float t[8];
+    load8_f32<XT>(xv, ldx, M, K, m, k0, vec, t);
+    fold(t, k0);
   }
   __shared__ float red[32];
   mn = wave_min(mn);

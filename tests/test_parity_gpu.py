@@ -292,6 +292,30 @@ def test_w8a8_bitexact(dev, M, N, K, xd):
     assert (np.float32(sx), zp) == (np.float32(info["scale"]), info["zero_point"])
 
 
+@pytest.mark.parametrize("M", [1, 8, 64, 512])
+def test_w8a8_quantizer_ties(dev, M):
+    """Activations that land exactly on .5 after fma(x, 1/s_x, zp): x >= 0
+    with max 255/16 gives s_x = 1/16, zp = 0, and x = (k + 0.5)/16 rounds half
+    to even.  The fused GEMV (M=1), the partials GEMV (M=8) and the GEMM paths
+    must match fbgemm's quantizer bit for bit."""
+    announce(f"w8a8 ties M={M}")
+    N, K = 256, 4096
+    w = make_weights(N, K, 3300)
+    kk = torch.arange(K).view(1, K)
+    mm = torch.arange(M).view(M, 1)
+    x = (((kk * 7 + mm * 13) % 255).float() + 0.5) / 16.0
+    x[:, 0] = 255.0 / 16.0
+    x = x.half()
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref, info = oracle.dyn_linear(x.float().numpy(), q, s, return_intermediates=True)
+    assert (float(info["scale"]), int(info["zero_point"])) == (1.0 / 16.0, 0)
+    lin = quant.DynamicInt8Linear(w, None)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y = quant.linear_w8a8(x.to(dev), lin.packed, lin.scale, lin.colsum, None, N, acc_out=acc)
+    np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
+    np.testing.assert_array_equal(y.cpu().numpy(), ref)
+
+
 def test_w8a8_golden_fixture(dev):
     announce("w8a8 golden fixture")
     d = np.load(GOLD / "int8_dyn.npz")
