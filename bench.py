@@ -198,15 +198,18 @@ def dominant_kernel(ctx, M=1, launches_per_copy=8, reps=5):
 # ---------------------------------------------------------------------------
 # prefill GEMM and int8-dyn
 # ---------------------------------------------------------------------------
-def prefill_bench(ctx, M, N=12288, K=4096, steps=10, warmup=3):
+def prefill_bench(ctx, M, N=12288, K=4096, steps=10, warmup=3, xdtype=None):
     quant = ctx.quant
     packed, s, _ = ctx.weights(N, K, 900)
     x = ctx.act(M, K, 901)
+    if xdtype is not None:
+        x = x.to(xdtype)
     y = ctx.torch.empty((M, N), dtype=ctx.torch.float16, device=ctx.dev)
     ws = quant.w8_workspace(M, K, ctx.dev, x.dtype)  # row-sum scratch: the pre-pass is part of each timed step
     ms = ctx.time_steps(lambda c: quant.linear_w8(x, packed, s, None, N, out=y, workspace=ws), 1, steps, warmup)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-    return {"M": M, "N": N, "K": K, "ms": ms, "TFLOPs": tflops, "mfma_frac": tflops / F16_PEAK_TFLOPS}
+    return {"M": M, "N": N, "K": K, "x": str(x.dtype).replace("torch.", ""), "ms": ms, "TFLOPs": tflops,
+            "mfma_frac": tflops / F16_PEAK_TFLOPS}
 
 
 def w8a8_bench(ctx, M, N, K=4096, steps=10, warmup=3):
@@ -543,6 +546,9 @@ def main():
                                                xdtype=torch.float32)
         log("prefill GEMM")
         extra["prefill"] = [prefill_bench(ctx, M) for M in (512, 2048, 8192)]
+        # the reference model's own activations are fp32: staged as fp16 hi + lo planes
+        extra["prefill_other_x"] = [prefill_bench(ctx, 2048, xdtype=dt)
+                                    for dt in (ctx.torch.bfloat16, ctx.torch.float32)]
         log("int8-dyn")
         extra["w8a8"] = [w8a8_bench(ctx, M, N) for M in (1, 128, 2048) for N in (4096, 12288)]
         log("36-layer linear stack")

@@ -251,18 +251,11 @@ __device__ inline ActQParams choose_act_qparams(float xmin, float xmax) {
   return p;
 }
 
-// xq - 128 as a signed byte: clamp(rint(fma(x, inv, zp)), 0, 255) - 128.
-__device__ __forceinline__ int quant_act_s8(float x, float inv, float zpf) {
-  float t = __builtin_fmaf(x, inv, zpf);
-  t = __builtin_rintf(t);
-  t = fminf(fmaxf(t, 0.0f), 255.0f);
-  return (int)t - 128;
-}
-
-// Four pre-rounding values t = fma(x, inv, zp) -> four packed s8 (xq - 128).
-// v_cvt_pk_u8_f32 computes clamp(rint(t), 0, 255) (ties to even, NaN -> 0,
-// as quant_act_s8 does; checked on MI355X) and packs the byte; ^ 0x80 maps
-// u8 to s8 - 128 for four values at once.
+// fbgemm's activation quantizer xq = clamp(rint(fma(x, 1/s_x, zp)), 0, 255),
+// kept as s8 xq - 128: four pre-rounding values t = fma(x, inv, zp) -> four
+// packed bytes.  v_cvt_pk_u8_f32 computes clamp(rint(t), 0, 255) (ties to
+// even, NaN -> 0; checked on MI355X) and packs the byte; ^ 0x80 maps u8 to
+// s8 - 128 for four values at once.
 __device__ __forceinline__ uint32_t pack_act_s8x4(float t0, float t1, float t2, float t3) {
   uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(t0, 0, 0u);
   w = __builtin_amdgcn_cvt_pk_u8_f32(t1, 1, w);
