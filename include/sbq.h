@@ -132,7 +132,8 @@ int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K, int x_dtype);
 
 /* Workspace bytes sbq_linear_w8a8 / sbq_act_qparams need for an [M, K] input:
  * 2.5 KiB of activation statistics plus M * ceil(K/64)*64 bytes for the
- * quantized activations of the tiled (M > 32) path, plus alignment slack. */
+ * quantized activations of the tiled (M > 32) path, M floats of per-token
+ * scales (sbq_linear_w8a8_token), plus alignment slack. */
 int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K);
 
 /* The activation quantization parameters that fbgemm's dynamic linear chooses
@@ -160,6 +161,22 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
                     const float* bias, int64_t N,
                     void* y, int y_dtype, int64_t ldy, int32_t* acc_out,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Per-token symmetric W8A8: an opt-in granularity with no counterpart in the
+ * reference, whose int8-dyn (quant.py:63-66, sbq_linear_w8a8 above) is
+ * per-tensor asymmetric; it does not reproduce the reference's outputs.  Each
+ * activation row is quantized exactly as quantize_per_channel (quant.py:25-29)
+ * quantizes a weight row:
+ *   s_t[m] = max(max_k |x[m,k]|, 1e-8) / 127      (IEEE fp32 division)
+ *   xq[m,k] = clamp(rne(x[m,k] / s_t[m]), -127, 127)
+ *   acc[m,n] = sum_k xq[m,k] * q[n,k]            (int32, exact; acc_out nullable)
+ *   y[m,n] = fp32(acc) * fp32(s_t[m] * scale[n]) (with a bias: one fma)
+ * workspace: >= sbq_w8a8_workspace_bytes(M, K) bytes.  Every M runs the
+ * row quantizer and the tiled int8 MFMA GEMM. */
+int sbq_linear_w8a8_token(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                          const uint8_t* packed, const float* scale, const float* bias, int64_t N,
+                          void* y, int y_dtype, int64_t ldy, int32_t* acc_out,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- greedy token selection (engine.py:30-31) ---- */
 

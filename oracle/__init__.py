@@ -27,6 +27,11 @@ How each function is pinned (tests/test_oracle.py):
   outliers, all-zero, tiny-range, one-signed and constant inputs; against the
   committed golden fixtures in tests/golden/; mutants (mul-then-round
   quantization, (acc*s_x)*s_w epilogue) must fail.
+* ``dyn_linear_token`` (per-token symmetric W8A8, an opt-in granularity with
+  no counterpart in the reference): its quantizer is ``quantize_per_channel``
+  applied to activation rows (pinned above), the int32 product is checked
+  against ``torch._int_mm``, and per-tensor-scale and (acc*s_t)*s_w epilogue
+  mutants must fail.
 """
 from __future__ import annotations
 
@@ -65,8 +70,9 @@ def lib():
         L.oracle_quantize_act.argtypes = [P, I, ctypes.c_float, ctypes.c_int32, P]
         L.oracle_dyn_linear.argtypes = [P, I, I, P, P, P, I, P, P, P, P, P]
         L.oracle_dyn_epilogue.argtypes = [P, I, I, ctypes.c_float, P, P, P]
+        L.oracle_dyn_epilogue_token.argtypes = [P, I, I, P, P, P, P]
         for f in ("oracle_quantize_per_channel", "oracle_int8_linear", "oracle_choose_qparams",
-                  "oracle_quantize_act", "oracle_dyn_linear", "oracle_dyn_epilogue"):
+                  "oracle_quantize_act", "oracle_dyn_linear", "oracle_dyn_epilogue", "oracle_dyn_epilogue_token"):
             getattr(L, f).restype = None
         _lib = L
     return _lib
@@ -194,6 +200,29 @@ def dyn_linear_c(x, q, scale, bias=None):
     lib().oracle_dyn_linear(_ptr(x), M, K, _ptr(q), _ptr(_f32(scale)), _ptr(b), N, _ptr(y),
                             _ptr(acc), _ptr(xq), _ptr(sx), _ptr(zp))
     return y, {"scale": float(sx[0]), "zero_point": int(zp[0]), "xq": xq, "acc": acc}
+
+
+# ---------------------------------------------------------------------------
+# Per-token symmetric W8A8 (opt-in granularity; not the reference's int8-dyn)
+# ---------------------------------------------------------------------------
+def dyn_linear_token(x, q, scale, bias=None, return_intermediates: bool = False):
+    """Each activation row quantized as quant.py:25-29 quantizes a weight row,
+    acc = sum_k xq * q in int32 (exact here as float64), then
+    y = fp32(acc) * fp32(s_t[m] * scale[n]), with a bias one fused multiply-add."""
+    x = _f32(x)
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    xq, st = quantize_per_channel(x2)
+    acc64 = xq.astype(np.float64) @ np.asarray(q, np.float64).T
+    acc = np.ascontiguousarray(acc64.astype(np.int64).astype(np.int32))
+    M, N = acc.shape
+    y = np.empty((M, N), np.float32)
+    b = None if bias is None else _f32(bias)
+    lib().oracle_dyn_epilogue_token(_ptr(acc), M, N, _ptr(_f32(st)), _ptr(_f32(scale)), _ptr(b), _ptr(y))
+    y = y.reshape(*shape[:-1], -1)
+    if return_intermediates:
+        return y, {"scale": st, "xq": xq, "acc": acc}
+    return y
 
 
 # ---------------------------------------------------------------------------

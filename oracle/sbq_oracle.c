@@ -139,6 +139,20 @@ void oracle_dyn_epilogue(const int32_t* acc, int64_t M, int64_t N, float sx, con
   }
 }
 
+/* Per-token symmetric W8A8 epilogue (opt-in granularity, no counterpart in the
+ * reference): y = fp32(acc) * fp32(s_t[m] * scale[n]), with a bias one fma. */
+void oracle_dyn_epilogue_token(const int32_t* acc, int64_t M, int64_t N, const float* st, const float* scale,
+                               const float* bias, float* y) {
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      volatile float mult = st[m] * scale[n];
+      float a = (float)acc[m * N + n];
+      volatile float out = bias ? fmaf(a, mult, bias[n]) : a * mult;
+      y[m * N + n] = out;
+    }
+  }
+}
+
 /* quant.py:63-66  DynamicInt8Linear.forward == linear_dynamic(x, packed):
  *   acc[m,n] = sum_k (xq[m,k] - zp) * q[n,k]            (exact integer)
  *   y[m,n]   = oracle_dyn_epilogue(acc)

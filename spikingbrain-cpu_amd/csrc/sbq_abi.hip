@@ -48,6 +48,11 @@ inline float2* ws_partials(void* workspace) {
 }
 inline float* ws_qp(void* workspace) { return (float*)((uint8_t*)ws_partials(workspace) + kWsPartialBytes); }
 inline int8_t* ws_xq(void* workspace) { return (int8_t*)((uint8_t*)ws_qp(workspace) + kWsQpBytes); }
+// per-token scales after the quantized activations
+inline float* ws_stok(void* workspace, int64_t M, int64_t K) {
+  const int64_t xq = M * (((K + 63) / 64) * 64);
+  return (float*)((uint8_t*)ws_xq(workspace) + ((xq + 255) & ~(int64_t)255));
+}
 
 }  // namespace
 
@@ -132,7 +137,7 @@ int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K) {
   static_assert(sbq::kMinMaxPartials * sizeof(float2) <= kWsPartialBytes, "partials fit");
   if (M < 0 || K < 0) return 0;
   const int64_t xq = M * (((K + 63) / 64) * 64);
-  return 256 + kWsPartialBytes + kWsQpBytes + ((xq + 255) & ~(int64_t)255);
+  return 256 + kWsPartialBytes + kWsQpBytes + ((xq + 255) & ~(int64_t)255) + ((M * 4 + 255) & ~(int64_t)255);
 }
 
 int sbq_act_qparams(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, float* scale_out,
@@ -147,6 +152,17 @@ int sbq_act_qparams(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
   int rc = sbq::launch_minmax_partials(x, x_dtype, M, K, ldx, parts, np, st);
   if (rc) return rc;
   return sbq::launch_qparams(parts, np, scale_out, zp_out, st);
+}
+
+int sbq_linear_w8a8_token(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
+                          const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
+                          int32_t* acc_out, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_linear(x, x_dtype, M, K, ldx, packed, scale, N, y, y_dtype, ldy);
+  if (rc || M == 0) return rc;
+  if (!workspace || (int64_t)workspace_bytes < sbq_w8a8_workspace_bytes(M, K)) return SBQ_ERR_WORKSPACE;
+  const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
+  return sbq::launch_gemm_w8a8_token(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, acc_out,
+                                     ws_xq(workspace), ws_stok(workspace, M, K), (hipStream_t)stream, yv);
 }
 
 int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,

@@ -516,11 +516,15 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   }
 
   const bool yvec = a.flags & 2;
+  // I8 per-token symmetric (flags bit 4): no zero point, y = fp32(acc) * fp32(s_t[m] * scale[n])
+  const bool ptok = I8 && (a.flags & 4);
   float sx = 0.0f;
   int corr = 0;
   if constexpr (I8) {
-    sx = a.qpbuf[0];
-    corr = 128 - __float_as_int(a.qpbuf[1]);
+    if (!ptok) {
+      sx = a.qpbuf[0];
+      corr = 128 - __float_as_int(a.qpbuf[1]);
+    }
   }
   // OFS: acc = 2^-24 * sum (q + 128) x, so y = (acc - 2^-17 * rowsum) * (scale * 2^24)
   // (* rscale[m] for staged fp32 / bf16 activations)
@@ -550,9 +554,9 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int nn = min(n + v, a.N - 1);
-      sc[v] = I8 ? sx * a.scale[nn] : (OFS ? a.scale[nn] * 0x1p24f : a.scale[nn]);
+      sc[v] = I8 ? (ptok ? a.scale[nn] : sx * a.scale[nn]) : (OFS ? a.scale[nn] * 0x1p24f : a.scale[nn]);
       bi[v] = a.bias ? a.bias[nn] : 0.0f;
-      cs[v] = I8 ? a.colsum[nn] : 0;
+      cs[v] = I8 && !ptok ? a.colsum[nn] : 0;
     }
 #pragma unroll
     for (int b = 0; b < FM; ++b) {
@@ -564,7 +568,8 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
         if constexpr (I8) {
           const int av = acc[t][b][v] + corr * cs[v];
           if (a.acc_out && v < nvalid) a.acc_out[(int64_t)m * a.N + n + v] = av;
-          o[v] = a.bias ? __builtin_fmaf((float)av, sc[v], bi[v]) : (float)av * sc[v];
+          const float f = ptok ? a.rscale[m] * sc[v] : sc[v];
+          o[v] = a.bias ? __builtin_fmaf((float)av, f, bi[v]) : (float)av * f;
         } else {
           float out = OFS ? ((acc[t][b][v] - rc[b]) * sc[v]) * rf[b] : acc[t][b][v] * sc[v];
           if (a.bias) out = out + bi[v];
@@ -838,6 +843,24 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
   a.packed = packed; a.scale = scale; a.bias = bias; a.colsum = colsum;
   a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.acc_out = acc_out; a.qpbuf = qpbuf;
   a.flags = flags;
+  return launch_gemm_dl_cfg(pick_gemm_dl(true, XT_F16, M, Nt), true, XT_F16, a, st);
+}
+
+// Per-token symmetric W8A8: xq [M, Kp] s8 and s_t [M] from the row quantizer,
+// then the i8 GEMM with the per-token epilogue (every M; small M is not a
+// GEMV here).
+int launch_gemm_w8a8_token(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec,
+                           const uint8_t* packed, const float* scale, const float* bias, int64_t N, void* y, int yt,
+                           int64_t ldy, int32_t* acc_out, int8_t* xq, float* s_t, hipStream_t st, bool yvec) {
+  const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64, Kp = Kc * 64;
+  if (Kp > ((int64_t)1 << 21)) return -1;  // 32-bit block offsets of the direct-to-LDS GEMM
+  int rc = launch_quantize_rows_sym(x, xt, ldx, xvec, M, K, Kp, xq, s_t, st);
+  if (rc) return rc;
+  GemmArgs a{};
+  a.x = xq; a.ldx = Kp; a.M = (int)M; a.Kc = (int)Kc;
+  a.packed = packed; a.scale = scale; a.bias = bias;
+  a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.acc_out = acc_out; a.rscale = s_t;
+  a.flags = (yvec ? 2 : 0) | 4;
   return launch_gemm_dl_cfg(pick_gemm_dl(true, XT_F16, M, Nt), true, XT_F16, a, st);
 }
 

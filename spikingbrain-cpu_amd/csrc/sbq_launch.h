@@ -52,6 +52,13 @@ struct W8Ws {
   int64_t rowsum, rscale, planes, bytes;
 };
 W8Ws w8_ws_layout(int64_t M, int64_t K, int xt);
+// Per-token symmetric W8A8 (opt-in int8-dyn granularity): xq scratch M x Kp
+// bytes (Kp = ceil(K/64)*64), s_t scratch M floats.
+int launch_gemm_w8a8_token(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec,
+                           const uint8_t* packed, const float* scale, const float* bias, int64_t N, void* y, int yt,
+                           int64_t ldy, int32_t* acc_out, int8_t* xq, float* s_t, hipStream_t st, bool yvec);
+int launch_quantize_rows_sym(const void* x, int xt, int64_t ldx, bool xvec, int64_t M, int64_t K, int64_t Kp,
+                             int8_t* xq, float* s_out, hipStream_t st);
 // Per-row sums in fp32 of fp16 x [M, K] (K % 8 == 0, 16-byte aligned rows).
 int launch_rowsum_f16(const void* x, int64_t ldx, int64_t M, int64_t K, float* out, hipStream_t st);
 // fp32 / bf16 x [M, K] -> scaled fp16 planes, row sums and row scales.

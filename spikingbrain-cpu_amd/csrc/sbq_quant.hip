@@ -204,6 +204,42 @@ __global__ __launch_bounds__(256) void rowsum_f16_kernel(const _Float16* __restr
   if (lane == 0) out[row] = s;
 }
 
+// Per-token symmetric activation quantization (the opt-in int8-dyn
+// granularity): each activation row is quantized exactly as
+// quantize_per_channel (spikingbrain_cpu/quant.py:25-29) quantizes a weight
+// row: s = max(max_k |x|, 1e-8) / 127 (IEEE division), xq = clamp(rne(x / s),
+// -127, 127).  xq rows have Kp bytes; columns K..Kp-1 are written as 0.
+template <int XT>
+__global__ __launch_bounds__(256) void quantize_rows_sym_kernel(const void* __restrict__ xv, int64_t ldx, int M, int K,
+                                                                int Kp, int vec, int8_t* __restrict__ xq,
+                                                                float* __restrict__ s_out) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  float amax = 0.0f;
+  for (int k = lane * 8; k < K; k += 512) {
+    float t[8];
+    load8_f32<XT>(xv, ldx, M, K, row, k, vec, t);  // columns >= K read as 0
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(t[j]));
+  }
+  amax = wave_max(amax);
+  const float sc = fmaxf(amax, 1e-8f) / 127.0f;
+  if (lane == 0) s_out[row] = sc;
+  int8_t* qrow = xq + (int64_t)row * Kp;
+  for (int k = lane * 8; k < Kp; k += 512) {
+    float t[8];
+    load8_f32<XT>(xv, ldx, M, K, row, k, vec, t);
+    uint32_t d[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float v = __builtin_rintf(t[j] / sc);
+      v = fminf(fmaxf(v, -127.0f), 127.0f);
+      d[j >> 2] |= ((uint32_t)(int)v & 0xffu) << (8 * (j & 3));
+    }
+    *(u32x2*)(qrow + k) = (u32x2){d[0], d[1]};  // Kp % 64 == 0 and Kp-byte rows: 8-byte aligned
+  }
+}
+
 // fp32 / bf16 activations -> power-of-two scaled fp16 planes for the fp16
 // prefill GEMM.  Row m is scaled by 2^e (max|x| * 2^e in [2^14, 2^15), an
 // exact scaling); plane 0 is hi = rn16(x * 2^e), plane 1 (fp32 only) is
@@ -389,6 +425,19 @@ int launch_stage_act(const void* x, int xt, int64_t ldx, int64_t M, int64_t K, _
     hipLaunchKernelGGL((stage_act_kernel<XT_BF16, 1>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale);
   else
     return -2;
+  return check_launch();
+}
+
+int launch_quantize_rows_sym(const void* x, int xt, int64_t ldx, bool xvec, int64_t M, int64_t K, int64_t Kp,
+                             int8_t* xq, float* s_out, hipStream_t st) {
+  const dim3 grid((unsigned)((M + 3) / 4)), block(256);
+  const int vec = xvec ? 1 : 0;
+  switch (xt) {
+    case XT_F32: hipLaunchKernelGGL(quantize_rows_sym_kernel<XT_F32>, grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kp, vec, xq, s_out); break;
+    case XT_F16: hipLaunchKernelGGL(quantize_rows_sym_kernel<XT_F16>, grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kp, vec, xq, s_out); break;
+    case XT_BF16: hipLaunchKernelGGL(quantize_rows_sym_kernel<XT_BF16>, grid, block, 0, st, x, ldx, (int)M, (int)K, (int)Kp, vec, xq, s_out); break;
+    default: return -2;
+  }
   return check_launch();
 }
 

@@ -172,6 +172,28 @@ def linear_w8a8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, col
     return y
 
 
+def linear_w8a8_token(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
+                      N: int, out_dtype: torch.dtype = torch.float32, acc_out: torch.Tensor | None = None,
+                      workspace: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-token symmetric W8A8 (opt-in; not the reference's int8-dyn): each
+    activation row is quantized as quantize_per_channel quantizes a weight
+    row, the int32 GEMM is exact, y = fp32(acc) * fp32(s_t[m] * scale[n])."""
+    x2 = _as_activation(x2)
+    M, K = x2.shape
+    y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x2.device)
+    ws = workspace if workspace is not None else w8a8_workspace(M, K, x2.device)
+    if acc_out is not None and (acc_out.dtype != torch.int32 or tuple(acc_out.shape) != (M, N)
+                                or not acc_out.is_contiguous()):
+        raise ValueError("acc_out must be a contiguous int32 [M, N] tensor")
+    with torch.cuda.device(x2.device):
+        _lib.check(_lib.load().sbq_linear_w8a8_token(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
+                                                     _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype),
+                                                     y.stride(0), _ptr(acc_out), _ptr(ws), ws.numel(),
+                                                     _stream(x2.device)),
+                   "sbq_linear_w8a8_token")
+    return y
+
+
 def greedy_tokens(logits: torch.Tensor) -> torch.Tensor:
     """engine.py:30-31 on the GPU: int64 [...] of row argmaxes of fp32 logits
     [..., V] (first index of the maximum, NaN above every number)."""
@@ -298,10 +320,18 @@ class Int8Linear(nn.Module):
 class DynamicInt8Linear(nn.Module):
     """quant.py:56-66.  The reference keeps only an opaque fbgemm prepacked
     weight (``packed``) and no state_dict entries; here ``packed`` is the tiled
-    device layout and ``scale``/``colsum`` are non-persistent buffers."""
+    device layout and ``scale``/``colsum`` are non-persistent buffers.
 
-    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None):
+    ``granularity="tensor"`` (default) is the reference's fbgemm semantics,
+    bit for bit.  ``granularity="token"`` opts into per-token symmetric
+    activation quantization (linear_w8a8_token), which has no counterpart in
+    the reference and does not reproduce its outputs."""
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, granularity: str = "tensor"):
         super().__init__()
+        if granularity not in ("tensor", "token"):
+            raise ValueError("granularity must be 'tensor' or 'token'")
+        self.granularity = granularity
         device = _gpu_for(weight)
         q, scale = quantize_per_channel_gpu(weight.to(device))
         packed, colsum = repack(q, with_colsum=True)
@@ -321,6 +351,8 @@ class DynamicInt8Linear(nn.Module):
         def run(xd):
             x2 = xd.reshape(-1, shape[-1])
             scale = self.scale if self.scale.dtype == torch.float32 else self.scale.float()
+            if getattr(self, "granularity", "tensor") == "token":
+                return linear_w8a8_token(x2, self.packed, scale, self.bias, self.out_features, self.out_dtype)
             return linear_w8a8(x2, self.packed, scale, self.colsum, self.bias, self.out_features, self.out_dtype)
 
         out = _run_on_device(x, self.packed.device, run)

@@ -233,6 +233,50 @@ def test_dyn_acc_is_exact_integer_gemm():
 
 
 # ---------------------------------------------------------------------------
+# per-token symmetric W8A8 (opt-in granularity)
+# ---------------------------------------------------------------------------
+def test_dyn_token_quantizer_is_the_weight_quantizer_on_rows():
+    """The per-token quantizer restates quant.py:25-29 on activation rows; check
+    it against torch CPU ops evaluating that expression (fp32 division, half-even)."""
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(37, 1000, generator=g) * torch.linspace(1e-3, 1e3, 37)[:, None]
+    x[3] = 0.0                                    # all-zero row: s = 1e-8 / 127
+    x[5, :4] = torch.tensor([0.5, 1.5, 2.5, -0.5]) * (x[5].abs().max() / 127)  # ties near the grid
+    q = np.random.default_rng(1).integers(-127, 128, (16, 1000)).astype(np.int8)
+    s = np.random.default_rng(2).random(16).astype(np.float32)
+    _, info = oracle.dyn_linear_token(x.numpy(), q, s, return_intermediates=True)
+    st = x.abs().amax(dim=1).clamp_min(1e-8) / 127.0
+    xq = torch.clamp(torch.round(x / st[:, None]), -127, 127).to(torch.int8)
+    np.testing.assert_array_equal(info["scale"], st.numpy())
+    np.testing.assert_array_equal(info["xq"], xq.numpy())
+
+
+def test_dyn_token_acc_and_epilogue():
+    g = torch.Generator().manual_seed(32)
+    M, N, K = 33, 24, 4096
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[:40]] *= 20.0
+    q = np.random.default_rng(3).integers(-127, 128, (N, K)).astype(np.int8)
+    s = (np.random.default_rng(4).random(N).astype(np.float32) + 0.5) * np.float32(1e-3)
+    b = np.random.default_rng(5).standard_normal(N).astype(np.float32)
+    y, info = oracle.dyn_linear_token(x.numpy(), q, s, return_intermediates=True)
+    # int32 accumulators: an independent route through torch's int8 GEMM
+    ti = torch._int_mm(torch.from_numpy(info["xq"]), torch.from_numpy(q).t().contiguous()).numpy()
+    np.testing.assert_array_equal(ti, info["acc"])
+    # epilogue: fp32(acc) * fp32(s_t * s_w); mutants must fail
+    acc = info["acc"].astype(np.float32)
+    st = info["scale"]
+    np.testing.assert_array_equal(y, acc * (st[:, None] * s[None, :]))
+    assert not np.array_equal(y, (acc * st[:, None]) * s[None, :])             # (acc * s_t) * s_w
+    assert not np.array_equal(y, acc * (np.float32(st.max()) * s[None, :]))   # one scale for the tensor
+    # bias: one fused multiply-add, not a separately rounded add
+    yb = oracle.dyn_linear_token(x.numpy(), q, s, bias=b)
+    fused = (acc.astype(np.float64) * (st[:, None] * s[None, :]).astype(np.float64) + b).astype(np.float32)
+    np.testing.assert_array_equal(yb, fused)
+    assert not np.array_equal(yb, (acc * (st[:, None] * s[None, :]) + b).astype(np.float32))
+
+
+# ---------------------------------------------------------------------------
 # packed layout model
 # ---------------------------------------------------------------------------
 def test_pack_layout_model():

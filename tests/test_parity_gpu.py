@@ -316,6 +316,42 @@ def test_w8a8_quantizer_ties(dev, M):
     np.testing.assert_array_equal(y.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("xd", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 64, 1000), (33, 512, 256), (128, 1024, 4096), (300, 130, 200),
+                                   (2048, 512, 4096)])
+def test_w8a8_token_bitexact(dev, M, N, K, xd):
+    """Per-token symmetric W8A8 (opt-in granularity): int32 accumulators and
+    fp32 outputs bit-exact against the oracle, on every activation dtype,
+    ragged K and small M; with 1% outlier channels x20."""
+    announce(f"w8a8 token M={M} N={N} K={K} x={xd}")
+    w = make_weights(N, K, 3500 + N + K)
+    x = make_x(M, K, 3600 + M + K, outliers=True).to(DT[xd])
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref, info = oracle.dyn_linear_token(x.float().numpy(), q, s, return_intermediates=True)
+    lin = quant.DynamicInt8Linear(w, None, granularity="token")
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y = quant.linear_w8a8_token(x.to(dev), lin.packed, lin.scale, None, N, acc_out=acc)
+    np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
+    np.testing.assert_array_equal(y.cpu().numpy(), ref)
+    np.testing.assert_array_equal(lin(x.to(dev)).cpu().numpy(), ref)
+
+
+def test_w8a8_token_bias_and_default_granularity(dev):
+    announce("w8a8 token bias")
+    M, N, K = 64, 300, 4096
+    w = make_weights(N, K, 3700)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(3701))
+    x = make_x(M, K, 3702, outliers=True)
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref = oracle.dyn_linear_token(x.numpy(), q, s, bias=b.numpy())
+    lin = quant.DynamicInt8Linear(w, b, granularity="token")
+    np.testing.assert_array_equal(lin(x.to(dev)).cpu().numpy(), ref)
+    # the default stays the reference's per-tensor semantics
+    assert quant.DynamicInt8Linear(w, None).granularity == "tensor"
+    with pytest.raises(ValueError):
+        quant.DynamicInt8Linear(w, None, granularity="row")
+
+
 def test_w8a8_golden_fixture(dev):
     announce("w8a8 golden fixture")
     d = np.load(GOLD / "int8_dyn.npz")
