@@ -701,6 +701,7 @@ int launch_dl_rsp(int id, const GemmArgs& a, hipStream_t st) {
   switch (id) {
     case 0: return launch_dl<false, XT_F16, 256, 128, 4, 2, 2, 1, true>(a, st);
     case 2: return launch_dl<false, XT_F16, 128, 128, 2, 2, 2, 1, true>(a, st);
+    case 3: return launch_dl<false, XT_F16, 128, 64, 2, 2, 2, 1, true>(a, st);
     case 5: return launch_dl<false, XT_F16, 128, 64, 2, 2, 2, 4, true>(a, st);
     case 8: return launch_dl<false, XT_F16, 64, 64, 1, 2, 2, 4, true>(a, st);
     case 10: return launch_dl<false, XT_F16, 256, 128, 4, 1, 2, 1, true>(a, st);
@@ -720,10 +721,9 @@ int launch_gemm_dl_cfg(int id, bool i8, int xt, const GemmArgs& a, hipStream_t s
 }
 
 // Configuration for a shape (measured on MI355X, K = 4096, M 128..8192,
-// N 1024..24576): big grids take 256 x 128 blocks (W8A8 and fp16 also
-// 128 x 128 for mid-size grids); grids that leave CUs short of waves take
-// 128 x 64 or 64 x 64 blocks with K split over 4 wave groups inside the
-// workgroup.  bf16 W-only keeps 64 x 128 wave tiles on the largest grids
+// N 1024..24576): big grids take 256 x 128 blocks, mid-size grids 128 x 128
+// or 128 x 64 blocks; grids that leave CUs short of waves take 128 x 64 or
+// 64 x 64 blocks with K split over 4 wave groups inside the workgroup.  bf16 W-only keeps 64 x 128 wave tiles on the largest grids
 // (half the conversion work per MFMA).
 int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt) {
   const int64_t t256 = ((Nt + 15) / 16) * ((M + 127) / 128);
@@ -736,8 +736,11 @@ int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt) {
     return 8;
   }
   if (xt == XT_F16) {
-    if (t256 >= 384) return 0;
-    if (t128 >= 256) return 2;
+    // measured over M = 256..8192, N = 4096..24576: the block size that keeps
+    // every CU busy with whole workgroups wins below M ~ 2048
+    if (t256 >= 768) return 0;
+    if (t128 >= 512) return 2;
+    if (t128x64 >= 384) return 3;
     if (t128x64 >= 128) return 5;
     return 8;
   }
