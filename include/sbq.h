@@ -171,8 +171,9 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
  *   xq[m,k] = clamp(rne(x[m,k] / s_t[m]), -127, 127)
  *   acc[m,n] = sum_k xq[m,k] * q[n,k]            (int32, exact; acc_out nullable)
  *   y[m,n] = fp32(acc) * fp32(s_t[m] * scale[n]) (with a bias: one fma)
- * workspace: >= sbq_w8a8_workspace_bytes(M, K) bytes.  Every M runs the
- * row quantizer and the tiled int8 MFMA GEMM. */
+ * workspace: >= sbq_w8a8_workspace_bytes(M, K) bytes.  The row quantizer runs
+ * first; then M <= 16 runs the HBM-streaming int8 MFMA GEMV on the s8 rows,
+ * larger M the tiled int8 MFMA GEMM. */
 int sbq_linear_w8a8_token(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                           const uint8_t* packed, const float* scale, const float* bias, int64_t N,
                           void* y, int y_dtype, int64_t ldy, int32_t* acc_out,

@@ -31,7 +31,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-enum XType { XT_F32 = 0, XT_F16 = 1, XT_BF16 = 2 };
+enum XType { XT_F32 = 0, XT_F16 = 1, XT_BF16 = 2, XT_S8 = 3 };  // XT_S8: pre-quantized activations (internal)
 
 // ---------------------------------------------------------------------------
 // int8 (offset binary) -> fp16 / bf16, exact.

@@ -23,6 +23,7 @@
 #include <type_traits>
 
 #include "sbq_common.h"
+#include "sbq_gemv_ops.h"
 #include "sbq_launch.h"
 
 namespace sbq {
@@ -850,8 +851,7 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
 }
 
 // Per-token symmetric W8A8: xq [M, Kp] s8 and s_t [M] from the row quantizer,
-// then the i8 GEMM with the per-token epilogue (every M; small M is not a
-// GEMV here).
+// then the fast GEMV (M <= 16) or the i8 GEMM with the per-token epilogue.
 int launch_gemm_w8a8_token(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec,
                            const uint8_t* packed, const float* scale, const float* bias, int64_t N, void* y, int yt,
                            int64_t ldy, int32_t* acc_out, int8_t* xq, float* s_t, hipStream_t st, bool yvec) {
@@ -859,6 +859,18 @@ int launch_gemm_w8a8_token(const void* x, int xt, int64_t M, int64_t K, int64_t 
   if (Kp > ((int64_t)1 << 21)) return -1;  // 32-bit block offsets of the direct-to-LDS GEMM
   int rc = launch_quantize_rows_sym(x, xt, ldx, xvec, M, K, Kp, xq, s_t, st);
   if (rc) return rc;
+  if (M <= 16) {  // decode sizes: the HBM-streaming GEMV on the s8 rows
+    GemvArgs g{};
+    g.x = xq; g.ldx = Kp; g.M = (int)M; g.K = (int)Kp; g.Kc = (int)Kc;
+    g.packed = packed; g.scale = scale; g.bias = bias;
+    g.N = (int)N; g.Nt = (int)Nt; g.y = y; g.yt = yt; g.ldy = ldy; g.acc_out = acc_out; g.rscale = s_t;
+    g.flags = 1 | (yvec ? 2 : 0);
+    int id = 0, ks = 0;
+    if (pick_gemv_fast(M, Kp, N, XT_F16, false, true, &id, &ks)) {
+      rc = launch_gemv_fast_cfg(id, ks, g, XT_S8, true, st);
+      if (rc != -1) return rc;
+    }
+  }
   GemmArgs a{};
   a.x = xq; a.ldx = Kp; a.M = (int)M; a.Kc = (int)Kc;
   a.packed = packed; a.scale = scale; a.bias = bias;

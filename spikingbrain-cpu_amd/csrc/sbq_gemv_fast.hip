@@ -65,7 +65,9 @@ __device__ __forceinline__ void lds_barrier() {
 // 16 consecutive activations of one row from global memory or LDS.
 template <int XT>
 __device__ __forceinline__ void load_frag(XRaw<XT>& f, const uint8_t* p) {
-  if constexpr (XT == XT_F32) {
+  if constexpr (XT == XT_S8) {
+    f.v = *(const u32x4*)p;
+  } else if constexpr (XT == XT_F32) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) f.v[i] = *(const f32x4*)(p + 16 * i);
   } else {
@@ -95,10 +97,14 @@ __host__ __device__ constexpr int mm_bytes() { return kFastMaxWaves * 8; }
 }  // namespace
 
 // QM: 0 weight-only; 1 W8A8 with the activation min/max partials of the
-// pre-pass; 2 W8A8 that reduces min/max over the whole (small) x itself.
+// pre-pass; 2 W8A8 that reduces min/max over the whole (small) x itself;
+// 3 per-token symmetric W8A8 on pre-quantized s8 activations (XT_S8) with
+// per-row scales a.rscale.
 template <int XT, int D, int G, bool XL, int QM>
 __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs a, int KW, int xch) {
   constexpr bool W8A8 = QM != 0;
+  constexpr bool PT = QM == 3;
+  static_assert(!PT || (XT == XT_S8 && !XL), "per-token: s8 fragments loaded directly");
   typedef typename std::conditional<W8A8, i32x4, f32x4>::type Acc;
   constexpr int EB = x_bytes<XT>();
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -129,7 +135,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       const int nn = min(ne + v, a.N - 1);
       sc[v] = a.scale[nn];
       if (a.bias) bi[v] = a.bias[nn];
-      if constexpr (W8A8) cs[v] = a.colsum[nn];
+      if constexpr (W8A8 && !PT) cs[v] = a.colsum[nn];
     }
   }
   // W8A8: min/max partials of the activation pre-pass, or (QM 2) up to
@@ -175,7 +181,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   }
 
   ActQParams qp = {};
-  if constexpr (XL || W8A8) {
+  if constexpr (XL || (W8A8 && !PT)) {
     if constexpr (QM == 2) {
       float mn = 0.0f, mx = 0.0f;
 #pragma unroll
@@ -256,7 +262,11 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
     XRaw<XT> f;
     if constexpr (XL) load_frag<XT>(f, xl + (kbeg + kt) * 64 * EB);
     else f = xd[p];
-    if constexpr (W8A8) {
+    if constexpr (PT) {
+      const i32x4 q = __builtin_bit_cast(i32x4, f.v);
+#pragma unroll
+      for (int j = 0; j < G; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_to_s8(w[p][j]), q, acc[j], 0, 0, 0);
+    } else if constexpr (W8A8) {
       const i32x4 q = quant16<XT>(f, qp.inv, qp.zpf);
 #pragma unroll
       for (int j = 0; j < G; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_to_s8(w[p][j]), q, acc[j], 0, 0, 0);
@@ -302,7 +312,15 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   }
   const int nvalid = min(4, a.N - n);
   f32x4 o;
-  if constexpr (W8A8) {
+  if constexpr (PT) {
+    const float st = a.rscale[r];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (a.acc_out && v < nvalid) a.acc_out[(int64_t)r * a.N + n + v] = s[v];
+      const float mult = st * sc[v];
+      o[v] = a.bias ? __builtin_fmaf((float)s[v], mult, bi[v]) : (float)s[v] * mult;
+    }
+  } else if constexpr (W8A8) {
     const int corr = 128 - qp.zp;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -349,11 +367,14 @@ template <int XT, int QM>
 int launch_fast_typed(int id, const GemvArgs& a, int ks, int KW, int xch, size_t lds, hipStream_t st) {
   const dim3 block(ks * 64);
   switch (id) {
-#define SBQ_FAST_CASE(ID, D, G, XL)                                                                         \
-  case ID:                                                                                                  \
-    hipLaunchKernelGGL((gemv_fast_kernel<XT, D, G, XL, QM>), dim3((a.Nt + G - 1) / G), block, lds, st, a, KW, \
-                       xch);                                                                                \
-    return check_launch();
+#define SBQ_FAST_CASE(ID, D, G, XL)                                                                           \
+  case ID:                                                                                                    \
+    if constexpr (QM != 3 || !XL) {                                                                           \
+      hipLaunchKernelGGL((gemv_fast_kernel<XT, D, G, XL, QM>), dim3((a.Nt + G - 1) / G), block, lds, st, a, KW, \
+                         xch);                                                                                \
+      return check_launch();                                                                                  \
+    }                                                                                                         \
+    return -1;
     SBQ_FAST_CONFIGS(SBQ_FAST_CASE)
 #undef SBQ_FAST_CASE
   }
@@ -373,6 +394,10 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   const int KW = (a.Kc + ks - 1) / ks;
   ks = (a.Kc + KW - 1) / KW;  // every wave gets at least one K tile
   if (ks < c.G) return -1;                  // each row tile's epilogue belongs to one wave
+  if (xt == XT_S8) {  // per-token W8A8 on pre-quantized activations: direct fragments only
+    if (c.XL || !a.rscale) return -1;
+    return launch_fast_typed<XT_S8, 3>(id, a, ks, KW, 0, (size_t)ks * c.G * 64 * 16 + mm_bytes(), st);
+  }
   if (w8a8 && ks * 64 < a.nparts) return -1;  // one min/max partial per thread
   const int eb = xt == XT_F32 ? 4 : 2;
   const int64_t xbytes = (int64_t)a.M * a.K * eb;

@@ -24,6 +24,7 @@ struct GemvArgs {
   int32_t* acc_out;
   const float2* partials;
   int nparts;
+  const float* rscale;  // per-token W8A8: s_t [M]
   int flags;
 };
 
@@ -33,6 +34,12 @@ struct GemvArgs {
 // ---------------------------------------------------------------------------
 template <int XT>
 struct XRaw;
+
+// 16 pre-quantized s8 activations: the i8 MFMA B operand as loaded
+template <>
+struct XRaw<XT_S8> {
+  u32x4 v;
+};
 
 template <>
 struct XRaw<XT_F16> {
@@ -120,7 +127,7 @@ struct XRaw<XT_F32> {
 
 // Element bytes of an activation type.
 template <int XT>
-constexpr int x_bytes() { return XT == XT_F32 ? 4 : 2; }
+constexpr int x_bytes() { return XT == XT_F32 ? 4 : (XT == XT_S8 ? 1 : 2); }
 
 // Default number of 16-byte chunks of x per thread the LDS staging holds.
 constexpr int kStageChunks = 4;
