@@ -13,7 +13,10 @@ oracle and not from importing the reference package:
   outlier channels x20, an all-zero input, a tiny-range input, one-signed
   inputs and a bias.
 
-Usage: python tests/golden/make_golden.py
+* int8_dyn_token.npz - the opt-in per-token symmetric W8A8 (see
+  gen_int8_dyn_token), torch CPU ops only.
+
+Usage: python tests/golden/make_golden.py [fixture names]
 """
 from __future__ import annotations
 
@@ -112,8 +115,37 @@ def gen_int8_dyn(out: dict):
     out["kinds"] = np.array(names)
 
 
-def main():
-    for name, fn in (("quantize_per_channel", gen_quantize), ("int8_linear", gen_int8_linear), ("int8_dyn", gen_int8_dyn)):
+def gen_int8_dyn_token(out: dict):
+    """Per-token symmetric W8A8 (the opt-in granularity; no reference operator
+    exists): rows quantized by the quant.py:25-29 expression in torch ops, the
+    int32 product by torch._int_mm, y = fp32(acc) * fp32(s_t * s_w) in torch
+    fp32.  No bias here: its fused multiply-add has no exact torch CPU op."""
+    cases = [(1, 64, 4096), (5, 64, 4096), (33, 64, 1024)]
+    for i, (M, N, K) in enumerate(cases):
+        g = torch.Generator().manual_seed(400 + i)
+        w = torch.randn(N, K, generator=g) * 0.02
+        x = torch.randn(M, K, generator=g)
+        idx = torch.randperm(K, generator=g)[: K // 100]
+        x[:, idx] *= 20
+        q, sc = torch_quantize(w)
+        xq, st = torch_quantize(x)
+        xp = torch.zeros(max(M, 17), K, dtype=torch.int8)  # _int_mm wants at least 17 rows
+        xp[:M] = xq
+        acc = torch._int_mm(xp, q.t().contiguous())[:M]
+        y = acc.float() * (st[:, None] * sc[None, :])
+        out[f"c{i}_x"], out[f"c{i}_q"], out[f"c{i}_scale"] = x.numpy(), q.numpy(), sc.numpy()
+        out[f"c{i}_st"], out[f"c{i}_xq"], out[f"c{i}_acc"], out[f"c{i}_y"] = st.numpy(), xq.numpy(), acc.numpy(), y.numpy()
+    out["cases"] = np.array(cases, dtype=np.int64)
+
+
+GENERATORS = (("quantize_per_channel", gen_quantize), ("int8_linear", gen_int8_linear), ("int8_dyn", gen_int8_dyn),
+              ("int8_dyn_token", gen_int8_dyn_token))
+
+
+def main(names=None):
+    for name, fn in GENERATORS:
+        if names and name not in names:
+            continue
         out: dict = {}
         fn(out)
         np.savez_compressed(HERE / f"{name}.npz", **out)
@@ -121,4 +153,6 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    import sys
+
+    main(sys.argv[1:])

@@ -251,6 +251,17 @@ def test_dyn_token_quantizer_is_the_weight_quantizer_on_rows():
     np.testing.assert_array_equal(info["xq"], xq.numpy())
 
 
+def test_dyn_token_golden_fixture():
+    """int8_dyn_token.npz: s_t, xq, int32 acc and y from torch CPU ops alone."""
+    d = np.load(GOLD / "int8_dyn_token.npz")
+    for i in range(len(d["cases"])):
+        y, info = oracle.dyn_linear_token(d[f"c{i}_x"], d[f"c{i}_q"], d[f"c{i}_scale"], return_intermediates=True)
+        np.testing.assert_array_equal(info["scale"], d[f"c{i}_st"])
+        np.testing.assert_array_equal(info["xq"], d[f"c{i}_xq"])
+        np.testing.assert_array_equal(info["acc"], d[f"c{i}_acc"])
+        np.testing.assert_array_equal(y, d[f"c{i}_y"])
+
+
 def test_dyn_token_acc_and_epilogue():
     g = torch.Generator().manual_seed(32)
     M, N, K = 33, 24, 4096

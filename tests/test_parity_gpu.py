@@ -364,6 +364,19 @@ def test_w8a8_golden_fixture(dev):
         np.testing.assert_array_equal(y.cpu().numpy(), yref, err_msg=str(kind))
 
 
+def test_w8a8_token_golden_fixture(dev):
+    announce("w8a8 token golden fixture")
+    d = np.load(GOLD / "int8_dyn_token.npz")
+    for i in range(len(d["cases"])):
+        x, q, s = d[f"c{i}_x"], d[f"c{i}_q"], d[f"c{i}_scale"]
+        packed, _ = quant.repack(torch.from_numpy(q).to(dev), with_colsum=False)
+        acc = torch.empty((x.shape[0], q.shape[0]), dtype=torch.int32, device=dev)
+        y = quant.linear_w8a8_token(torch.from_numpy(x).to(dev), packed, torch.from_numpy(s).to(dev), None,
+                                    q.shape[0], acc_out=acc)
+        np.testing.assert_array_equal(acc.cpu().numpy(), d[f"c{i}_acc"], err_msg=f"case {i}")
+        np.testing.assert_array_equal(y.cpu().numpy(), d[f"c{i}_y"], err_msg=f"case {i}")
+
+
 @pytest.mark.parametrize("kind", ["zeros", "tiny", "tinypos", "tinyneg", "positive", "negative", "const", "huge"])
 def test_w8a8_qparams_edge_cases(dev, kind):
     announce(f"qparams {kind}")
