@@ -243,18 +243,15 @@ __global__ __launch_bounds__(WN* WM * 64) void gemm_w8_kernel(const void* __rest
 // 256 x 128, 8 waves (4 x 2, wave tile 64 x 64) and 2 stages: measured on
 // MI355X this beats 4-wave / 3-stage variants, because two 64 KiB workgroups
 // share a CU (4 waves per SIMD) and hide each other's LDS and barrier stalls.
-// Each stage is filled by global_load_lds_dwordx4 (16 bytes per lane straight
-// into LDS, no register staging): the packed weight tiles land verbatim, the
-// activation rows land with their 16-byte chunks XOR-swizzled by
+// Each stage is filled by buffer_load_dwordx4 ... lds (16 bytes per lane
+// straight into LDS, no register staging): the packed weight tiles land
+// verbatim, the activation rows land with their 16-byte chunks XOR-swizzled by
 // ((row >> 1) & 7), which spreads the 16 rows one ds_read_b128 quarter-wave
 // touches over all 64 LDS banks.  With NS stages, NS-1 are in flight while one
 // is multiplied.
 // Rows >= M and tiles >= Nt are loaded from clamped (in-bounds) addresses and
 // never stored.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
 
 // Raw buffer over [base, base + bytes): loads outside it return zeros.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, uint32_t bytes) {
