@@ -45,6 +45,7 @@ I8_PEAK_TOPS = 5000.0
 DECODE_SHAPES = [(6144, 4096), (24576, 4096), (4096, 12288)]  # fused QKV, gate+up, down
 DOMINANT = (24576, 4096)
 ROTATE_BYTES = 512 << 20
+WARM_MS = 100.0  # untimed sustained load before each timed region
 SOFTMAX_LAYERS = (0, 1, 2, 3, 6, 12, 17, 21, 24, 35)
 
 
@@ -100,13 +101,19 @@ class Ctx:
             fn()
         return g
 
-    def time_graphs(self, graphs, steps, warmup):
+    def time_graphs(self, graphs, steps, warmup, warm_ms=WARM_MS):
         """Replay graphs round-robin; return ms per replay (events on the
-        stream the graphs are launched on, synchronize on both sides)."""
+        stream the graphs are launched on, synchronize on both sides).  Untimed
+        warmup: `warmup` replays, then more until `warm_ms` of wall time."""
         torch = self.torch
         for i in range(warmup):
             graphs[i % len(graphs)].replay()
         torch.cuda.synchronize()
+        t0, i = time.perf_counter(), 0
+        while (time.perf_counter() - t0) * 1e3 < warm_ms:
+            graphs[i % len(graphs)].replay()
+            torch.cuda.synchronize()
+            i += 1
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -116,10 +123,12 @@ class Ctx:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps
 
-    def time_steps(self, step, copies, steps, warmup):
+    def time_steps(self, step, copies, steps, warmup, warm_ms=WARM_MS):
         """ms per step for exactly `steps` steps; step(c) runs one step on weight
         copy c.  One graph holds `copies` consecutive steps (so the host replays
-        once per `copies` steps); a second graph holds the remainder."""
+        once per `copies` steps); a second graph holds the remainder.  Untimed
+        warmup: `warmup` steps, then replays of the same graph until `warm_ms`
+        of wall time has passed (the shader clock settles under sustained load)."""
         torch = self.torch
         full = self.graph(lambda: [step(c) for c in range(copies)])
         rem_n = steps % copies
@@ -127,6 +136,10 @@ class Ctx:
         for _ in range(max(1, -(-warmup // copies))):
             full.replay()
         torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < warm_ms:
+            full.replay()
+            torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -198,7 +211,7 @@ def dominant_kernel(ctx, M=1, launches_per_copy=8, reps=5):
 # ---------------------------------------------------------------------------
 # prefill GEMM and int8-dyn
 # ---------------------------------------------------------------------------
-def prefill_bench(ctx, M, N=12288, K=4096, steps=10, warmup=3, xdtype=None):
+def prefill_bench(ctx, M, N=12288, K=4096, steps=20, warmup=5, xdtype=None, per_graph=5):
     quant = ctx.quant
     packed, s, _ = ctx.weights(N, K, 900)
     x = ctx.act(M, K, 901)
@@ -206,22 +219,26 @@ def prefill_bench(ctx, M, N=12288, K=4096, steps=10, warmup=3, xdtype=None):
         x = x.to(xdtype)
     y = ctx.torch.empty((M, N), dtype=ctx.torch.float16, device=ctx.dev)
     ws = quant.w8_workspace(M, K, ctx.dev, x.dtype)  # row-sum scratch: the pre-pass is part of each timed step
-    ms = ctx.time_steps(lambda c: quant.linear_w8(x, packed, s, None, N, out=y, workspace=ws), 1, steps, warmup)
+    # per_graph steps per graph replay: the launch gap between replays is not the kernel's
+    ms = ctx.time_steps(lambda c: quant.linear_w8(x, packed, s, None, N, out=y, workspace=ws), per_graph, steps,
+                        warmup)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     return {"M": M, "N": N, "K": K, "x": str(x.dtype).replace("torch.", ""), "ms": ms, "TFLOPs": tflops,
             "mfma_frac": tflops / F16_PEAK_TFLOPS}
 
 
-def w8a8_bench(ctx, M, N, K=4096, steps=10, warmup=3):
+def w8a8_bench(ctx, M, N, K=4096, steps=20, warmup=5):
     torch, quant = ctx.torch, ctx.quant
     wbytes = N * K
-    copies = 1 if M >= 128 else math.ceil(ROTATE_BYTES / wbytes) + 1
-    layers = [ctx.weights(N, K, 950 + c, colsum=True) for c in range(copies)]
+    # decode sizes rotate weight copies (HBM-bound); prefill sizes reuse one copy, 5 steps per graph replay
+    ncopy = 1 if M >= 128 else math.ceil(ROTATE_BYTES / wbytes) + 1
+    copies = 5 if M >= 128 else ncopy
+    layers = [ctx.weights(N, K, 950 + c, colsum=True) for c in range(ncopy)]
     x = ctx.act(M, K, 951, outliers=True)
     y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
     ws = quant.w8a8_workspace(M, K, ctx.dev)
     def step(c):
-        L = layers[c]
+        L = layers[c % ncopy]
         quant.linear_w8a8(x, L[0], L[1], L[2], None, N, torch.float16, workspace=ws, out=y)
 
     ms = ctx.time_steps(step, copies, max(steps, copies), warmup)

@@ -332,7 +332,12 @@ constexpr int dl_min_waves() { return (BN / WN) * (BM / WM) > 64 * 64 ? 2 : 4; }
 
 // RSP (fp16 W-only): the per-row sums of x come precomputed in a.rsum instead
 // of being accumulated in the K loop.
-template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false>
+// KT (W8A8, one K group): K tiles per stage.  An i8 MFMA covers a whole 64-wide
+// K tile, so a one-tile stage holds half the MFMAs of an fp16 stage per
+// barrier; two tiles per stage restore the ratio.  Sub-stage j of a stage holds
+// weight tiles and activation columns of K tile KT * stage + j, laid out as a
+// one-tile stage.
+template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false, int KT = 1>
 __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) void gemm_dl_kernel(const GemmArgs a) {
   typedef GemmOp<XT> Op;
   typedef typename Op::V V;
@@ -342,8 +347,8 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   constexpr int XB = I8 ? 64 : 128;     // bytes of one activation row per stage
   constexpr int WT = BN / 16;           // weight tiles per stage
   constexpr int XR = BM * XB / 1024;    // 1 KiB activation chunks per stage
-  constexpr int WBYTES = WT * 1024, STAGE = WBYTES + BM * XB;
-  constexpr int LPS = (WT + XR) / GW;   // DMA instructions per wave per stage
+  constexpr int WBYTES = WT * 1024, SUB = WBYTES + BM * XB, STAGE = KT * SUB;
+  constexpr int LPS = KT * (WT + XR) / GW;  // DMA instructions per wave per stage
   constexpr int RED = (KG - 1) * GW * FN * FM * 1024;
   constexpr int LDSB = KG * NS * STAGE > RED ? KG * NS * STAGE : RED;
   // fp16 activations: weights enter the MFMA as subnormals u * 2^-24 (u = q + 128,
@@ -354,6 +359,7 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   static_assert(WT % GW == 0 && XR % GW == 0, "even DMA split");
   static_assert(NS >= 2 && NS <= 8, "stages");
   static_assert(FM % WN == 0, "row-sum split");
+  static_assert(KT == 1 || (I8 && KG == 1), "K-tile pairs: W8A8 with one K group");
   // one LDS object: with a second one the compiler waits for every stage DMA in
   // flight before any LDS read of the main loop (it cannot tell them apart)
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDSB + (RSK ? KG * BM * 4 : 0)];
@@ -365,7 +371,9 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   const int wn = w / WM, wm = w % WM;
   const int nt0 = blockIdx.x * WT, m0 = blockIdx.y * BM;
   const int M = a.M, Kc = a.Kc, Nt = a.Nt;
-  const int KX = a.kx > 0 ? a.kx : Kc;  // activation K tiles: x tile kc meets weight tile kc mod Kc
+  // stages of activation K tiles: x tile kc meets weight tile kc mod Kc (the
+  // host keeps Kc % KT == 0)
+  const int KX = (a.kx > 0 ? a.kx : Kc) / KT;
   const int KW = (KX + KG - 1) / KG;
   const int kbeg = kg * KW;
   const int cnt = min(KW, KX - kbeg);  // tiles of this group (<= 0: none)
@@ -405,14 +413,18 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   const int xslot = __builtin_amdgcn_readfirstlane(WBYTES + w * (XR / GW) * 1024);
   auto issue = [&](int i, int st) {
     // clamped: the surplus stages of a short last group are never multiplied
-    const int kc = KG == 1 ? i : max(0, min(kbeg + min(i, cnt - 1), KX - 1));
-    const int kw = kc >= Kc ? kc - Kc : kc;
-    const int sb = __builtin_amdgcn_readfirstlane((kg * NS + st) * STAGE);
+    const int ks = KG == 1 ? i : max(0, min(kbeg + min(i, cnt - 1), KX - 1));
 #pragma unroll
-    for (int i2 = 0; i2 < WT / GW; ++i2) lds_dma16_buf(wrs, woff[i2], kw * 1024, lds + sb + wslot + i2 * 1024);
+    for (int j = 0; j < KT; ++j) {
+      const int kc = ks * KT + j;
+      const int kw = kc >= Kc ? kc - Kc : kc;
+      const int sb = __builtin_amdgcn_readfirstlane((kg * NS + st) * STAGE + j * SUB);
 #pragma unroll
-    for (int i2 = 0; i2 < XR / GW; ++i2)
-      lds_dma16_buf(xrs, xoff[i2], kc * (I8 ? 64 : 128), lds + sb + xslot + i2 * 1024);
+      for (int i2 = 0; i2 < WT / GW; ++i2) lds_dma16_buf(wrs, woff[i2], kw * 1024, lds + sb + wslot + i2 * 1024);
+#pragma unroll
+      for (int i2 = 0; i2 < XR / GW; ++i2)
+        lds_dma16_buf(xrs, xoff[i2], kc * (I8 ? 64 : 128), lds + sb + xslot + i2 * 1024);
+    }
   };
 
   Acc acc[FN][FM];
@@ -439,14 +451,18 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
       const uint8_t* wb = lds + (kg * NS + i % NS) * STAGE;
       const uint8_t* xs = wb + WBYTES;
       if constexpr (I8) {
-        i32x4 xf[FM];
 #pragma unroll
-        for (int b = 0; b < FM; ++b) xf[b] = *(const i32x4*)(xs + xq_off(wm * TM + b * 16 + r, g));
+        for (int j = 0; j < KT; ++j) {
+          i32x4 xf[FM];
 #pragma unroll
-        for (int t = 0; t < FN; ++t) {
-          const i32x4 wf = tile_to_s8(*(const u32x4*)(wb + (wn * FN + t) * 1024 + lane * 16));
+          for (int b = 0; b < FM; ++b) xf[b] = *(const i32x4*)(xs + j * SUB + xq_off(wm * TM + b * 16 + r, g));
 #pragma unroll
-          for (int b = 0; b < FM; ++b) acc[t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, xf[b], acc[t][b], 0, 0, 0);
+          for (int t = 0; t < FN; ++t) {
+            const i32x4 wf = tile_to_s8(*(const u32x4*)(wb + j * SUB + (wn * FN + t) * 1024 + lane * 16));
+#pragma unroll
+            for (int b = 0; b < FM; ++b)
+              acc[t][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, xf[b], acc[t][b], 0, 0, 0);
+          }
         }
       } else {
 #pragma unroll
@@ -579,10 +595,12 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   }
 }
 
-template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false>
+template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false, int KT = 1>
 int launch_dl(const GemmArgs& a, hipStream_t st) {
+  if (a.Kc % KT) return -1;
   const dim3 grid((unsigned)((a.Nt + BN / 16 - 1) / (BN / 16)), (unsigned)((a.M + BM - 1) / BM));
-  hipLaunchKernelGGL((gemm_dl_kernel<I8, XT, BN, BM, WN, WM, NS, KG, RSP>), grid, dim3(KG * WN * WM * 64), 0, st, a);
+  hipLaunchKernelGGL((gemm_dl_kernel<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>), grid, dim3(KG * WN * WM * 64), 0, st,
+                     a);
   return check_launch();
 }
 
@@ -710,9 +728,24 @@ int launch_dl_rsp(int id, const GemmArgs& a, hipStream_t st) {
   return launch_dl_id<false, XT_F16>(id, b, st);
 }
 
+// W8A8 configurations with two K tiles per stage (ids 13-15); an odd number of
+// K tiles takes the one-tile configuration of the same block shape.
+int launch_dl_i8(int id, const GemmArgs& a, hipStream_t st) {
+  const bool kt2 = a.Kc % 2 == 0;
+  switch (id) {
+    case 13:
+      return kt2 ? launch_dl<true, XT_F16, 256, 256, 4, 2, 2, 1, false, 2>(a, st) : launch_dl_id<true, XT_F16>(12, a, st);
+    case 14:
+      return kt2 ? launch_dl<true, XT_F16, 128, 128, 2, 2, 2, 1, false, 2>(a, st) : launch_dl_id<true, XT_F16>(2, a, st);
+    case 15:
+      return kt2 ? launch_dl<true, XT_F16, 128, 64, 2, 2, 2, 1, false, 2>(a, st) : launch_dl_id<true, XT_F16>(3, a, st);
+  }
+  return launch_dl_id<true, XT_F16>(id, a, st);
+}
+
 // Launch of direct-to-LDS configuration `id` (tuning entry; -1: no such id).
 int launch_gemm_dl_cfg(int id, bool i8, int xt, const GemmArgs& a, hipStream_t st) {
-  if (i8) return launch_dl_id<true, XT_F16>(id, a, st);
+  if (i8) return launch_dl_i8(id, a, st);
   if (xt == XT_F16) return a.rsum ? launch_dl_rsp(id, a, st) : launch_dl_id<false, XT_F16>(id, a, st);
   if (xt == XT_BF16) return launch_dl_id<false, XT_BF16>(id, a, st);
   return -2;
@@ -728,10 +761,13 @@ int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt) {
   const int64_t t128 = ((Nt + 7) / 8) * ((M + 127) / 128);
   const int64_t t128x64 = ((Nt + 7) / 8) * ((M + 63) / 64);
   if (i8) {
-    if (t256 >= 512) return 0;
-    if (t128 >= 256) return 2;
-    if (t128x64 >= 256) return 5;
-    return 8;
+    // measured over M = 128..8192, N = 4096..24576: two K tiles per stage
+    // except on 256 x 128 blocks, which take three one-tile stages instead
+    if (t256 >= 1536) return 13;   // 256 x 256
+    if (t256 >= 512) return 1;     // 256 x 128
+    if (t128 >= 256) return 14;    // 128 x 128
+    if (t128x64 >= 256) return 15; // 128 x 64
+    return 8;                      // 64 x 64, K split over 4 wave groups
   }
   if (xt == XT_F16) {
     // measured over M = 256..8192, N = 4096..24576: the block size that keeps

@@ -292,6 +292,42 @@ def test_w8a8_bitexact(dev, M, N, K, xd):
     assert (np.float32(sx), zp) == (np.float32(info["scale"]), info["zero_point"])
 
 
+# W8A8 GEMM block configurations, chosen by grid size (short K keeps the oracle
+# fast): 256x256 blocks with two K tiles per stage, and its one-tile fallback
+# for an odd tile count; 256x128 with three stages; 128x128 and 128x64 with two
+# K tiles per stage and their odd-count fallbacks; ragged M and N.
+W8A8_GEMM_CFG = [(2048, 24576, 128), (2048, 24576, 192), (1024, 24576, 256), (512, 12288, 256), (512, 12288, 320),
+                 (256, 8192, 512), (256, 8192, 448), (1000, 12290, 256)]
+
+
+@pytest.mark.parametrize("M,N,K", W8A8_GEMM_CFG)
+def test_w8a8_gemm_block_configs(dev, M, N, K):
+    announce(f"w8a8 gemm config M={M} N={N} K={K}")
+    w = make_weights(N, K, 3700 + N + K)
+    x = make_x(M, K, 3800 + M + K, outliers=True).half()
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref, info = oracle.dyn_linear(x.float().numpy(), q, s, return_intermediates=True)
+    lin = quant.DynamicInt8Linear(w, None)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y = quant.linear_w8a8(x.to(dev), lin.packed, lin.scale, lin.colsum, None, N, acc_out=acc)
+    np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
+    np.testing.assert_array_equal(y.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 24576, 128), (1000, 12290, 256), (256, 8192, 448)])
+def test_w8a8_token_gemm_block_configs(dev, M, N, K):
+    announce(f"w8a8 token gemm config M={M} N={N} K={K}")
+    w = make_weights(N, K, 3900 + N + K)
+    x = make_x(M, K, 3950 + M + K, outliers=True).half()
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref, info = oracle.dyn_linear_token(x.float().numpy(), q, s, return_intermediates=True)
+    lin = quant.DynamicInt8Linear(w, None, granularity="token")
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y = quant.linear_w8a8_token(x.to(dev), lin.packed, lin.scale, None, N, acc_out=acc)
+    np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
+    np.testing.assert_array_equal(y.cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("M", [1, 8, 64, 512])
 def test_w8a8_quantizer_ties(dev, M):
     """Activations that land exactly on .5 after fma(x, 1/s_x, zp): x >= 0
