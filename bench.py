@@ -340,8 +340,10 @@ def traffic_probe(ctx, launches=24, cal_reps=4):
     log(f"traffic probe: {launches} gate+up launches, {cal_reps} copies of {CAL_BYTES >> 20} MiB")
 
 
-def prefill_probe(ctx, M=2048, N=12288, K=4096, launches=4):
-    """The prefill GEMM alone (int8 weights, fp16 x and y), for counter passes."""
+def prefill_probe(ctx, M=2048, N=12288, K=4096, launches=100):
+    """The prefill operation alone (row-sum pre-pass + GEMM; int8 weights, fp16
+    x and y), for counter passes; enough back-to-back launches (~17 ms) for
+    the shader clock to settle under the load."""
     torch, quant = ctx.torch, ctx.quant
     packed, s, _ = ctx.weights(N, K, 900)
     x = ctx.act(M, K, 901)
