@@ -13,7 +13,8 @@
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *     Every call is asynchronous on that stream and reentrant: the library
  *     keeps no mutable state between calls.
- *   - matrices are row-major; `ld*` is the row stride in elements.
+ *   - matrices are row-major; `ld*` is the row stride in elements.  Row and
+ *     column counts (M, N, K) above 2^31 - 1 are rejected with SBQ_ERR_ARG.
  *   - return value: SBQ_OK (0) or a negative SBQ_ERR_* code; nothing throws.
  *     sbq_status_string() names a code.
  *

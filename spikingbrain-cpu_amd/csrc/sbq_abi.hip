@@ -84,7 +84,7 @@ int sbq_check_device(void) {
 int sbq_quantize_per_channel(const void* w, int w_dtype, int64_t N, int64_t K, int64_t ldw, int8_t* q, int64_t ldq,
                              float* scale, void* stream) {
   if (!valid_dtype(w_dtype)) return SBQ_ERR_DTYPE;
-  if (N < 0 || K < 1 || ldw < K || ldq < K) return SBQ_ERR_ARG;
+  if (N < 0 || K < 1 || ldw < K || ldq < K || N > kIntMax || K > kIntMax) return SBQ_ERR_ARG;
   if (N == 0) return SBQ_OK;
   if (!w || !q || !scale) return SBQ_ERR_ARG;
   return sbq::launch_quantize_per_channel(w, w_dtype, N, K, ldw, q, ldq, scale, (hipStream_t)stream);
@@ -104,7 +104,7 @@ int sbq_repack_w8(const int8_t* q, int64_t N, int64_t K, int64_t ldq, uint8_t* p
 }
 
 int sbq_unpack_w8(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_t ldq, void* stream) {
-  if (N < 1 || K < 1 || ldq < K) return SBQ_ERR_ARG;
+  if (N < 1 || K < 1 || ldq < K || N > kIntMax || K > kIntMax) return SBQ_ERR_ARG;
   if (!q || !packed) return SBQ_ERR_ARG;
   return sbq::launch_unpack(packed, N, K, q, ldq, (hipStream_t)stream);
 }
@@ -135,7 +135,7 @@ int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
 
 int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K) {
   static_assert(sbq::kMinMaxPartials * sizeof(float2) <= kWsPartialBytes, "partials fit");
-  if (M < 0 || K < 0) return 0;
+  if (M < 0 || K < 0 || M > kIntMax || K > kIntMax) return 0;
   const int64_t xq = M * (((K + 63) / 64) * 64);
   return 256 + kWsPartialBytes + kWsQpBytes + ((xq + 255) & ~(int64_t)255) + ((M * 4 + 255) & ~(int64_t)255);
 }

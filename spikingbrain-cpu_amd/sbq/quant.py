@@ -74,6 +74,46 @@ def _as_activation(x2: torch.Tensor) -> torch.Tensor:
     return x2
 
 
+def packed_bytes(N: int, K: int) -> int:
+    """Size of the packed tiles of an int8 [N, K] weight (sbq_packed_bytes)."""
+    return ((N + 15) // 16) * 16 * ((K + 63) // 64) * 64
+
+
+def _check_operands(fn: str, x2: torch.Tensor, packed: torch.Tensor, N: int, y: torch.Tensor,
+                    vectors: tuple = (), ws: torch.Tensor | None = None) -> None:
+    """The sizes, dtypes and devices the kernels assume: the C ABI sees raw
+    pointers only, so a short buffer here would be read or written out of
+    bounds on the GPU.  vectors: (name, tensor or None, dtype) of the [N]
+    per-channel operands."""
+    M, K = x2.shape
+    dev = x2.device
+    if not x2.is_cuda:
+        raise ValueError(f"{fn}: x must be a GPU tensor")
+    if N < 1:
+        raise ValueError(f"{fn}: N must be >= 1")
+    need = packed_bytes(N, K)
+    if (packed.dtype != torch.uint8 or packed.device != dev or not packed.is_contiguous()
+            or packed.numel() < need):
+        raise ValueError(f"{fn}: packed must be contiguous uint8 on {dev} with >= {need} bytes (N={N}, K={K})")
+    for name, t, dt in vectors:
+        if t is not None and (t.dtype != dt or t.device != dev or not t.is_contiguous() or t.numel() < N):
+            raise ValueError(f"{fn}: {name} must be a contiguous {dt} tensor of N={N} elements on {dev}")
+    if y.device != dev or y.dim() != 2 or tuple(y.shape) != (M, N) or y.stride(-1) != 1:
+        raise ValueError(f"{fn}: out must be a [M={M}, N={N}] tensor with unit column stride on {dev}")
+    if ws is not None and (ws.device != dev or not ws.is_contiguous()):
+        raise ValueError(f"{fn}: workspace must be a contiguous tensor on {dev}")
+
+
+def _nbytes(t: torch.Tensor | None) -> int:
+    return 0 if t is None else t.numel() * t.element_size()
+
+
+def _check_in_features(x: torch.Tensor, K: int) -> None:
+    # torch's matmul in the reference forward raises RuntimeError on this
+    if x.dim() == 0 or x.shape[-1] != K:
+        raise RuntimeError(f"sbq: input of shape {tuple(x.shape)} does not end in in_features={K}")
+
+
 # ---------------------------------------------------------------------------
 # functional API over the C ABI (GPU tensors in, GPU tensors out)
 # ---------------------------------------------------------------------------
@@ -111,6 +151,10 @@ def repack(q: torch.Tensor, with_colsum: bool = True) -> tuple[torch.Tensor, tor
 
 
 def unpack(packed: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    """Packed tiles -> int8 [N, K] (the inverse of repack)."""
+    if (packed.dtype != torch.uint8 or not packed.is_cuda or not packed.is_contiguous()
+            or packed.numel() < packed_bytes(N, K)):
+        raise ValueError(f"unpack expects contiguous uint8 GPU tiles of >= {packed_bytes(N, K)} bytes")
     q = torch.empty((N, K), dtype=torch.int8, device=packed.device)
     with torch.cuda.device(packed.device):
         _lib.check(_lib.load().sbq_unpack_w8(_ptr(packed), N, K, _ptr(q), K, _stream(packed.device)),
@@ -138,10 +182,12 @@ def linear_w8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias:
     ws = workspace
     if ws is None and M > 16:  # decode sizes run the GEMV, which needs none
         ws = w8_workspace(M, K, x2.device, x2.dtype)
+    _check_operands("linear_w8", x2, packed, N, y, (("scale", scale, torch.float32), ("bias", bias, torch.float32)),
+                    ws)
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
                                              _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype), y.stride(0),
-                                             _ptr(ws), 0 if ws is None else ws.numel(), _stream(x2.device)),
+                                             _ptr(ws), _nbytes(ws), _stream(x2.device)),
                    "sbq_linear_w8")
     return y
 
@@ -161,12 +207,14 @@ def linear_w8a8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, col
     y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x2.device)
     ws = workspace if workspace is not None else w8a8_workspace(M, K, x2.device)
     if acc_out is not None and (acc_out.dtype != torch.int32 or tuple(acc_out.shape) != (M, N)
-                                or not acc_out.is_contiguous()):
-        raise ValueError("acc_out must be a contiguous int32 [M, N] tensor")
+                                or not acc_out.is_contiguous() or acc_out.device != x2.device):
+        raise ValueError("acc_out must be a contiguous int32 [M, N] tensor on the input's device")
+    _check_operands("linear_w8a8", x2, packed, N, y, (("scale", scale, torch.float32), ("bias", bias, torch.float32),
+                                                      ("colsum", colsum, torch.int32)), ws)
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8a8(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
                                                _ptr(scale), _ptr(colsum), _ptr(bias), N, _ptr(y), _code(y.dtype),
-                                               y.stride(0), _ptr(acc_out), _ptr(ws), ws.numel(),
+                                               y.stride(0), _ptr(acc_out), _ptr(ws), _nbytes(ws),
                                                _stream(x2.device)),
                    "sbq_linear_w8a8")
     return y
@@ -183,12 +231,14 @@ def linear_w8a8_token(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tenso
     y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x2.device)
     ws = workspace if workspace is not None else w8a8_workspace(M, K, x2.device)
     if acc_out is not None and (acc_out.dtype != torch.int32 or tuple(acc_out.shape) != (M, N)
-                                or not acc_out.is_contiguous()):
-        raise ValueError("acc_out must be a contiguous int32 [M, N] tensor")
+                                or not acc_out.is_contiguous() or acc_out.device != x2.device):
+        raise ValueError("acc_out must be a contiguous int32 [M, N] tensor on the input's device")
+    _check_operands("linear_w8a8_token", x2, packed, N, y,
+                    (("scale", scale, torch.float32), ("bias", bias, torch.float32)), ws)
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8a8_token(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
                                                      _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype),
-                                                     y.stride(0), _ptr(acc_out), _ptr(ws), ws.numel(),
+                                                     y.stride(0), _ptr(acc_out), _ptr(ws), _nbytes(ws),
                                                      _stream(x2.device)),
                    "sbq_linear_w8a8_token")
     return y
@@ -219,7 +269,7 @@ def act_qparams(x2: torch.Tensor) -> tuple[float, int]:
     ws = w8a8_workspace(M, K, x2.device)
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_act_qparams(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(s), _ptr(z),
-                                               _ptr(ws), ws.numel(), _stream(x2.device)),
+                                               _ptr(ws), _nbytes(ws), _stream(x2.device)),
                    "sbq_act_qparams")
     return float(s.item()), int(z.item())
 
@@ -303,6 +353,7 @@ class Int8Linear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not self.qweight.is_cuda:
             raise RuntimeError("sbq Int8Linear: weights are on the CPU; move the module to a ROCm GPU")
+        _check_in_features(x, self.in_features)
         self._refresh()
         shape = x.shape
         N = self.out_features
@@ -346,6 +397,7 @@ class DynamicInt8Linear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not self.packed.is_cuda:
             raise RuntimeError("sbq DynamicInt8Linear: weights are on the CPU; move the module to a ROCm GPU")
+        _check_in_features(x, self.in_features)
         shape = x.shape
 
         def run(xd):
@@ -508,6 +560,7 @@ class FusedLinear(nn.Module):
         self._memo_out = None
 
     def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, ...]:
+        _check_in_features(x, self.in_features)
         shape = x.shape
 
         def run(xd):

@@ -89,6 +89,13 @@ def test_argument_validation_without_gpu(lib):
     assert lib.sbq_argmax_rows(dummy, 1, 8, 4, dummy, None) == -1
     assert lib.sbq_argmax_rows(None, 1, 8, 8, dummy, None) == -1
     assert lib.sbq_argmax_rows(None, 0, 8, 8, None, None) == 0
+    # row / column counts beyond 2^31 - 1 are rejected before any launch
+    big = 1 << 31
+    assert lib.sbq_linear_w8(dummy, 0, big, 64, 64, dummy, dummy, None, 16, dummy, 0, 16, None, 0, None) == -1
+    assert lib.sbq_quantize_per_channel(dummy, 0, big, 4, 4, dummy, 4, dummy, None) == -1
+    assert lib.sbq_repack_w8(dummy, big, 64, 64, dummy, None, None) == -1
+    assert lib.sbq_unpack_w8(dummy, 16, big, dummy, big, None) == -1
+    assert lib.sbq_w8a8_workspace_bytes(big, 64) == 0
 
 
 def test_python_binding_maps_status_to_exceptions():

@@ -502,6 +502,40 @@ def test_int8_state_dict_roundtrip(dev):
     np.testing.assert_array_equal(lin2(x.to(dev)).cpu().numpy(), lin1(x.to(dev)).cpu().numpy())
 
 
+def test_mismatched_operands_raise_before_launch(dev):
+    """The C ABI sees raw pointers: the Python layer rejects operands whose
+    sizes, dtypes or devices do not match (N, K) before any kernel runs, and
+    the modules raise RuntimeError for an input that does not end in
+    in_features, as the reference's matmul does."""
+    announce("operand validation")
+    N, K, M = 64, 256, 3
+    w = make_weights(N, K, 51)
+    lin = quant.Int8Linear(w, None)
+    dyn = quant.DynamicInt8Linear(w, None)
+    x = make_x(M, K, 52).to(dev)
+    ok = quant.linear_w8(x, lin.packed, lin.scale, None, N)
+    with pytest.raises(ValueError):  # tiles of a smaller weight
+        quant.linear_w8(x, lin.packed[: quant.packed_bytes(N - 16, K)], lin.scale, None, N)
+    with pytest.raises(ValueError):  # scale too short
+        quant.linear_w8(x, lin.packed, lin.scale[:N - 1], None, N)
+    with pytest.raises(ValueError):  # fp16 bias
+        quant.linear_w8(x, lin.packed, lin.scale, torch.zeros(N, device=dev, dtype=torch.float16), N)
+    with pytest.raises(ValueError):  # output of the wrong shape
+        quant.linear_w8(x, lin.packed, lin.scale, None, N, out=torch.empty((M, N - 4), device=dev))
+    with pytest.raises(ValueError):  # x on the CPU
+        quant.linear_w8(x.cpu(), lin.packed, lin.scale, None, N)
+    with pytest.raises(ValueError):  # colsum too short
+        quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum[:8], None, N)
+    with pytest.raises(ValueError):
+        quant.linear_w8a8_token(x, dyn.packed, dyn.scale[:8], None, N)
+    with pytest.raises(ValueError):
+        quant.unpack(lin.packed[:1024], N, K)
+    for mod in (lin, dyn, quant.fuse_linears([lin, quant.Int8Linear(w, None)])):
+        with pytest.raises(RuntimeError):
+            mod(make_x(M, K + 64, 53).to(dev))
+    np.testing.assert_array_equal(quant.linear_w8(x, lin.packed, lin.scale, None, N).cpu().numpy(), ok.cpu().numpy())
+
+
 def test_cpu_tensors_in_and_out(dev):
     """The reference model feeds CPU fp32 [T, B, K] tensors and views the
     fp32 contiguous result (model.py:262-264): same contract here."""
