@@ -433,14 +433,17 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
 // 8-tile steps over one row tile for long K or narrow N, two waves per row tile
 // once M > 8 (the activation fragments then dominate the registers).  bf16
 // activations follow the fp16 rules; fp32 activations are copied to LDS and
-// split once into bf16 high / remainder planes when x fits.
+// split once into bf16 high / remainder planes when x fits, and otherwise take
+// direct steps with two row tiles per wave on wide layers (M = 4, N = 6144 and
+// 24576: 21-28% faster than one row tile).
 bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks) {
   if (M < 1 || M > 16 || K % 64 != 0 || !xvec) return false;
   const int64_t Kc = K / 64, Nt = (N + 15) / 16;
   if (xt == XT_F32) {
-    // x in LDS, split once into bf16 planes, when it fits; else 8- or 4-tile
-    // direct steps
-    *id = M * K * 4 <= kFastSplitBytes ? 0 : (Kc >= 128 ? 3 : 2);
+    // x in LDS, split once into bf16 planes, when it fits; else direct steps:
+    // 8 tiles over one row tile for long K, 4 tiles over two row tiles for
+    // wide layers, 4 tiles over one row tile otherwise
+    *id = M * K * 4 <= kFastSplitBytes ? 0 : (Kc >= 128 ? 3 : (Nt >= 384 ? 4 : 2));
     *ks = 4;
   } else if (M <= 8) {
     const bool wide = Kc < 128 && Nt >= 384;
