@@ -356,6 +356,22 @@ def prefill_probe(ctx, M=2048, N=12288, K=4096, launches=100):
     log(f"prefill probe: {launches} launches of M={M} N={N} K={K}")
 
 
+def w8a8_probe(ctx, M=2048, N=12288, K=4096, launches=100):
+    """The int8-dyn prefill operation alone (activation min/max and quantize
+    pre-passes + the i8 GEMM; fp16 x with 1% outlier channels, fp16 y), for
+    counter passes; enough back-to-back launches for the clock to settle."""
+    torch, quant = ctx.torch, ctx.quant
+    packed, s, cs = ctx.weights(N, K, 950, colsum=True)
+    x = ctx.act(M, K, 951, outliers=True)
+    y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
+    ws = quant.w8a8_workspace(M, K, ctx.dev)
+    torch.cuda.synchronize()
+    for _ in range(launches):
+        quant.linear_w8a8(x, packed, s, cs, None, N, torch.float16, workspace=ws, out=y)
+    torch.cuda.synchronize()
+    log(f"w8a8 probe: {launches} launches of M={M} N={N} K={K}")
+
+
 def summarize_counters(dirs, match, command):
     """Markdown table: per-dispatch averages of every counter collected in the
     rocprofv3 --pmc output directories, for kernels whose name contains match."""
@@ -519,6 +535,8 @@ def main():
                     help="print the traffic JSON from FETCH_SIZE and WRITE_SIZE passes over --traffic-probe")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only run the M=2048 prefill GEMM (workload of the prefill counter passes)")
+    ap.add_argument("--w8a8-probe", action="store_true",
+                    help="only run the M=2048 int8-dyn prefill (workload of the W8A8 counter passes)")
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
                     help="print per-dispatch counter averages from rocprofv3 --pmc directories")
     ap.add_argument("--match", default="gemm_dl_kernel", help="kernel-name filter for --summarize-counters")
@@ -534,8 +552,8 @@ def main():
         print(summarize_counters(args.summarize_counters, args.match, args.command), end="")
         return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported in this build "
-              "(the sharding design is described in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding of this path is a design note, not built)", file=sys.stderr)
         sys.exit(2)
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs one process on one GPU; WORLD_SIZE > 1 is not supported", file=sys.stderr)
@@ -548,6 +566,9 @@ def main():
         return
     if args.prefill_probe:
         prefill_probe(ctx)
+        return
+    if args.w8a8_probe:
+        w8a8_probe(ctx)
         return
     log("decode M=1 (headline)")
     head = decode_bench(ctx, 1, args.steps, args.warmup)

@@ -1,6 +1,6 @@
 """CPU oracle for the quantized-linear path (TEST INFRASTRUCTURE ONLY).
 
-This package is the checker the HIP kernels are compared against.  Only
+This package is the oracle the HIP kernels are compared against.  Only
 ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
 may import it; the product package (``sbq``) never does, and it never stands
 in for a GPU result.

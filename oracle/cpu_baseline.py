@@ -1,8 +1,8 @@
 """CPU baseline timing of the reference path (TEST/BENCH INFRASTRUCTURE ONLY).
 
-Used only by bench.py's cpu_baseline leg.  The reference's own files never
-travel to the GPU box, so this restates, with torch CPU operators, what the
-reference executes (paths relative to the reference repository):
+Used only by bench.py's cpu_baseline leg.  The reference's own files are not
+shipped with this package, so this restates, with torch CPU operators, what
+the reference executes (paths relative to the reference repository):
 
 * int8:     Int8Linear.forward, quant.py:46-53 - 128-row blocks dequantized to
             fp32, fp32 sgemm per block, torch.cat, then * scale.

@@ -1,7 +1,7 @@
 /*
  * sbq_oracle.c - CPU restatement of spikingbrain-cpu's quantized-linear path.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP kernels are
+ * TEST INFRASTRUCTURE ONLY.  This file is the oracle that the HIP kernels are
  * compared against; it is never linked into libsbq.so and never runs on the
  * product path.  Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg load it.

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/) before the GPU results are compared with it.
 
 Each oracle function is checked against something it does not share code
 with: torch's CPU operators evaluating the reference expressions
