@@ -746,3 +746,39 @@ def test_graph_replays_match_eager(dev):
             np.testing.assert_array_equal(outs[("dyn", i)].cpu().numpy(), eager_dyn.cpu().numpy(),
                                           err_msg=f"w8a8 replay {rep} M={x.shape[0]}")
         assert outs["tok"].item() == int(torch.argmax(outs[("w8", 0)][0]).item())
+
+
+# ---------------------------------------------------------------------------
+# concurrency: the library keeps no state, so calls on two streams at once
+# give the same results as the same calls one after the other
+# ---------------------------------------------------------------------------
+def test_concurrent_streams_match_sequential(dev):
+    announce("two streams")
+    K = 4096
+    layers = [quant.Int8Linear(make_weights(N, K, 160 + i), None) for i, N in enumerate((6144, 4096))]
+    dyns = [quant.DynamicInt8Linear(make_weights(N, K, 170 + i), None) for i, N in enumerate((4096, 1024))]
+    xs = [make_x(M, K, 180 + M).to(dev).half() for M in (1, 8, 300)]
+    # a workspace is scratch of one call at a time: one per stream and size
+    wss = {(i, M): quant.w8a8_workspace(M, K, dev) for i in range(2) for M in (1, 8, 300)}
+
+    def work(i, x):
+        lin, dyn = layers[i], dyns[i]
+        return (quant.linear_w8(x, lin.packed, lin.scale, None, lin.out_features),
+                quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, dyn.out_features,
+                                  workspace=wss[(i, x.shape[0])]))
+
+    ref = [[work(i, x) for x in xs] for i in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]  # default priority
+    got = [[None] * len(xs) for _ in range(2)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for j, x in enumerate(xs):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                got[i][j] = work(i, x)
+    torch.cuda.synchronize()
+    for i in range(2):
+        for j, x in enumerate(xs):
+            for a, b in zip(got[i][j], ref[i][j]):
+                np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy(), err_msg=f"stream {i} M={x.shape[0]}")
