@@ -4,17 +4,19 @@
 // quant.py:63-66 (DynamicInt8Linear.forward) for the prompt chunks the model
 // feeds (model.py:439: up to 512 tokens per chunk) and larger batches.
 //
-// Block tile BN (output channels) x BM (tokens) x 64 (K per stage), WN x WM
-// waves.  Each stage copies BN/16 packed weight tiles verbatim into LDS and the
-// BM x 64 activation slab into an XOR-swizzled LDS tile, straight from global
-// memory (LDS DMA); later stages land while MFMAs run on the current one (one
-// barrier per stage).
+// Block tile BN (output channels) x BM (tokens) x 64*KT (K per stage; KT = 2
+// on most W8A8 configurations), WN x WM waves.  Each stage copies BN/16 packed
+// weight tiles per K tile verbatim into LDS and the BM x 64 activation slab
+// into an XOR-swizzled LDS tile, straight from global memory (LDS DMA); later
+// stages land while MFMAs run on the current one (one barrier per stage).
 //   W-only: fp16 activations meet the weights as fp16 subnormals
 //           (q + 128) * 2^-24 (one v_perm per pair) and the epilogue removes
 //           128 * rowsum(x); bf16 activations meet exact bf16 weights.  Both
-//           run v_mfma_f32_16x16x32_{f16,bf16}; fp32 activations run as bf16
-//           hi + lo planes (register-staged kernel).  Epilogue: * scale[n]
-//           (+ bias[n]).
+//           run v_mfma_f32_16x16x32_{f16,bf16}.  With a workspace, fp32 and
+//           bf16 activations are first staged as row-scaled fp16 planes (fp32:
+//           hi + lo) for the fp16 kernel; without one, fp32 runs as bf16
+//           hi + lo planes in the register-staged kernel.  Epilogue:
+//           * scale[n] (+ bias[n]).
 //   W8A8:   the activations are quantized to s8 (xq - 128) once, by a
 //           pre-pass into the workspace; weights are used as s8,
 //           v_mfma_i32_16x16x64_i8 accumulates exactly; the epilogue adds
