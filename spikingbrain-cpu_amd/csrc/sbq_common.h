@@ -160,6 +160,14 @@ __device__ __forceinline__ void store_y(void* y, int ytype, int64_t idx, float v
   }
 }
 
+// Two 2-byte values in one dword, element 0 in the low half.
+__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+__device__ __forceinline__ uint32_t pack_b2(__bf16 a, __bf16 b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
 // Four consecutive outputs; `vec` says the 4-element group is in range and
 // aligned for one vector store.
 __device__ __forceinline__ void store_y4(void* y, int ytype, int64_t idx, f32x4 v, bool vec, int nvalid) {

@@ -831,3 +831,44 @@ def test_toy_model_fidelity_per_format(dev, T):
         assert cos > (0.95 if fmt == "int8-dyn" else 0.99), (fmt, cos)  # the reference's bar
         # the oracle's arithmetic in the same toy model reaches 0.99995 (int8-dyn) and 0.99998 (int8)
         assert cos > (0.999 if fmt == "int8-dyn" else 0.9999), (fmt, cos)
+
+
+# ---------------------------------------------------------------------------
+# fp16 / bf16 outputs of the prefill GEMM leave through an LDS-staged
+# epilogue; fp32 outputs are stored directly.  Both compute the same fp32
+# value, so the 2-byte output must equal the fp32 output rounded on the host,
+# for every block configuration, ragged M and N, and strided / misaligned rows.
+# ---------------------------------------------------------------------------
+def _bits(t):
+    """Raw 16-bit patterns of a 2-byte tensor (numpy has no bfloat16)."""
+    return t.contiguous().view(torch.int16).cpu().numpy()
+
+
+LEPI_CASES = [(2048, 12288, 128), (2048, 4096, 192), (1024, 4096, 256), (100, 1000, 320), (1000, 12290, 256),
+              (2048, 24576, 128), (256, 8192, 448)]
+
+
+@pytest.mark.parametrize("M,N,K", LEPI_CASES)
+def test_gemm_2byte_outputs_equal_rounded_fp32(dev, M, N, K):
+    announce(f"gemm 2-byte outputs M={M} N={N} K={K}")
+    w = make_weights(N, K, 4100 + N + K)
+    x = make_x(M, K, 4200 + M + K, outliers=True).half().to(dev)
+    lin = quant.Int8Linear(w, None)
+    dyn = quant.DynamicInt8Linear(w, None)
+    y32 = quant.linear_w8(x, lin.packed, lin.scale, None, N)
+    d32 = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N)
+    t32 = quant.linear_w8a8_token(x, dyn.packed, dyn.scale, None, N)
+    for od in (torch.float16, torch.bfloat16):
+        wide = torch.empty((M, N + 3), dtype=od, device=dev)
+        for out in (None, wide[:, :N]):  # dense rows; rows with an odd stride (no 16-byte stores)
+            got = quant.linear_w8(x, lin.packed, lin.scale, None, N, od, out=out)
+            np.testing.assert_array_equal(_bits(got), _bits(y32.to(od)))
+            got = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N, od, out=out)
+            np.testing.assert_array_equal(_bits(got), _bits(d32.to(od)))
+            got = quant.linear_w8a8_token(x, dyn.packed, dyn.scale, None, N, od, out=out)
+            np.testing.assert_array_equal(_bits(got), _bits(t32.to(od)))
+    xb = x.to(torch.bfloat16)  # bf16 activations without a workspace: the bf16 kernel
+    ref = quant.linear_w8(xb, lin.packed, lin.scale, None, N, workspace=torch.empty(0, dtype=torch.uint8, device=dev))
+    got = quant.linear_w8(xb, lin.packed, lin.scale, None, N, torch.bfloat16,
+                          workspace=torch.empty(0, dtype=torch.uint8, device=dev))
+    np.testing.assert_array_equal(_bits(got), _bits(ref.to(torch.bfloat16)))
