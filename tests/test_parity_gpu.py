@@ -872,3 +872,41 @@ def test_gemm_2byte_outputs_equal_rounded_fp32(dev, M, N, K):
     got = quant.linear_w8(xb, lin.packed, lin.scale, None, N, torch.bfloat16,
                           workspace=torch.empty(0, dtype=torch.uint8, device=dev))
     np.testing.assert_array_equal(_bits(got), _bits(ref.to(torch.bfloat16)))
+
+
+def test_graph_replays_lds_epilogue(dev):
+    """fp16 outputs of one-group GEMM blocks (the LDS-staged epilogue, W-only
+    and W8A8) replayed from a HIP graph with eager work between replays."""
+    announce("graph replays, LDS-staged epilogue")
+    M, N, K = 1024, 4096, 1024
+    w = make_weights(N, K, 190)
+    lin = quant.Int8Linear(w, None)
+    dyn = quant.DynamicInt8Linear(w, None)
+    x = make_x(M, K, 191).half().to(dev)
+    ws8 = quant.w8_workspace(M, K, dev)
+    wsd = quant.w8a8_workspace(M, K, dev)
+    y8 = torch.empty((M, N), dtype=torch.float16, device=dev)
+    yd = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+    def body():
+        quant.linear_w8(x, lin.packed, lin.scale, None, N, torch.float16, out=y8, workspace=ws8)
+        quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N, torch.float16, workspace=wsd, out=yd)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        body()
+    for rep in range(3):
+        x.mul_(-1.5).add_(0.25 * rep)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ref8 = quant.linear_w8(x, lin.packed, lin.scale, None, N).to(torch.float16)
+        refd = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N).to(torch.float16)
+        np.testing.assert_array_equal(_bits(y8), _bits(ref8), err_msg=f"w8 replay {rep}")
+        np.testing.assert_array_equal(_bits(yd), _bits(refd), err_msg=f"w8a8 replay {rep}")
