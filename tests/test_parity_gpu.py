@@ -910,3 +910,50 @@ def test_graph_replays_lds_epilogue(dev):
         refd = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N).to(torch.float16)
         np.testing.assert_array_equal(_bits(y8), _bits(ref8), err_msg=f"w8 replay {rep}")
         np.testing.assert_array_equal(_bits(yd), _bits(refd), err_msg=f"w8a8 replay {rep}")
+
+
+# ---------------------------------------------------------------------------
+# seeded random shapes: every dispatch path (fast / general GEMV, each GEMM
+# block configuration, the register-staged GEMM) against the oracle, with
+# random activation and output dtypes and aligned or misaligned row strides
+# ---------------------------------------------------------------------------
+def _random_cases(n, seed):
+    g = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        M = int(g.choice([1, 2, 3, 5, 8, 13, 16, 17, 31, 33, 64, 65, 100, 128, 200, 257, 300, 384]))
+        N = int(g.integers(1, 2049))
+        K = int(g.choice([int(g.integers(1, 2049)), 64 * int(g.integers(1, 33))]))
+        xd = str(g.choice(["f32", "f16", "bf16"]))
+        yd = str(g.choice(["f32", "f16", "bf16"]))
+        pad = int(g.choice([0, 0, 1, 8]))  # extra row elements; odd pads misalign the rows
+        cases.append((i, M, N, K, xd, yd, pad))
+    return cases
+
+
+@pytest.mark.parametrize("i,M,N,K,xd,yd,pad", _random_cases(40, 2024))
+def test_random_shapes_match_oracle(dev, i, M, N, K, xd, yd, pad):
+    announce(f"random case {i}: M={M} N={N} K={K} x={xd} y={yd} pad={pad}")
+    w = make_weights(N, K, 5000 + i)
+    xf = make_x(M, K, 5100 + i, outliers=True)
+    big = torch.zeros((M, K + pad), dtype=DT[xd])
+    big[:, pad:] = xf.to(DT[xd])
+    x = big.to(dev)[:, pad:]  # row stride K + pad, first row offset by pad elements
+    xv = x.float().cpu().numpy()
+    q, s = oracle.quantize_per_channel(w.numpy())
+    lin = quant.Int8Linear(w, None)
+    dyn = quant.DynamicInt8Linear(w, None)
+    # int8 weight-only: rel-L2 against the oracle.  fp32 outputs: the path's 1e-3, and fp32 summation order only
+    # for exact (fp16 / bf16) inputs; 2-byte outputs add one output rounding (rms 2^-11 / sqrt 3 for fp16,
+    # 2^-8 / sqrt 3 for bf16)
+    y = quant.linear_w8(x, lin.packed, lin.scale, None, N, DT[yd])
+    ref = oracle.int8_linear(xv, q, s)
+    err = oracle.rel_l2(y.float().cpu().numpy(), ref)
+    bound = {"f32": 2e-6 if xd != "f32" else W8_TOL, "f16": W8_TOL, "bf16": 5e-3}[yd]
+    assert err <= bound, err
+    # int8-dyn: int32 accumulators bit-exact, fp32 outputs bit-exact
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    yd8 = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N, acc_out=acc)
+    refd, info = oracle.dyn_linear(xv, q, s, return_intermediates=True)
+    np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
+    np.testing.assert_array_equal(yd8.cpu().numpy(), refd)
