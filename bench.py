@@ -590,7 +590,7 @@ def main():
         extra["prefill_other_x"] = [prefill_bench(ctx, 2048, xdtype=dt)
                                     for dt in (ctx.torch.bfloat16, ctx.torch.float32)]
         log("int8-dyn")
-        extra["w8a8"] = [w8a8_bench(ctx, M, N) for M in (1, 128, 2048) for N in (4096, 12288)]
+        extra["w8a8"] = [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)]
         log("36-layer linear stack")
         extra["stack"] = stack_bench(ctx)
         log("36-layer linear stack, layers reading the same input fused")

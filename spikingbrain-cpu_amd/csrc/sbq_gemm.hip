@@ -333,6 +333,20 @@ struct GemmArgs {
 template <int BN, int BM, int WN, int WM>
 constexpr int dl_min_waves() { return (BN / WN) * (BM / WM) > 64 * 64 ? 2 : 4; }
 
+// LDS bytes of one workgroup: the stage rings (or, after the K loop, the
+// cross-group reduction buffer / the staged output tile), plus the in-loop row
+// sums of fp16 W-only blocks without precomputed sums.
+template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP, int KT>
+constexpr int dl_lds_bytes() {
+  const int stage = KT * ((BN / 16) * 1024 + BM * (I8 ? 64 : 128));
+  const int red = (KG - 1) * WN * WM * (BN / WN / 16) * (BM / WM / 16) * 1024;
+  const int ldsb = KG * NS * stage > red ? KG * NS * stage : red;
+  const int epi = KG == 1 ? BM * (BN * 2 + 32) : 0;
+  const bool rsk = !I8 && XT == XT_F16 && !RSP;
+  return (epi > ldsb ? epi : ldsb) + (rsk ? KG * BM * 4 : 0);
+}
+constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950: LDS per workgroup
+
 // RSP (fp16 W-only): the per-row sums of x come precomputed in a.rsum instead
 // of being accumulated in the K loop.
 // KT (W8A8, one K group): K tiles per stage.  An i8 MFMA covers a whole 64-wide
@@ -373,6 +387,7 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   // one LDS object: with a second one the compiler waits for every stage DMA in
   // flight before any LDS read of the main loop (it cannot tell them apart)
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDSA + (RSK ? KG * BM * 4 : 0)];
+  static_assert(sizeof(lds) == dl_lds_bytes<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>(), "launcher's LDS model");
   float* const rsum_lds = (float*)(lds + LDSA);
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -650,11 +665,15 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
 
 template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false, int KT = 1>
 int launch_dl(const GemmArgs& a, hipStream_t st) {
-  if (a.Kc % KT) return -1;
-  const dim3 grid((unsigned)((a.Nt + BN / 16 - 1) / (BN / 16)), (unsigned)((a.M + BM - 1) / BM));
-  hipLaunchKernelGGL((gemm_dl_kernel<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>), grid, dim3(KG * WN * WM * 64), 0, st,
-                     a);
-  return check_launch();
+  if constexpr (dl_lds_bytes<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>() > kMaxLdsBytes) {
+    return -1;  // no such kernel: its LDS would not fit (the pickers never ask for it)
+  } else {
+    if (a.Kc % KT) return -1;
+    const dim3 grid((unsigned)((a.Nt + BN / 16 - 1) / (BN / 16)), (unsigned)((a.M + BM - 1) / BM));
+    hipLaunchKernelGGL((gemm_dl_kernel<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>), grid, dim3(KG * WN * WM * 64), 0,
+                       st, a);
+    return check_launch();
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -751,7 +770,11 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restric
   X(9, 128, 64, 2, 2, 3, 2)  \
   X(10, 256, 128, 4, 1, 2, 1) \
   X(11, 128, 256, 2, 2, 2, 1) \
-  X(12, 256, 256, 4, 2, 2, 1)
+  X(12, 256, 256, 4, 2, 2, 1) \
+  X(16, 192, 64, 4, 1, 2, 1)  \
+  X(17, 192, 64, 4, 1, 2, 4)  \
+  X(18, 192, 128, 4, 1, 2, 1) \
+  X(19, 192, 128, 4, 1, 3, 1)
 
 template <bool I8, int XT>
 int launch_dl_id(int id, const GemmArgs& a, hipStream_t st) {
@@ -774,6 +797,9 @@ int launch_dl_rsp(int id, const GemmArgs& a, hipStream_t st) {
     case 5: return launch_dl<false, XT_F16, 128, 64, 2, 2, 2, 4, true>(a, st);
     case 8: return launch_dl<false, XT_F16, 64, 64, 1, 2, 2, 4, true>(a, st);
     case 10: return launch_dl<false, XT_F16, 256, 128, 4, 1, 2, 1, true>(a, st);
+    case 16: return launch_dl<false, XT_F16, 192, 64, 4, 1, 2, 1, true>(a, st);
+    case 17: return launch_dl<false, XT_F16, 192, 64, 4, 1, 2, 4, true>(a, st);
+    case 18: return launch_dl<false, XT_F16, 192, 128, 4, 1, 2, 1, true>(a, st);
   }
   if (a.rscale) return -1;  // staged activations need the row scale: only the configurations above apply it
   GemmArgs b = a;
@@ -781,8 +807,8 @@ int launch_dl_rsp(int id, const GemmArgs& a, hipStream_t st) {
   return launch_dl_id<false, XT_F16>(id, b, st);
 }
 
-// W8A8 configurations with two K tiles per stage (ids 13-15); an odd number of
-// K tiles takes the one-tile configuration of the same block shape.
+// W8A8 configurations with two K tiles per stage (ids 13-15, 20); an odd number
+// of K tiles takes the one-tile configuration of the same block shape.
 int launch_dl_i8(int id, const GemmArgs& a, hipStream_t st) {
   const bool kt2 = a.Kc % 2 == 0;
   switch (id) {
@@ -792,6 +818,8 @@ int launch_dl_i8(int id, const GemmArgs& a, hipStream_t st) {
       return kt2 ? launch_dl<true, XT_F16, 128, 128, 2, 2, 2, 1, false, 2>(a, st) : launch_dl_id<true, XT_F16>(2, a, st);
     case 15:
       return kt2 ? launch_dl<true, XT_F16, 128, 64, 2, 2, 2, 1, false, 2>(a, st) : launch_dl_id<true, XT_F16>(3, a, st);
+    case 20:
+      return kt2 ? launch_dl<true, XT_F16, 192, 64, 4, 1, 2, 1, false, 2>(a, st) : launch_dl_id<true, XT_F16>(16, a, st);
   }
   return launch_dl_id<true, XT_F16>(id, a, st);
 }
@@ -799,37 +827,43 @@ int launch_dl_i8(int id, const GemmArgs& a, hipStream_t st) {
 // Launch of direct-to-LDS configuration `id` (tuning entry; -1: no such id).
 int launch_gemm_dl_cfg(int id, bool i8, int xt, const GemmArgs& a, hipStream_t st) {
   if (i8) return launch_dl_i8(id, a, st);
-  if (xt == XT_F16) return a.rsum ? launch_dl_rsp(id, a, st) : launch_dl_id<false, XT_F16>(id, a, st);
+  // 192 x 64 blocks with K split over 4 wave groups leave no LDS for the
+  // in-loop row sums: without precomputed sums the 128 x 64 split runs
+  if (xt == XT_F16) return a.rsum ? launch_dl_rsp(id, a, st) : launch_dl_id<false, XT_F16>(id == 17 ? 5 : id, a, st);
   if (xt == XT_BF16) return launch_dl_id<false, XT_BF16>(id, a, st);
   return -2;
 }
 
-// Configuration for a shape (measured on MI355X, K = 4096, M 128..8192,
-// N 1024..24576): big grids take 256 x 128 blocks, mid-size grids 128 x 128
-// or 128 x 64 blocks; grids that leave CUs short of waves take 128 x 64 or
-// 64 x 64 blocks with K split over 4 wave groups inside the workgroup.  bf16 W-only keeps 64 x 128 wave tiles on the largest grids
-// (half the conversion work per MFMA).
+// Configuration for a shape, by the number of 256 x 128 blocks the output
+// takes (t256).  A CU's throughput is about the same with one or two
+// workgroups of a configuration, so the kernel time follows the busiest CU's
+// share of the grid: each range below picks the block shape whose grid splits
+// most evenly over the 256 CUs (192-row blocks turn 1.5 blocks per CU into 2,
+// 0.75 into 1), and grids too small for two workgroups per CU split K over 4
+// wave groups inside the workgroup.  Measured on MI355X over K = 4096 and
+// 12288, M = 256..4096, N = 2048..24576: the best of 10 (fp16) / 11 (W8A8)
+// configurations, or within 4% of it, at every point.  bf16 W-only keeps
+// 64 x 128 wave tiles on the largest grids (half the conversion work per MFMA).
 int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt) {
   const int64_t t256 = ((Nt + 15) / 16) * ((M + 127) / 128);
-  const int64_t t128 = ((Nt + 7) / 8) * ((M + 127) / 128);
   const int64_t t128x64 = ((Nt + 7) / 8) * ((M + 63) / 64);
   if (i8) {
-    // measured over M = 128..8192, N = 4096..24576: two K tiles per stage
-    // except on 256 x 128 blocks, which take three one-tile stages instead
-    if (t256 >= 1536) return 13;   // 256 x 256
-    if (t256 >= 512) return 1;     // 256 x 128
-    if (t128 >= 256) return 14;    // 128 x 128
-    if (t128x64 >= 256) return 15; // 128 x 64
-    return 8;                      // 64 x 64, K split over 4 wave groups
+    // two K tiles per stage except on 192 x 128 blocks (three one-tile stages)
+    if (t256 >= 1024 || (t256 >= 448 && t256 < 704)) return 13;  // 256 x 256
+    if (t256 >= 320) return 19;                                   // 192 x 128
+    if (t256 >= 224) return 14;                                   // 128 x 128
+    if (t256 >= 160) return 20;                                   // 192 x 64
+    if (t256 >= 80) return 15;                                    // 128 x 64
+    return 8;                                                     // 64 x 64, K split over 4 wave groups
   }
   if (xt == XT_F16) {
-    // measured over M = 256..8192, N = 4096..24576: the block size that keeps
-    // every CU busy with whole workgroups wins below M ~ 2048
-    if (t256 >= 768) return 0;
-    if (t128 >= 512) return 2;
-    if (t128x64 >= 384) return 3;
-    if (t128x64 >= 128) return 5;
-    return 8;
+    if (t256 >= 448 || (t256 >= 224 && t256 < 320)) return 0;  // 256 x 128
+    if (t256 >= 320) return 18;                                 // 192 x 128
+    if (t256 >= 160) return 16;                                 // 192 x 64
+    if (t256 >= 112) return 3;                                  // 128 x 64
+    if (t256 >= 80) return 17;                                  // 192 x 64, K split over 4 wave groups
+    if (t256 >= 40) return 5;                                   // 128 x 64, K split over 4 wave groups
+    return 8;                                                   // 64 x 64, K split over 4 wave groups
   }
   if (t256 >= 1536) return 10;
   if (t256 >= 256 || t128x64 >= 512) return 0;

@@ -150,6 +150,36 @@ def test_w8_f16_prefill_row_sum_paths(dev, M, N, K):
         assert e_pre <= bound and e_loop <= bound, (positive, e_pre, e_loop)
 
 
+# fp16 W-only GEMM block configurations, chosen by the number t256 of 256x128
+# blocks the output takes (short K keeps the oracle fast): 256x128 (t256 = 256
+# and 768), 192x128 (384), 192x64 (192), 128x64 (128), 192x64 with K split over
+# 4 wave groups (96; without precomputed row sums the 128x64 split runs), 128x64
+# split (64), 64x64 split (4); ragged M and N.
+W8_GEMM_CFG = [(2048, 4096, 128), (2048, 12288, 128), (1024, 12288, 192), (1000, 12290, 256), (512, 12288, 256),
+               (500, 12300, 192), (512, 8192, 256), (512, 6144, 320), (450, 6100, 320), (256, 8192, 448),
+               (100, 1000, 320)]
+
+
+@pytest.mark.parametrize("M,N,K", W8_GEMM_CFG)
+def test_w8_gemm_block_configs(dev, M, N, K):
+    """Every fp16 W-only block configuration, with row sums from the pre-pass
+    (workspace), from the K loop (no workspace), and over fp32 activations
+    staged as fp16 planes; the activations are fp16 values, so all three must
+    match the oracle to fp32 summation order."""
+    announce(f"w8 gemm config M={M} N={N} K={K}")
+    w = make_weights(N, K, 7300 + N + K)
+    x = make_x(M, K, 7400 + M + K).half()
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref = oracle.int8_linear(x.float().numpy(), q, s)
+    lin = quant.Int8Linear(w, None)
+    xd = x.to(dev)
+    none = torch.empty(0, dtype=torch.uint8, device=dev)
+    for xin, ws in ((xd, None), (xd, none), (xd.float(), None)):
+        y = quant.linear_w8(xin, lin.packed, lin.scale, None, N, workspace=ws)
+        err = oracle.rel_l2(y.cpu().numpy(), ref)
+        assert err <= 2e-6, (xin.dtype, ws is None, err)
+
+
 @pytest.mark.parametrize("xd", ["f32", "bf16"])
 @pytest.mark.parametrize("M,N,K", [(64, 512, 2560), (200, 130, 4096), (512, 2048, 512), (300, 4096, 4096)])
 def test_w8_staged_prefill_rows(dev, M, N, K, xd):
@@ -292,12 +322,15 @@ def test_w8a8_bitexact(dev, M, N, K, xd):
     assert (np.float32(sx), zp) == (np.float32(info["scale"]), info["zero_point"])
 
 
-# W8A8 GEMM block configurations, chosen by grid size (short K keeps the oracle
-# fast): 256x256 blocks with two K tiles per stage, and its one-tile fallback
-# for an odd tile count; 256x128 with three stages; 128x128 and 128x64 with two
-# K tiles per stage and their odd-count fallbacks; ragged M and N.
-W8A8_GEMM_CFG = [(2048, 24576, 128), (2048, 24576, 192), (1024, 24576, 256), (512, 12288, 256), (512, 12288, 320),
-                 (256, 8192, 512), (256, 8192, 448), (1000, 12290, 256)]
+# W8A8 GEMM block configurations, chosen by the number t256 of 256x128 blocks
+# the output takes (short K keeps the oracle fast): 256x256 blocks with two K
+# tiles per stage (t256 >= 1024) and its one-tile fallback for an odd tile
+# count; 192x128 with three stages (t256 = 768 and 384); 128x128 (256),
+# 192x64 (192) and 128x64 (128) with two K tiles per stage and their odd-count
+# fallbacks; 64x64 with K split over 4 wave groups (64); ragged M and N.
+W8A8_GEMM_CFG = [(2048, 24576, 128), (2048, 24576, 192), (2048, 12288, 128), (1024, 12288, 256), (1024, 8192, 256),
+                 (1024, 8192, 320), (512, 12288, 256), (512, 12288, 320), (512, 8192, 256), (512, 8192, 448),
+                 (256, 8192, 448), (1000, 12290, 256), (500, 12300, 192)]
 
 
 @pytest.mark.parametrize("M,N,K", W8A8_GEMM_CFG)
@@ -314,7 +347,7 @@ def test_w8a8_gemm_block_configs(dev, M, N, K):
     np.testing.assert_array_equal(y.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 24576, 128), (1000, 12290, 256), (256, 8192, 448)])
+@pytest.mark.parametrize("M,N,K", [(2048, 24576, 128), (1000, 12290, 256), (512, 12288, 256), (256, 8192, 448)])
 def test_w8a8_token_gemm_block_configs(dev, M, N, K):
     announce(f"w8a8 token gemm config M={M} N={N} K={K}")
     w = make_weights(N, K, 3900 + N + K)
@@ -845,7 +878,7 @@ def _bits(t):
 
 
 LEPI_CASES = [(2048, 12288, 128), (2048, 4096, 192), (1024, 4096, 256), (100, 1000, 320), (1000, 12290, 256),
-              (2048, 24576, 128), (256, 8192, 448)]
+              (2048, 24576, 128), (256, 8192, 448), (512, 12288, 256), (500, 12300, 192), (512, 6144, 320)]
 
 
 @pytest.mark.parametrize("M,N,K", LEPI_CASES)
