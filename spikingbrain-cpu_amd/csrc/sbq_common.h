@@ -147,6 +147,21 @@ __device__ __forceinline__ void split_bf16(float v, __bf16& hi, __bf16& lo) {
   lo = (__bf16)(v - (float)hi);
 }
 
+// Exponent e of the power-of-two row scale that puts a row's largest
+// magnitude mx into [2^14, 2^15) before the row is split into fp16 planes
+// (exact scaling; no fp16 overflow, at most 2^28 of range lost to
+// subnormals below the maximum).  Rows with no finite nonzero maximum keep
+// e = 0.
+__device__ __forceinline__ int row_scale_exp(float mx) {
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.4028235e38f) {
+    int ex;
+    (void)frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+    e = min(max(15 - ex, -112), 120);
+  }
+  return e;
+}
+
 // ---------------------------------------------------------------------------
 // Output element store
 // ---------------------------------------------------------------------------

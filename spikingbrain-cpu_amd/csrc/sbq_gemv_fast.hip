@@ -42,7 +42,7 @@ constexpr int kFastXLdsBytes = 32768;  // x[M][K] copied to LDS up to this size
 constexpr int kFastMaxWaves = 8;
 constexpr int kFusedChunks = 4;         // QM 2: 16-byte chunks of x per thread
 constexpr int kFusedMinWaves = 4;       // QM 2: x <= kFusedChunks * 16 * 64 * waves bytes
-constexpr int kFastSplitBytes = 24576;  // fp32 x split into bf16 planes in LDS up to this size
+constexpr int kFastSplitBytes = 49152;  // fp32 x split into bf16 planes in LDS up to this size
 
 __device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
@@ -401,15 +401,13 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   if (w8a8 && ks * 64 < a.nparts) return -1;  // one min/max partial per thread
   const int eb = xt == XT_F32 ? 4 : 2;
   const int64_t xbytes = (int64_t)a.M * a.K * eb;
-  if (c.XL && xbytes > kFastXLdsBytes) return -1;
+  const bool split = c.XL && xt == XT_F32 && !w8a8;  // fp32 x: raw copy + bf16 planes
+  if (c.XL && xbytes > (split ? kFastSplitBytes : kFastXLdsBytes)) return -1;
   if (c.D * c.G > 32) return -1;
   const int T = ks * 64;
   const int xch = c.XL ? (int)((xbytes / 16 + T - 1) / T) : 0;
   size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
-  if (c.XL && xt == XT_F32 && !w8a8) {  // bf16 high / remainder planes
-    if (xbytes > kFastSplitBytes) return -1;
-    lds += (size_t)a.M * a.K * 4;
-  }
+  if (split) lds += (size_t)a.M * a.K * 4;  // bf16 high / remainder planes
   const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
   if (qm == 2 && (xbytes > (int64_t)kFusedChunks * 16 * T || ks < kFusedMinWaves)) return -1;
 #define SBQ_FAST_QM(XT_)                                                  \
@@ -440,11 +438,16 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
   if (M < 1 || M > 16 || K % 64 != 0 || !xvec) return false;
   const int64_t Kc = K / 64, Nt = (N + 15) / 16;
   if (xt == XT_F32) {
-    // x in LDS, split once into bf16 planes, when it fits; else direct steps:
-    // 8 tiles over one row tile for long K, 4 tiles over two row tiles for
-    // wide layers, 4 tiles over one row tile otherwise
-    *id = M * K * 4 <= kFastSplitBytes ? 0 : (Kc >= 128 ? 3 : (Nt >= 384 ? 4 : 2));
-    *ks = 4;
+    // x in LDS (weight-only: split once into bf16 planes) when it fits 24 KiB,
+    // or 48 KiB for one row (M = 1, K = 12288: 16% faster than direct steps;
+    // the raw copy and the planes then hold 96 KiB of LDS, one workgroup per
+    // CU); 8 waves per row tile for long K.  Else direct steps: 8 tiles over
+    // one row tile for long K, 4 tiles over two row tiles for wide layers, 4
+    // tiles over one row tile otherwise.
+    const int64_t xb = M * K * 4;
+    const bool xl = xb <= 24576 || (!w8a8 && M == 1 && xb <= kFastSplitBytes);
+    *id = xl ? 0 : (Kc >= 128 ? 3 : (Nt >= 384 ? 4 : 2));
+    *ks = xl && Kc >= 128 ? 8 : 4;
   } else if (M <= 8) {
     const bool wide = Kc < 128 && Nt >= 384;
     *id = wide ? 4 : 3;  // D=4, G=2 | D=8, G=1

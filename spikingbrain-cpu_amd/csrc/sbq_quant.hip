@@ -262,12 +262,7 @@ __global__ __launch_bounds__(256) void stage_act_kernel(const void* __restrict__
     for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(t[j]));
   }
   mx = wave_max(mx);
-  int e = 0;
-  if (mx > 0.0f && mx <= 3.4028235e38f) {
-    int ex;
-    (void)frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
-    e = min(max(15 - ex, -112), 120);
-  }
+  const int e = row_scale_exp(mx);
   const float sc = ldexpf(1.0f, e);
   _Float16* out = xs + (int64_t)row * NP * K;
   float s0 = 0.0f, s1 = 0.0f;

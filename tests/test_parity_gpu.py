@@ -219,6 +219,37 @@ def test_w8_low_precision_output(dev, M, yd):
     assert oracle.rel_l2(y.float().cpu().numpy(), ref) <= 4e-3
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 12288), (1, 6144, 4096), (1, 24, 128), (2, 300, 6144), (3, 1000, 4096)])
+def test_w8_decode_fp32_rows_split(dev, M, N, K):
+    """fp32 decode activations run as bf16 hi + remainder (16 significant bits,
+    fp32 range): a single row that fits in LDS is split once, in place; several
+    rows are split per tile.  Rows of 1e-30, 1 and 1e30 magnitude each match
+    the oracle to that precision; a NaN poisons its own row only."""
+    bound = 2e-5
+    announce(f"w8 fp32 split M={M} N={N} K={K}")
+    w = make_weights(N, K, 7600 + N + K)
+    b = torch.randn(N)
+    q, s = oracle.quantize_per_channel(w.numpy())
+    lin = quant.Int8Linear(w, b)
+    base = make_x(M, K, 7700 + M + K, outliers=True)
+    for shift in range(3):
+        scales = torch.tensor([[1e-30], [1.0], [1e30]]).roll(shift, 0)[:M] if M > 1 else \
+            torch.tensor([[(1e-30, 1.0, 1e30)[shift]]])
+        x = (base * scales).float()
+        ref = oracle.int8_linear(x.numpy(), q, s)
+        y = quant.linear_w8(x.to(dev), lin.packed, lin.scale, None, N).cpu().numpy()
+        for m in range(M):
+            err = oracle.rel_l2(y[m], ref[m])
+            assert err <= bound, (shift, m, err)
+    x = base.clone()
+    x[0, K // 3] = float("nan")
+    y = quant.linear_w8(x.to(dev), lin.packed, lin.scale, lin.bias, N).cpu().numpy()
+    assert np.isnan(y[0]).all()
+    if M > 1:
+        ref = oracle.int8_linear(x[1:].numpy(), q, s, b.numpy())
+        assert oracle.rel_l2(y[1:], ref) <= bound
+
+
 def test_w8_bias_and_strided_input(dev):
     announce("w8 bias + strided")
     N, K, M = 96, 512, 20
