@@ -40,7 +40,7 @@ namespace {
 
 constexpr int kFastXLdsBytes = 32768;  // x[M][K] copied to LDS up to this size
 constexpr int kFastMaxWaves = 8;
-constexpr int kFusedChunks = 4;         // QM 2: 16-byte chunks of x per thread
+constexpr int kFusedChunks = 8;         // QM 2: 16-byte chunks of x per thread (at most)
 constexpr int kFusedMinWaves = 4;       // QM 2: x <= kFusedChunks * 16 * 64 * waves bytes
 constexpr int kFastSplitBytes = 49152;  // fp32 x split into bf16 planes in LDS up to this size
 
@@ -139,15 +139,19 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
     }
   }
   // W8A8: min/max partials of the activation pre-pass, or (QM 2) up to
-  // kFusedChunks 16-byte chunks of x per thread; duplicates are harmless
+  // kFusedChunks 16-byte chunks of x per thread: chunk rounds past the end
+  // of x are skipped (the condition is uniform over the workgroup), and the
+  // clamped duplicates of a partial round are harmless
   float2 part = {0.f, 0.f};
   u32x4 xmm[QM == 2 ? kFusedChunks : 1];
+  const int xm_nch = M * (K * EB / 16);  // QM 2: 16-byte chunks of x
   if constexpr (QM == 1) part = a.partials[min(tid, a.nparts - 1)];
   if constexpr (QM == 2) {
-    const int cpr = K * EB / 16, nch = M * cpr;
+    const int cpr = K * EB / 16;
 #pragma unroll
     for (int i = 0; i < kFusedChunks; ++i) {
-      const int c = min(tid + i * (int)blockDim.x, nch - 1);
+      if (i * (int)blockDim.x >= xm_nch) break;
+      const int c = min(tid + i * (int)blockDim.x, xm_nch - 1);
       const int m = c / cpr;
       xmm[i] = *(const u32x4*)((const uint8_t*)a.x + (int64_t)m * a.ldx * EB + (c - m * cpr) * 16);
     }
@@ -186,6 +190,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       float mn = 0.0f, mx = 0.0f;
 #pragma unroll
       for (int i = 0; i < kFusedChunks; ++i) {
+        if (i * (int)blockDim.x >= xm_nch) break;
         constexpr int NE = 16 / EB;
 #pragma unroll
         for (int j = 0; j < NE; ++j) {
@@ -461,7 +466,14 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     *id = wide ? 5 : 3;  // D=8, G=2 | D=8, G=1
     *ks = 2;
   }
-  if (w8a8 && *ks < kFusedMinWaves) *ks = kFusedMinWaves;  // 256 threads cover the min/max partials / fused x
+  if (w8a8) {
+    // the activation min/max is reduced in the kernel for x <= 64 KiB (up to
+    // 8 chunks of 16 bytes per thread, one pre-pass launch less: M = 1..4
+    // decode 8-24% faster); 8 waves beyond 32 KiB and on the widest layers
+    const int64_t xb = M * K * (xt == XT_F32 ? 4 : 2);
+    if (xb > 16384 && xb <= 65536 && (xb > 32768 || Nt >= 1024)) *ks = 8;
+    if (*ks < kFusedMinWaves) *ks = kFusedMinWaves;  // 256 threads cover the min/max partials / fused x
+  }
   return true;
 }
 
