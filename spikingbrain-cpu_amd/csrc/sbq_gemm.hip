@@ -682,25 +682,25 @@ int launch_dl(const GemmArgs& a, hipStream_t st) {
 // meet zero weights); gemm_w8a8_dl_kernel then runs the direct-to-LDS
 // pipeline on s8 operands with v_mfma_i32_16x16x64_i8.
 // ---------------------------------------------------------------------------
-constexpr int kQuantChunks = 4;
-
-// VEC: 16-byte aligned rows and K % 16 == 0 (every chunk is whole, branch-free loads)
-template <int XT, bool VEC>
+// VEC: 16-byte aligned rows and K % 16 == 0 (every chunk is whole, branch-free loads).
+// QC: 16-element chunks per thread (1 for small x, so that the grid still
+// covers every CU).
+template <int XT, bool VEC, int QC>
 __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restrict__ x, int64_t ldx, int M, int K,
                                                            int Kp, const float2* __restrict__ partials, int nparts,
                                                            int8_t* __restrict__ xq, float* __restrict__ qp_out,
                                                            int flags) {
-  // kQuantChunks 16-element chunks per thread, chunk i of the block at
-  // (block * kQuantChunks + i) * 256 + thread.  The activation loads go out
+  // QC 16-element chunks per thread, chunk i of the block at
+  // (block * QC + i) * 256 + thread.  The activation loads go out
   // first; the (latency-bound) reduction of the partials and fbgemm's
   // double-precision parameter choice run while they are in flight.
   const int cpr = Kp / 16;
   const int64_t nch = (int64_t)M * cpr;
-  float t[kQuantChunks][16];
-  int64_t cc[kQuantChunks];
+  float t[QC][16];
+  int64_t cc[QC];
 #pragma unroll
-  for (int i = 0; i < kQuantChunks; ++i) {
-    cc[i] = ((int64_t)blockIdx.x * kQuantChunks + i) * blockDim.x + threadIdx.x;
+  for (int i = 0; i < QC; ++i) {
+    cc[i] = ((int64_t)blockIdx.x * QC + i) * blockDim.x + threadIdx.x;
     const int64_t c = min(cc[i], nch - 1);  // clamped: surplus chunks are loaded but not stored
     const int m = (int)(c / cpr), k0 = (int)(c - (int64_t)m * cpr) * 16;
     if constexpr (VEC) {
@@ -737,7 +737,7 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restric
     qp_out[1] = __int_as_float(qp.zp);
   }
 #pragma unroll
-  for (int i = 0; i < kQuantChunks; ++i) {
+  for (int i = 0; i < QC; ++i) {
     if (cc[i] >= nch) break;
     const int m = (int)(cc[i] / cpr), k0 = (int)(cc[i] - (int64_t)m * cpr) * 16;
     uint32_t d[4];
@@ -951,15 +951,25 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
   if (prc) return prc;
   const int flags = (xvec ? 1 : 0) | (yvec ? 2 : 0) | y16_flag(y, yt, ldy);
   const int64_t chunks = M * (Kp / 16);
-  const dim3 qgrid((unsigned)((chunks + 256 * kQuantChunks - 1) / (256 * kQuantChunks)));
+  // chunks per thread: 4 once that still gives >= 512 workgroups, 2 from 256
+  // workgroups, else 1 (measured at K = 4096: M = 128 4.2 -> 3.1 us, M = 512
+  // 4.4 -> 3.7 us, M = 2048 unchanged)
+  const int qc = chunks >= (int64_t)256 * 4 * 512 ? 4 : (chunks >= (int64_t)256 * 2 * 256 ? 2 : 1);
+  const dim3 qgrid((unsigned)((chunks + 256 * qc - 1) / (256 * qc)));
   const bool qvec = xvec && K % 16 == 0;
-#define SBQ_QUANT_LAUNCH(XT_)                                                                                       \
-  if (qvec)                                                                                                           \
-    hipLaunchKernelGGL((quantize_act_kernel<XT_, true>), qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp,    \
-                       partials, nparts, xq, qpbuf, flags);                                                          \
-  else                                                                                                                \
-    hipLaunchKernelGGL((quantize_act_kernel<XT_, false>), qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp,   \
-                       partials, nparts, xq, qpbuf, flags);
+#define SBQ_QUANT_LAUNCH1(XT_, VEC_, QC_)                                                                          \
+  hipLaunchKernelGGL((quantize_act_kernel<XT_, VEC_, QC_>), qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp, \
+                     partials, nparts, xq, qpbuf, flags);
+#define SBQ_QUANT_LAUNCH(XT_)                       \
+  if (qvec) {                                       \
+    if (qc == 4) SBQ_QUANT_LAUNCH1(XT_, true, 4)    \
+    else if (qc == 2) SBQ_QUANT_LAUNCH1(XT_, true, 2) \
+    else SBQ_QUANT_LAUNCH1(XT_, true, 1)            \
+  } else {                                          \
+    if (qc == 4) SBQ_QUANT_LAUNCH1(XT_, false, 4)   \
+    else if (qc == 2) SBQ_QUANT_LAUNCH1(XT_, false, 2) \
+    else SBQ_QUANT_LAUNCH1(XT_, false, 1)           \
+  }
   switch (xt) {
     case XT_F16: SBQ_QUANT_LAUNCH(XT_F16) break;
     case XT_BF16: SBQ_QUANT_LAUNCH(XT_BF16) break;
@@ -967,6 +977,7 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
     default: return -2;
   }
 #undef SBQ_QUANT_LAUNCH
+#undef SBQ_QUANT_LAUNCH1
   int rc = check_launch();
   if (rc) return rc;
   GemmArgs a{};
