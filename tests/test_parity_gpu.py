@@ -1021,3 +1021,43 @@ def test_random_shapes_match_oracle(dev, i, M, N, K, xd, yd, pad):
     refd, info = oracle.dyn_linear(xv, q, s, return_intermediates=True)
     np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
     np.testing.assert_array_equal(yd8.cpu().numpy(), refd)
+
+
+def _random_prefill_cases(n, seed):
+    """Prefill-sized shapes (grids of every block configuration), M*N*K <= 3e9."""
+    g = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        while True:
+            M = int(g.choice([33, 100, 128, 250, 256, 384, 500, 512, 640, 1000, 1024, 1536, 2048]))
+            N = int(g.choice([int(g.integers(16, 16385)), 16 * int(g.integers(1, 1025)), 4096, 6144, 12288]))
+            K = 64 * int(g.integers(1, 33)) if g.random() < 0.8 else int(g.integers(1, 2049))
+            if M * N * K <= 3 * 10 ** 9:
+                break
+        xd = str(g.choice(["f32", "f16", "bf16"]))
+        ws = str(g.choice(["auto", "none"]))
+        cases.append((i, M, N, K, xd, ws))
+    return cases
+
+
+@pytest.mark.parametrize("i,M,N,K,xd,ws", _random_prefill_cases(40, 2025))
+def test_random_prefill_shapes_match_oracle(dev, i, M, N, K, xd, ws):
+    """Seeded prefill shapes across the GEMM block configurations, with and
+    without a workspace: W-only to fp32 summation order for fp16 / bf16
+    inputs (1e-3 for fp32 inputs), W8A8 acc and y bit-exact."""
+    announce(f"random prefill case {i}: M={M} N={N} K={K} x={xd} ws={ws}")
+    w = make_weights(N, K, 5200 + i)
+    x = make_x(M, K, 5300 + i, outliers=True).to(DT[xd]).to(dev)
+    xv = x.float().cpu().numpy()
+    q, s = oracle.quantize_per_channel(w.numpy())
+    lin = quant.Int8Linear(w, None)
+    dyn = quant.DynamicInt8Linear(w, None)
+    kw = {} if ws == "auto" else {"workspace": torch.empty(0, dtype=torch.uint8, device=dev)}
+    y = quant.linear_w8(x, lin.packed, lin.scale, None, N, **kw)
+    err = oracle.rel_l2(y.cpu().numpy(), oracle.int8_linear(xv, q, s))
+    assert err <= (2e-6 if xd != "f32" else W8_TOL), err
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    yd8 = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N, acc_out=acc)
+    refd, info = oracle.dyn_linear(xv, q, s, return_intermediates=True)
+    np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
+    np.testing.assert_array_equal(yd8.cpu().numpy(), refd)
