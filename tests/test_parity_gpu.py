@@ -812,6 +812,56 @@ def test_graph_replays_match_eager(dev):
         assert outs["tok"].item() == int(torch.argmax(outs[("w8", 0)][0]).item())
 
 
+def test_graph_replays_size_dependent_paths(dev):
+    """Paths chosen by activation size, replayed from a HIP graph with new
+    activations written between replays: the in-kernel W8A8 min/max over 24
+    and 48 KiB of x, the prefill quantizer at 1 and 2 chunks per thread with
+    256- and 512-thread min/max workgroups, and the 48 KiB fp32 split of the
+    decode GEMV."""
+    announce("graph replays, size-dependent paths")
+    N = 320
+    cases = [(1, 12288, torch.float16), (2, 12288, torch.float16), (128, 4096, torch.float16),
+             (512, 4096, torch.float16), (1, 12288, torch.float32)]
+    mods = {}
+    for _, K, _ in cases:
+        if K not in mods:
+            w = make_weights(N, K, 150 + K)
+            mods[K] = (quant.Int8Linear(w, None), quant.DynamicInt8Linear(w, None))
+    xs = [make_x(M, K, 160 + M + K, outliers=True).to(xd).to(dev) for M, K, xd in cases]
+    wss = [quant.w8a8_workspace(M, K, dev) for M, K, _ in cases]
+    outs = {}
+
+    def body():
+        for i, (x, (M, K, _)) in enumerate(zip(xs, cases)):
+            lin, dyn = mods[K]
+            outs[("w8", i)] = quant.linear_w8(x, lin.packed, lin.scale, None, N)
+            outs[("dyn", i)] = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N, workspace=wss[i])
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        body()
+    for rep in range(3):
+        for x in xs:
+            x.mul_(-1.5).add_(0.25 * rep)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (x, (M, K, xd)) in enumerate(zip(xs, cases)):
+            lin, dyn = mods[K]
+            eager_w8 = quant.linear_w8(x, lin.packed, lin.scale, None, N)
+            eager_dyn = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N)
+            np.testing.assert_array_equal(outs[("w8", i)].cpu().numpy(), eager_w8.cpu().numpy(),
+                                          err_msg=f"w8 replay {rep} M={M} K={K} {xd}")
+            np.testing.assert_array_equal(outs[("dyn", i)].cpu().numpy(), eager_dyn.cpu().numpy(),
+                                          err_msg=f"w8a8 replay {rep} M={M} K={K} {xd}")
+
+
 # ---------------------------------------------------------------------------
 # concurrency: the library keeps no state, so calls on two streams at once
 # give the same results as the same calls one after the other
