@@ -580,6 +580,9 @@ def main():
         for M in (4, 16):
             log(f"decode M={M}")
             extra[f"decode_M{M}"] = decode_bench(ctx, M, args.steps, args.warmup)
+        # the same step with fp32 activations, the reference model's own dtype
+        log("decode M=1, fp32 activations")
+        extra["decode_M1_f32x"] = decode_bench(ctx, 1, args.steps, args.warmup, xdtype=torch.float32)
         log("single 4096x4096 GEMV")
         extra["gemv_4096_f16x"] = decode_bench(ctx, 1, args.steps, args.warmup, shapes=[(4096, 4096)])
         extra["gemv_4096_f32x"] = decode_bench(ctx, 1, args.steps, args.warmup, shapes=[(4096, 4096)],
