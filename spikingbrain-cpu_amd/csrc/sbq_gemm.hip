@@ -26,6 +26,7 @@
 
 #include "sbq_common.h"
 #include "sbq_gemv_ops.h"
+#include "sbq_index.h"
 #include "sbq_launch.h"
 
 namespace sbq {
@@ -706,7 +707,11 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restric
     if constexpr (VEC) {
       typedef typename XElem<XT>::T T;
       typedef T v8 __attribute__((ext_vector_type(8)));
-      const T* p = (const T*)x + (int64_t)m * ldx + k0;
+      // K % 16 == 0: a chunk is either inside the row or wholly in the
+      // padding columns K..Kp-1, whose values are never used (they quantize
+      // to s8 0 below); padding chunks load the row's last chunk instead of
+      // reading past the row (past the end of x on the last row)
+      const T* p = (const T*)x + act_chunk_src(c, cpr, K, ldx);
       if constexpr (XT == XT_F32) {
         const f32x4 a0 = *(const f32x4*)p, a1 = *(const f32x4*)(p + 4);
         const f32x4 a2 = *(const f32x4*)(p + 8), a3 = *(const f32x4*)(p + 12);

@@ -67,11 +67,20 @@ def _code(dtype: torch.dtype) -> int:
 
 
 def _as_activation(x2: torch.Tensor) -> torch.Tensor:
+    """x2 [M, K] with unit column stride and rows that do not overlap (the
+    kernels read row m at m * ldx).  Broadcast rows (stride 0, from expand)
+    and other overlapping layouts are copied; one row is passed as it is."""
     if x2.dtype not in _DTYPE_CODE:
         x2 = x2.float()
-    if x2.stride(-1) != 1:
+    if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < x2.shape[1]):
         x2 = x2.contiguous()
     return x2
+
+
+def _ldx(x2: torch.Tensor) -> int:
+    """Row stride to pass for an activation from _as_activation: a single row
+    is contiguous whatever its stride(0) says (e.g. a transposed [K, 1])."""
+    return x2.shape[1] if x2.shape[0] <= 1 else x2.stride(0)
 
 
 def packed_bytes(N: int, K: int) -> int:
@@ -185,7 +194,7 @@ def linear_w8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias:
     _check_operands("linear_w8", x2, packed, N, y, (("scale", scale, torch.float32), ("bias", bias, torch.float32)),
                     ws)
     with torch.cuda.device(x2.device):
-        _lib.check(_lib.load().sbq_linear_w8(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
+        _lib.check(_lib.load().sbq_linear_w8(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
                                              _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype), y.stride(0),
                                              _ptr(ws), _nbytes(ws), _stream(x2.device)),
                    "sbq_linear_w8")
@@ -212,7 +221,7 @@ def linear_w8a8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, col
     _check_operands("linear_w8a8", x2, packed, N, y, (("scale", scale, torch.float32), ("bias", bias, torch.float32),
                                                       ("colsum", colsum, torch.int32)), ws)
     with torch.cuda.device(x2.device):
-        _lib.check(_lib.load().sbq_linear_w8a8(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
+        _lib.check(_lib.load().sbq_linear_w8a8(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
                                                _ptr(scale), _ptr(colsum), _ptr(bias), N, _ptr(y), _code(y.dtype),
                                                y.stride(0), _ptr(acc_out), _ptr(ws), _nbytes(ws),
                                                _stream(x2.device)),
@@ -236,7 +245,7 @@ def linear_w8a8_token(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tenso
     _check_operands("linear_w8a8_token", x2, packed, N, y,
                     (("scale", scale, torch.float32), ("bias", bias, torch.float32)), ws)
     with torch.cuda.device(x2.device):
-        _lib.check(_lib.load().sbq_linear_w8a8_token(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(packed),
+        _lib.check(_lib.load().sbq_linear_w8a8_token(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
                                                      _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype),
                                                      y.stride(0), _ptr(acc_out), _ptr(ws), _nbytes(ws),
                                                      _stream(x2.device)),
@@ -268,7 +277,7 @@ def act_qparams(x2: torch.Tensor) -> tuple[float, int]:
     z = torch.empty((1,), dtype=torch.int32, device=x2.device)
     ws = w8a8_workspace(M, K, x2.device)
     with torch.cuda.device(x2.device):
-        _lib.check(_lib.load().sbq_act_qparams(_ptr(x2), _code(x2.dtype), M, K, x2.stride(0), _ptr(s), _ptr(z),
+        _lib.check(_lib.load().sbq_act_qparams(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(s), _ptr(z),
                                                _ptr(ws), _nbytes(ws), _stream(x2.device)),
                    "sbq_act_qparams")
     return float(s.item()), int(z.item())
@@ -368,15 +377,37 @@ class Int8Linear(nn.Module):
         return out.reshape(*shape[:-1], -1)
 
 
-class DynamicInt8Linear(nn.Module):
+class _Fp32Buffers:
+    """Mixin: the buffers named in ``_fp32_buffers`` keep their fp32 values
+    across module dtype conversions (``.half()``, ``.to(torch.bfloat16)``);
+    device moves still apply.  quant.py:61 keeps the int8-dyn scales and bias
+    inside fbgemm's packed weight, which those conversions never touch."""
+
+    _fp32_buffers: tuple = ()
+
+    def _apply(self, fn, recurse=True):
+        keep = {n: self._buffers.get(n) for n in self._fp32_buffers}
+        super()._apply(fn, recurse)
+        for n, old in keep.items():
+            new = self._buffers.get(n)
+            if old is not None and new is not None and new.dtype != old.dtype:
+                self._buffers[n] = old.to(new.device)
+        return self
+
+
+class DynamicInt8Linear(_Fp32Buffers, nn.Module):
     """quant.py:56-66.  The reference keeps only an opaque fbgemm prepacked
     weight (``packed``) and no state_dict entries; here ``packed`` is the tiled
-    device layout and ``scale``/``colsum`` are non-persistent buffers.
+    device layout and ``scale``/``colsum`` are non-persistent buffers.  The
+    scales and bias stay fp32 under ``.half()`` / ``.to(dtype)``, as they do
+    inside the reference's packed weight.
 
     ``granularity="tensor"`` (default) is the reference's fbgemm semantics,
     bit for bit.  ``granularity="token"`` opts into per-token symmetric
     activation quantization (linear_w8a8_token), which has no counterpart in
     the reference and does not reproduce its outputs."""
+
+    _fp32_buffers = ("scale", "bias")
 
     def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, granularity: str = "tensor"):
         super().__init__()
@@ -402,10 +433,11 @@ class DynamicInt8Linear(nn.Module):
 
         def run(xd):
             x2 = xd.reshape(-1, shape[-1])
-            scale = self.scale if self.scale.dtype == torch.float32 else self.scale.float()
+            scale = self.scale.float()
+            bias = None if self.bias is None else self.bias.float()
             if getattr(self, "granularity", "tensor") == "token":
-                return linear_w8a8_token(x2, self.packed, scale, self.bias, self.out_features, self.out_dtype)
-            return linear_w8a8(x2, self.packed, scale, self.colsum, self.bias, self.out_features, self.out_dtype)
+                return linear_w8a8_token(x2, self.packed, scale, bias, self.out_features, self.out_dtype)
+            return linear_w8a8(x2, self.packed, scale, self.colsum, bias, self.out_features, self.out_dtype)
 
         out = _run_on_device(x, self.packed.device, run)
         return out.reshape(*shape[:-1], -1)
@@ -514,7 +546,7 @@ class FloatLinear(nn.Module):
         return _run_on_device(x, self.weight.device, lambda xd: F.linear(xd.float(), self.weight, self.bias))
 
 
-class FusedLinear(nn.Module):
+class FusedLinear(_Fp32Buffers, nn.Module):
     """Quantized linears that read the same input, run as one launch over their
     row-concatenated weights (the q/k/v and gate/up projections of model.py
     call their modules back to back on one x: model.py:262-264, 363-365).
@@ -525,7 +557,14 @@ class FusedLinear(nn.Module):
 
     forward(x) returns one tensor per part (contiguous, like the parts').
     part(i) is a drop-in module for part i: the parts share the result of one
-    launch for the same input tensor (identity and in-place version checked)."""
+    launch for the same input tensor.  The shared result is reused while x is
+    the same tensor object at the same address with the same version counter.
+    Inference tensors (torch.inference_mode, as model.py:427 runs the model)
+    carry no version counter: for them an in-place edit of x between two
+    parts' calls is not detected.  Scales and bias stay fp32 under .half() /
+    .to(dtype)."""
+
+    _fp32_buffers = ("scale", "bias")
 
     def __init__(self, parts: list[nn.Module]):
         super().__init__()
@@ -556,7 +595,7 @@ class FusedLinear(nn.Module):
         self.register_buffer("bias", bias, persistent=False)
         self.out_dtype = torch.float32
         self._memo_ref = None
-        self._memo_version = -1
+        self._memo_key = None
         self._memo_out = None
 
     def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, ...]:
@@ -565,10 +604,11 @@ class FusedLinear(nn.Module):
 
         def run(xd):
             x2 = xd.reshape(-1, shape[-1])
+            scale = self.scale.float()
+            bias = None if self.bias is None else self.bias.float()
             if self.w8a8:
-                return linear_w8a8(x2, self.packed, self.scale, self.colsum, self.bias, self.out_features,
-                                   self.out_dtype)
-            return linear_w8(x2, self.packed, self.scale, self.bias, self.out_features, self.out_dtype)
+                return linear_w8a8(x2, self.packed, scale, self.colsum, bias, self.out_features, self.out_dtype)
+            return linear_w8(x2, self.packed, scale, bias, self.out_features, self.out_dtype)
 
         y = _run_on_device(x, self.packed.device, run)
         outs = torch.split(y, self.sizes, dim=-1)
@@ -576,9 +616,11 @@ class FusedLinear(nn.Module):
 
     def _shared(self, x: torch.Tensor) -> tuple[torch.Tensor, ...]:
         ref = self._memo_ref() if self._memo_ref is not None else None
-        if ref is not x or x._version != self._memo_version:
+        # inference tensors raise on ._version: their key is the address only
+        key = (x.data_ptr(), -1 if x.is_inference() else x._version)
+        if ref is not x or key != self._memo_key:
             out = self.forward(x)
-            self._memo_ref, self._memo_version, self._memo_out = weakref.ref(x), x._version, out
+            self._memo_ref, self._memo_key, self._memo_out = weakref.ref(x), key, out
         return self._memo_out
 
     def part(self, i: int) -> nn.Module:

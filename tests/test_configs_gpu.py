@@ -1,0 +1,327 @@
+"""GPU parity at the full sizes of the benchmark configurations and of the real
+checkpoint (run on the MI355X box), against the CPU oracle.
+
+Covered shapes (paths relative to the reference repository):
+  * lm_head V=151936 at K=4096 (36-layer benchmark model) and K=2560 (the
+    real checkpoint, config.py:16,19), model.py:410,445-447, M=1 and M=8;
+  * down projections K=12288 and K=9728 (config.py:18), M=1 and M=8;
+  * the 4096x4096 single GEMV and the 24576x4096 gate+up GEMV at M=1;
+  * prefill N=12288, K=4096 at M=512, 2048 (fp32 activations, the module
+    default) and M=8192 (fp16);
+  * int8-dyn at M=1/128/2048 over N=4096/12288;
+  * the fused hybrid "reads-x" group (model.py:317-329,363-365: sse_q/k/v,
+    lora_q[0]/lora_k[0], sse_a/b/e, swa_q/k/v; N=18820) against the oracle in
+    both formats, its parts inside torch.inference_mode();
+  * one decode step through all 539 quantized linears of the 36-layer hybrid
+    model (26 hybrid + 10 softmax blocks, hidden 4096, FFN 12288, 32/8 heads
+    of 128, router 4, vocab 151936) at M=1 and M=8, in both formats, with the
+    lora_*[0] -> lora_*[1] chain fed as model.py:318-319 feeds it.
+
+Outputs are checked on samples: one output channel per 16-row weight tile
+(every workgroup of the GEMV and every GEMM block is checked) and one token
+per 16-token fragment.  Bars, as in the other GPU tests: int8 weight-only
+relative L2 <= 1e-3 against the oracle (2e-6 for fp16 activations, which the
+kernels use exactly, with fp32 outputs); int8-dyn int32 accumulators and fp32
+outputs bit-exact, with the activation quantization parameters of the whole
+tensor.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import announce
+from sbq import quant
+
+W8_TOL = 1e-3
+W8_TOL_EXACT_X = 2e-6
+DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def gpu_weight(N, K, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(N, K, generator=g, device=dev) * 0.02
+
+
+def cpu_x(M, K, seed, outliers=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    if outliers:
+        idx = torch.randperm(K, generator=g)[: max(1, K // 100)]
+        x[:, idx] *= 20
+    return x
+
+
+def tile_sample(n, seed, block=16, cap=None):
+    """One index per `block`-sized tile of range(n) (offset varying by tile),
+    plus n - 1; `cap` keeps that many tiles (spread over the range)."""
+    rng = np.random.default_rng(seed)
+    starts = np.arange(0, n, block)
+    if cap is not None and len(starts) > cap:
+        starts = np.unique(np.linspace(0, len(starts) - 1, cap).astype(int)) * block
+    idx = np.minimum(starts + rng.integers(0, block, len(starts)), n - 1)
+    return np.unique(np.append(idx, n - 1))
+
+
+def ref_rows(w_gpu, cols):
+    """Oracle quantization of the sampled weight rows (fp32 [len, K] -> q, s)."""
+    w = w_gpu[torch.from_numpy(cols).to(w_gpu.device)].float().cpu().numpy()
+    return oracle.quantize_per_channel(w)
+
+
+def ref_w8a8(x_full, rows, q, s, bias=None):
+    """int32 accumulators and outputs of the sampled rows x columns, with the
+    activation parameters of the WHOLE tensor (fbgemm's per-tensor choice)."""
+    sx, zp = oracle.act_qparams(x_full)
+    xq = oracle.quantize_act(x_full[rows], sx, zp)
+    acc64 = (xq.astype(np.float64) - zp) @ np.asarray(q, np.float64).T  # exact: |acc| < 2^53
+    acc = np.ascontiguousarray(acc64.astype(np.int64).astype(np.int32))
+    return acc, oracle.dyn_epilogue(acc, sx, s, bias)
+
+
+def pick(t, rows, cols):
+    return t[torch.from_numpy(rows).to(t.device)][:, torch.from_numpy(cols).to(t.device)].float().cpu().numpy()
+
+
+# ---------------------------------------------------------------------------
+# single linears at full size
+# ---------------------------------------------------------------------------
+W8_FULL = [
+    # (M, N, K, x dtype, y dtype)
+    (1, 24576, 4096, "f16", "f16"),    # gate+up, the dominant decode launch
+    (1, 24576, 4096, "f32", "f32"),
+    (1, 4096, 4096, "f16", "f32"),     # single 4096x4096 GEMV
+    (1, 4096, 4096, "f32", "f32"),
+    (1, 151936, 4096, "f32", "f32"),   # lm_head, 36-layer benchmark model
+    (8, 151936, 4096, "f32", "f32"),
+    (1, 151936, 2560, "f32", "f32"),   # lm_head, real checkpoint
+    (8, 151936, 2560, "f32", "f32"),
+    (1, 4096, 12288, "f32", "f32"),    # down
+    (8, 4096, 12288, "f16", "f32"),
+    (1, 2560, 9728, "f32", "f32"),     # down, real checkpoint
+    (8, 2560, 9728, "f32", "f32"),
+    (512, 12288, 4096, "f32", "f32"),  # prefill chunk as the model issues it (fp32 in and out)
+    (2048, 12288, 4096, "f32", "f32"),
+    (8192, 12288, 4096, "f16", "f16"),  # prefill, M=8192
+    (8192, 12288, 4096, "f16", "f32"),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,xd,yd", W8_FULL)
+def test_w8_full_size(dev, M, N, K, xd, yd):
+    announce(f"w8 full M={M} N={N} K={K} x={xd} y={yd}")
+    w = gpu_weight(N, K, 11, dev)
+    lin = quant.Int8Linear(w, None)
+    cols = tile_sample(N, 1)
+    q, s = ref_rows(w, cols)
+    np.testing.assert_array_equal(lin.qweight[torch.from_numpy(cols).to(dev)].cpu().numpy(), q)
+    del w
+    x = cpu_x(M, K, 2).to(DT[xd])
+    out = torch.empty((M, N), dtype=DT[yd], device=dev)
+    quant.linear_w8(x.to(dev), lin.packed, lin.scale, None, N, out=out)
+    rows = tile_sample(M, 3)
+    ref = oracle.int8_linear(x.float().numpy()[rows], q, s)
+    tol = W8_TOL_EXACT_X if (xd != "f32" and yd == "f32") else W8_TOL
+    assert oracle.rel_l2(pick(out, rows, cols), ref) <= tol
+
+
+W8A8_FULL = [
+    (1, 151936, 4096, "f32"), (8, 151936, 4096, "f32"),   # lm_head
+    (1, 151936, 2560, "f32"), (8, 151936, 2560, "f32"),
+    (1, 4096, 12288, "f32"), (8, 4096, 12288, "f32"),     # down
+    (1, 2560, 9728, "f32"), (8, 2560, 9728, "f32"),
+    (1, 12288, 4096, "f16"), (128, 4096, 4096, "f16"),    # int8-dyn benchmark shapes
+    (2048, 4096, 4096, "f16"), (512, 12288, 4096, "f32"),
+    (8192, 12288, 4096, "f16"),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,xd", W8A8_FULL)
+def test_w8a8_full_size(dev, M, N, K, xd):
+    announce(f"w8a8 full M={M} N={N} K={K} x={xd}")
+    w = gpu_weight(N, K, 21, dev)
+    lin = quant.DynamicInt8Linear(w, None)
+    cols = tile_sample(N, 4)
+    q, s = ref_rows(w, cols)
+    del w
+    x = cpu_x(M, K, 5, outliers=True).to(DT[xd])
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y = quant.linear_w8a8(x.to(dev), lin.packed, lin.scale, lin.colsum, None, N, acc_out=acc)
+    rows = tile_sample(M, 6)
+    acc_ref, y_ref = ref_w8a8(x.float().numpy(), rows, q, s)
+    np.testing.assert_array_equal(acc[torch.from_numpy(rows).to(dev)][:, torch.from_numpy(cols).to(dev)].cpu().numpy(),
+                                  acc_ref)
+    np.testing.assert_array_equal(pick(y, rows, cols), y_ref)
+
+
+# ---------------------------------------------------------------------------
+# the fused hybrid "reads-x" group (N = 18820)
+# ---------------------------------------------------------------------------
+HYBRID_READS_X = [("sse_q", 4096), ("sse_k", 4096), ("sse_v", 4096), ("lora_q0", 128), ("lora_k0", 128),
+                  ("sse_a", 64), ("sse_b", 64), ("sse_e", 4), ("swa_q", 4096), ("swa_k", 1024), ("swa_v", 1024)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["int8", "int8-dyn"])
+@pytest.mark.parametrize("M", [1, 8])
+def test_fused_hybrid_group_vs_oracle(dev, fmt, M):
+    announce(f"fused hybrid reads-x group fmt={fmt} M={M}")
+    K = 4096
+    ws = [gpu_weight(n, K, 40 + i, dev) for i, (_, n) in enumerate(HYBRID_READS_X)]
+    mods = [quant.make_linear(fmt, w) for w in ws]
+    fused = quant.fuse_linears(mods)
+    assert fused.out_features == 18820
+    x = cpu_x(M, K, 41)
+    outs = fused(x.to(dev))
+    parts = [fused.part(i) for i in range(len(mods))]
+    with torch.inference_mode():  # as model.py:427 runs the model
+        xi = x.to(dev)
+        part_outs = [p(xi) for p in parts]
+    rows = np.arange(M)
+    for (name, n), w, o, po in zip(HYBRID_READS_X, ws, outs, part_outs):
+        cols = tile_sample(n, 7)
+        q, s = ref_rows(w, cols)
+        got = o.cpu().numpy()[:, cols]
+        if fmt == "int8":
+            assert oracle.rel_l2(got, oracle.int8_linear(x.numpy(), q, s)) <= W8_TOL, name
+            np.testing.assert_array_equal(po.cpu().numpy(), o.cpu().numpy())
+        else:
+            _, y_ref = ref_w8a8(x.numpy(), rows, q, s)
+            np.testing.assert_array_equal(got, y_ref, err_msg=name)
+            np.testing.assert_array_equal(po.cpu().numpy(), o.cpu().numpy())
+
+
+# ---------------------------------------------------------------------------
+# one decode step through the 539 quantized linears of the 36-layer model
+# ---------------------------------------------------------------------------
+SOFTMAX_LAYERS = (0, 1, 2, 3, 6, 12, 17, 21, 24, 35)
+
+
+def stack_layout(H=4096, F=12288, heads=32, kv=8, d=128, routers=4, vocab=151936, layers=36):
+    """(name, N, K, input) of every quantized linear of one decode step, in
+    model order.  input: "h" (the normed hidden state), "attn" (an attention
+    output), "ffn" (the gated MLP activation) or the name of the linear whose
+    output it reads (lora_*[1] read lora_*[0], model.py:318-319)."""
+    out = []
+    for i in range(layers):
+        p = f"l{i}."
+        if i in SOFTMAX_LAYERS:  # model.py:250-253,262-270
+            out += [(p + "q", heads * d, H, "h"), (p + "k", kv * d, H, "h"), (p + "v", kv * d, H, "h"),
+                    (p + "o", H, heads * d, "attn")]
+        else:  # model.py:284-301,317-329,359-371
+            out += [(p + n, heads * d, H, "h") for n in ("sse_q", "sse_k", "sse_v")]
+            out += [(p + "lora_q0", d, H, "h"), (p + "lora_k0", d, H, "h")]
+            out += [(p + "lora_q1", heads * d, d, p + "lora_q0"), (p + "lora_k1", heads * d, d, p + "lora_k0")]
+            out += [(p + "sse_a", 2 * heads, H, "h"), (p + "sse_b", 2 * heads, H, "h"), (p + "sse_e", routers, H, "h")]
+            out += [(p + "sse_o", H, heads * d, "attn")]
+            out += [(p + "swa_q", heads * d, H, "h"), (p + "swa_k", kv * d, H, "h"), (p + "swa_v", kv * d, H, "h"),
+                    (p + "swa_o", H, heads * d, "attn")]
+        out += [(p + "gate", F, H, "h"), (p + "up", F, H, "h"), (p + "down", H, F, "ffn")]  # model.py:235-240
+    out.append(("lm_head", vocab, H, "h"))  # model.py:410,447
+    return out
+
+
+def test_stack_layout_counts():
+    lay = stack_layout()
+    assert len(lay) == 539
+    assert sum(n * k for _, n, k, _ in lay) == 9381511168
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["int8", "int8-dyn"])
+def test_decode_step_539_linears(dev, fmt):
+    """Every linear's output at M=1 and M=8 checked on up to 48 sampled output
+    channels (one per sampled 16-row tile); every distinct (N, K) appears."""
+    lay = stack_layout()
+    announce(f"539-linear decode step fmt={fmt}: building")
+    mods, refs = {}, {}
+    for i, (name, n, k, _) in enumerate(lay):
+        w = gpu_weight(n, k, 1000 + i, dev)
+        mods[name] = quant.make_linear(fmt, w)
+        cols = tile_sample(n, i, cap=48)
+        refs[name] = (cols, *ref_rows(w, cols))
+        del w
+    torch.cuda.synchronize()
+    for M in (1, 8):
+        announce(f"539-linear decode step fmt={fmt} M={M}")
+        src = {"h": cpu_x(M, 4096, 51), "attn": cpu_x(M, 4096, 52), "ffn": cpu_x(M, 12288, 53)}
+        dsrc = {key: v.to(dev) for key, v in src.items()}
+        outs = {}
+        with torch.inference_mode():
+            for name, n, k, inp in lay:  # eager, in model order
+                outs[name] = mods[name](dsrc[inp] if inp in dsrc else outs[inp])
+        torch.cuda.synchronize()
+        for name, n, k, inp in lay:
+            cols, q, s = refs[name]
+            x = src[inp].numpy() if inp in src else outs[inp].cpu().numpy()
+            got = outs[name].cpu().numpy()[:, cols]
+            if fmt == "int8":
+                assert oracle.rel_l2(got, oracle.int8_linear(x, q, s)) <= W8_TOL, (name, M)
+            else:
+                _, y_ref = ref_w8a8(x, np.arange(M), q, s)
+                np.testing.assert_array_equal(got, y_ref, err_msg=f"{name} M={M}")
+    del mods
+
+
+# ---------------------------------------------------------------------------
+# the module API under the reference model's calling conventions
+# ---------------------------------------------------------------------------
+@pytest.mark.gpu
+def test_loader_swap_inference_mode_and_dtype_moves(dev):
+    """loader.py:43-51 swaps nn.Linear children (including nn.Sequential ones)
+    for make_linear modules; model.py:427 then calls them under
+    torch.inference_mode().  Fused parts must work there, .half() must leave
+    the int8-dyn scales and bias fp32 (they live in fbgemm's packed weight in
+    the reference, quant.py:61), and broadcast / transposed-row activations
+    must be accepted as the reference's matmul accepts them."""
+    announce("loader swap + inference mode + dtype moves")
+    K = 256
+    model = torch.nn.ModuleDict({"q": torch.nn.Linear(K, 64, bias=False), "k": torch.nn.Linear(K, 32, bias=False),
+                                 "lora": torch.nn.Sequential(torch.nn.Linear(K, 16, bias=False),
+                                                             torch.nn.Linear(16, 64, bias=False))})
+    g = torch.Generator().manual_seed(9)
+    for m in model.modules():
+        if isinstance(m, torch.nn.Linear):
+            m.weight.data = torch.randn(m.weight.shape, generator=g) * 0.02
+    for fmt in ("int8", "int8-dyn"):
+        swapped = torch.nn.ModuleDict()
+        for name, child in model.items():
+            if isinstance(child, torch.nn.Sequential):
+                swapped[name] = torch.nn.Sequential(*[quant.make_linear(fmt, c.weight.data) for c in child])
+            else:
+                swapped[name] = quant.make_linear(fmt, child.weight.data)
+        fused = quant.fuse_linears([swapped["q"], swapped["k"]])
+        x = torch.randn(3, K, generator=g).to(dev)
+        with torch.inference_mode():
+            xi = x.clone()
+            pq, pk = fused.part(0)(xi), fused.part(1)(xi)
+            sq, sk = swapped["q"](xi), swapped["k"](xi)
+            lo = swapped["lora"](xi)
+        if fmt == "int8-dyn":
+            np.testing.assert_array_equal(pq.cpu().numpy(), sq.cpu().numpy())
+            np.testing.assert_array_equal(pk.cpu().numpy(), sk.cpu().numpy())
+        else:
+            assert oracle.rel_l2(pq.cpu().numpy(), sq.cpu().numpy()) <= 1e-5
+            assert oracle.rel_l2(pk.cpu().numpy(), sk.cpu().numpy()) <= 1e-5
+        assert lo.shape == (3, 64)
+        # broadcast rows and a transposed [K, 1] row
+        xb = x[:1].expand(3, K)
+        np.testing.assert_array_equal(swapped["q"](xb).cpu().numpy(), swapped["q"](xb.contiguous()).cpu().numpy())
+        xt = x[:1].t().contiguous().t()  # shape [1, K], strides (1, 1)
+        assert xt.stride() == (1, 1)
+        np.testing.assert_array_equal(swapped["q"](xt).cpu().numpy(), swapped["q"](x[:1]).cpu().numpy())
+    dyn = quant.DynamicInt8Linear(torch.randn(40, K, generator=g) * 0.02, torch.randn(40, generator=g))
+    x = torch.randn(2, K, generator=g).to(dev)
+    before = dyn(x).cpu().numpy()
+    dyn.half()
+    assert dyn.scale.dtype == torch.float32 and dyn.bias.dtype == torch.float32
+    np.testing.assert_array_equal(dyn(x).cpu().numpy(), before)
+    fz = quant.fuse_linears([quant.DynamicInt8Linear(torch.randn(16, K, generator=g) * 0.02, torch.randn(16)),
+                             quant.DynamicInt8Linear(torch.randn(16, K, generator=g) * 0.02, None)])
+    fb = [o.cpu().numpy() for o in fz(x)]
+    fz.to(torch.bfloat16)
+    assert fz.scale.dtype == torch.float32 and fz.bias.dtype == torch.float32
+    for a, b in zip(fz(x), fb):
+        np.testing.assert_array_equal(a.cpu().numpy(), b)
