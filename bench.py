@@ -340,6 +340,58 @@ def traffic_probe(ctx, launches=24, cal_reps=4):
     log(f"traffic probe: {launches} gate+up launches, {cal_reps} copies of {CAL_BYTES >> 20} MiB")
 
 
+def gemv_probe(ctx, N=4096, K=4096, M=1, launches_per_copy=8, reps=20):
+    """Back-to-back decode GEMV launches (fp16 x and y, weights rotating over
+    >= 512 MB of copies) captured in one HIP graph and replayed `reps` times:
+    the workload of the kernel-trace pass that splits each launch's duration
+    from the gap to the next launch."""
+    torch, quant = ctx.torch, ctx.quant
+    copies = math.ceil(ROTATE_BYTES / (N * K)) + 1
+    layers = [ctx.weights(N, K, 700 + c) for c in range(copies)]
+    x = ctx.act(M, K, 7)
+    y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
+
+    def run():
+        for _ in range(launches_per_copy):
+            for packed, s, _ in layers:
+                quant.linear_w8(x, packed, s, None, N, out=y)
+
+    g = ctx.graph(run)
+    ms = ctx.time_graphs([g], reps, 1)
+    n = launches_per_copy * copies
+    log(f"gemv probe: M={M} N={N} K={K}, {reps} replays of {n} launches, {ms * 1e3 / n:.3f} us per launch (events)")
+
+
+def summarize_gaps(d, match, command):
+    """Markdown: per-dispatch duration and the gap from each dispatch's end to
+    the next dispatch's start, over runs of consecutive dispatches of the
+    kernels whose name contains `match` (the back-to-back launches of a graph)."""
+    import statistics
+
+    rows = sorted(_csv_rows(d, "kernel_trace.csv"), key=lambda r: int(r["Start_Timestamp"]))
+    dur, gap, period = [], [], []
+    for a, b in zip(rows, rows[1:]):
+        if match in a["Kernel_Name"] and match in b["Kernel_Name"]:
+            s0, e0, s1 = int(a["Start_Timestamp"]), int(a["End_Timestamp"]), int(b["Start_Timestamp"])
+            dur.append((e0 - s0) / 1e3)
+            gap.append((s1 - e0) / 1e3)
+            period.append((s1 - s0) / 1e3)
+    if not dur:
+        raise SystemExit(f"no consecutive dispatches of {match} in {d}")
+    name = _short(next(r["Kernel_Name"] for r in rows if match in r["Kernel_Name"]))
+
+    def line(label, v):
+        q = statistics.quantiles(v, n=20)
+        return (f"| {label} | {statistics.mean(v):.3f} | {statistics.median(v):.3f} | {q[0]:.3f} | {q[-1]:.3f} |")
+
+    out = [f"# Launch duration vs launch-to-launch gap: `{name}`", "", "Command:", "", "```", command, "```", "",
+           f"Pairs of consecutive dispatches: {len(dur)}.", "",
+           "| us | mean | median | p5 | p95 |", "|---|---|---|---|---|",
+           line("duration (start to end)", dur), line("gap (end to next start)", gap),
+           line("period (start to next start)", period)]
+    return "\n".join(out) + "\n"
+
+
 def prefill_probe(ctx, M=2048, N=12288, K=4096, launches=100):
     """The prefill operation alone (row-sum pre-pass + GEMM; int8 weights, fp16
     x and y), for counter passes; enough back-to-back launches (~17 ms) for
@@ -537,6 +589,10 @@ def main():
                     help="only run the M=2048 prefill GEMM (workload of the prefill counter passes)")
     ap.add_argument("--w8a8-probe", action="store_true",
                     help="only run the M=2048 int8-dyn prefill (workload of the W8A8 counter passes)")
+    ap.add_argument("--gemv-probe", nargs=3, type=int, metavar=("M", "N", "K"),
+                    help="only run back-to-back decode GEMV launches in a graph (workload of the gap trace)")
+    ap.add_argument("--summarize-gaps", metavar="DIR",
+                    help="print launch duration vs launch-to-launch gap from a rocprofv3 kernel trace")
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
                     help="print per-dispatch counter averages from rocprofv3 --pmc directories")
     ap.add_argument("--match", default="gemm_dl_kernel", help="kernel-name filter for --summarize-counters")
@@ -550,6 +606,9 @@ def main():
         return
     if args.summarize_counters:
         print(summarize_counters(args.summarize_counters, args.match, args.command), end="")
+        return
+    if args.summarize_gaps:
+        print(summarize_gaps(args.summarize_gaps, args.match, args.command), end="")
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -569,6 +628,10 @@ def main():
         return
     if args.w8a8_probe:
         w8a8_probe(ctx)
+        return
+    if args.gemv_probe:
+        M, N, K = args.gemv_probe
+        gemv_probe(ctx, N, K, M)
         return
     log("decode M=1 (headline)")
     head = decode_bench(ctx, 1, args.steps, args.warmup)

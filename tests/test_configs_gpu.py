@@ -309,7 +309,7 @@ def test_loader_swap_inference_mode_and_dtype_moves(dev):
         # broadcast rows and a transposed [K, 1] row
         xb = x[:1].expand(3, K)
         np.testing.assert_array_equal(swapped["q"](xb).cpu().numpy(), swapped["q"](xb.contiguous()).cpu().numpy())
-        xt = x[:1].t().contiguous().t()  # shape [1, K], strides (1, 1)
+        xt = x[0].clone().reshape(K, 1).t()  # shape [1, K], strides (1, 1)
         assert xt.stride() == (1, 1)
         np.testing.assert_array_equal(swapped["q"](xt).cpu().numpy(), swapped["q"](x[:1]).cpu().numpy())
     dyn = quant.DynamicInt8Linear(torch.randn(40, K, generator=g) * 0.02, torch.randn(40, generator=g))
