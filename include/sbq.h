@@ -163,6 +163,29 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
                     void* y, int y_dtype, int64_t ldy, int32_t* acc_out,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Largest quantized-activation scratch of sbq_linear_w8a8_noalloc:
+ * M * ceil(K/64)*64 bytes must not exceed it (e.g. M = 2048 at K = 4096,
+ * M = 512 at K = 12288). */
+#define SBQ_NOALLOC_XQ_BYTES (8 << 20)
+
+/* sbq_linear_w8a8 without a workspace: no counterpart in the reference.  It is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc); it calls no
+ * allocating routine.  Same arguments, results and bit-exactness as
+ * sbq_linear_w8a8.  Its scratch (activation min/max partials, (s_x, zp), the
+ * quantized activations) is a static device array of 2304 bytes +
+ * SBQ_NOALLOC_XQ_BYTES that each GPU the library runs on holds until the
+ * process ends; the first call on a device looks up that device's copy (make
+ * it outside graph capture).  Inputs with M * ceil(K/64)*64 >
+ * SBQ_NOALLOC_XQ_BYTES return SBQ_ERR_WORKSPACE before any launch.  Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other threads) race on it.  Nothing in it needs clearing between
+ * calls (each call writes every byte it reads). */
+int sbq_linear_w8a8_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                            const uint8_t* packed, const float* scale, const int32_t* colsum,
+                            const float* bias, int64_t N,
+                            void* y, int y_dtype, int64_t ldy, int32_t* acc_out, void* stream);
+
 /* Per-token symmetric W8A8: an opt-in granularity with no counterpart in the
  * reference, whose int8-dyn (quant.py:63-66, sbq_linear_w8a8 above) is
  * per-tensor asymmetric; it does not reproduce the reference's outputs.  Each

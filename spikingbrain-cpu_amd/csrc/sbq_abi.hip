@@ -6,6 +6,8 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "sbq.h"
 #include "sbq_common.h"
 #include "sbq_launch.h"
@@ -52,6 +54,52 @@ inline int8_t* ws_xq(void* workspace) { return (int8_t*)((uint8_t*)ws_qp(workspa
 inline float* ws_stok(void* workspace, int64_t M, int64_t K) {
   const int64_t xq = M * (((K + 63) / 64) * 64);
   return (float*)((uint8_t*)ws_xq(workspace) + ((xq + 255) & ~(int64_t)255));
+}
+
+// The int8-dyn path of one call as the entry points below run it: scratch
+// from a caller's workspace or from the no-allocation array.
+int linear_w8a8_run(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
+                    const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int y_dtype,
+                    int64_t ldy, int32_t* acc_out, float2* parts, float* qp, int8_t* xq, hipStream_t st) {
+  const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
+  if (sbq::gemv_supports(M, K, true, x_dtype))
+    return sbq::launch_gemv_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
+                                 parts, st, yv);
+  return sbq::launch_gemm_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
+                               parts, xq, qp, st, yv);
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of sbq_linear_w8a8_noalloc: one static array per GPU (each device
+// that loads the library holds its own copy until the process ends), laid out
+// as the workspace of sbq_linear_w8a8 from its first 256-byte boundary: the
+// activation min/max partials, (s_x, zp), then the quantized activations.
+// Host code never passes the array's name to a kernel (on the host it is a
+// stand-in, not a device address): the device address comes from
+// hipGetSymbolAddress, looked up once per device with that device current.
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocHead = kWsPartialBytes + kWsQpBytes;
+static_assert(kNoAllocHead % 256 == 0, "xq starts 256-byte aligned");
+__device__ __align__(256) uint8_t scratch[kNoAllocHead + SBQ_NOALLOC_XQ_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+int g_scratch_rc[kMaxDevices];
+
+// Device address of this GPU's scratch array (the current device's).
+int scratch_ptr(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SBQ_ERR_DEVICE;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = p;
+    g_scratch_rc[dev] = (e == hipSuccess && p != nullptr) ? SBQ_OK : SBQ_ERR_LAUNCH;
+  });
+  if (g_scratch_rc[dev] != SBQ_OK) return g_scratch_rc[dev];
+  *out = g_scratch_ptr[dev];
+  return SBQ_OK;
 }
 
 }  // namespace
@@ -172,14 +220,27 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
   if (rc || M == 0) return rc;
   if (!colsum) return SBQ_ERR_ARG;
   if (!workspace || (int64_t)workspace_bytes < sbq_w8a8_workspace_bytes(M, K)) return SBQ_ERR_WORKSPACE;
-  const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
-  hipStream_t st = (hipStream_t)stream;
-  float2* parts = ws_partials(workspace);
-  if (sbq::gemv_supports(M, K, true, x_dtype))
-    return sbq::launch_gemv_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
-                                 parts, st, yv);
-  return sbq::launch_gemm_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
-                               parts, ws_xq(workspace), ws_qp(workspace), st, yv);
+  return linear_w8a8_run(x, x_dtype, M, K, ldx, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
+                         ws_partials(workspace), ws_qp(workspace), ws_xq(workspace), (hipStream_t)stream);
+}
+
+int sbq_linear_w8a8_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
+                            const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y,
+                            int y_dtype, int64_t ldy, int32_t* acc_out, void* stream) {
+  int rc = check_linear(x, x_dtype, M, K, ldx, packed, scale, N, y, y_dtype, ldy);
+  if (rc || M == 0) return rc;
+  if (!colsum) return SBQ_ERR_ARG;
+  if (M * (((K + 63) / 64) * 64) > SBQ_NOALLOC_XQ_BYTES) return SBQ_ERR_WORKSPACE;
+  void* s = nullptr;
+  rc = scratch_ptr(&s);
+  if (rc) return rc;
+  // every scratch byte a call reads is written earlier in the same call (the
+  // partials by the min/max pass, (s_x, zp) and xq by the quantizer), so
+  // nothing is cleared between calls
+  uint8_t* base = (uint8_t*)s;
+  return linear_w8a8_run(x, x_dtype, M, K, ldx, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
+                         (float2*)base, (float*)(base + kWsPartialBytes), (int8_t*)(base + kNoAllocHead),
+                         (hipStream_t)stream);
 }
 
 int sbq_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* idx, void* stream) {

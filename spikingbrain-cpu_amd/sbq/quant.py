@@ -229,6 +229,34 @@ def linear_w8a8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, col
     return y
 
 
+def linear_w8a8_noalloc(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, colsum: torch.Tensor,
+                        bias: torch.Tensor | None, N: int, out: torch.Tensor,
+                        acc_out: torch.Tensor | None = None) -> torch.Tensor:
+    """linear_w8a8 with no workspace (sbq_linear_w8a8_noalloc): the library's
+    static per-GPU scratch holds the activation statistics and quantized
+    activations, and nothing is allocated, here or in the library; the caller
+    supplies `out` (and `acc_out`).  x2 must already be a GPU tensor the
+    kernels take as it is (fp32 / fp16 / bf16, unit column stride).  Calls that
+    overlap on one GPU race on the shared scratch."""
+    if x2.dim() != 2 or x2.dtype not in _DTYPE_CODE or x2.stride(-1) != 1 or (
+            x2.shape[0] > 1 and x2.stride(0) < x2.shape[1]):
+        raise ValueError("linear_w8a8_noalloc: x must be a 2-D fp32/fp16/bf16 tensor with unit column stride")
+    M, K = x2.shape
+    if acc_out is not None and (acc_out.dtype != torch.int32 or tuple(acc_out.shape) != (M, N)
+                                or not acc_out.is_contiguous() or acc_out.device != x2.device):
+        raise ValueError("acc_out must be a contiguous int32 [M, N] tensor on the input's device")
+    _check_operands("linear_w8a8_noalloc", x2, packed, N, out, (("scale", scale, torch.float32),
+                                                                 ("bias", bias, torch.float32),
+                                                                 ("colsum", colsum, torch.int32)))
+    with torch.cuda.device(x2.device):
+        _lib.check(_lib.load().sbq_linear_w8a8_noalloc(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
+                                                       _ptr(scale), _ptr(colsum), _ptr(bias), N, _ptr(out),
+                                                       _code(out.dtype), out.stride(0), _ptr(acc_out),
+                                                       _stream(x2.device)),
+                   "sbq_linear_w8a8_noalloc")
+    return out
+
+
 def linear_w8a8_token(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None,
                       N: int, out_dtype: torch.dtype = torch.float32, acc_out: torch.Tensor | None = None,
                       workspace: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -84,6 +84,14 @@ def test_argument_validation_without_gpu(lib):
     assert lib.sbq_quantize_per_channel(dummy, 5, 4, 4, 4, dummy, 4, dummy, None) == -2
     assert lib.sbq_repack_w8(dummy, 4, 64, 32, dummy, None, None) == -1
     assert lib.sbq_act_qparams(dummy, 0, 1, 64, 64, dummy, dummy, None, 0, None) == -4
+    # the no-allocation W8A8 entry point: colsum required; quantized activations
+    # beyond its static scratch (M * ceil(K/64)*64 > SBQ_NOALLOC_XQ_BYTES) rejected
+    from sbq import _lib
+    assert lib.sbq_linear_w8a8_noalloc(dummy, 0, 1, 64, 64, dummy, dummy, None, None, 16, dummy, 0, 16, None,
+                                       None) == -1
+    m_over = _lib.SBQ_NOALLOC_XQ_BYTES // 4096 + 1
+    assert lib.sbq_linear_w8a8_noalloc(dummy, 1, m_over, 4096, 4096, dummy, dummy, dummy, None, 16, dummy, 0, 16,
+                                       None, None) == -4
     # argmax: N < 1, ldy < N, null pointers; M == 0 is a no-op
     assert lib.sbq_argmax_rows(dummy, 1, 0, 0, dummy, None) == -1
     assert lib.sbq_argmax_rows(dummy, 1, 8, 4, dummy, None) == -1
