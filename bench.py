@@ -208,6 +208,41 @@ def dominant_kernel(ctx, M=1, launches_per_copy=8, reps=5):
             "launches": n * reps}
 
 
+def lm_head_greedy_bench(ctx, V=151936, K=4096, M=1, steps=40, warmup=5):
+    """lm_head (model.py:445-447) at M=1 with fp32 activations and logits (the
+    reference model's dtypes), three ways: the logits alone; the logits and
+    the greedy token in one pass (sbq_linear_w8_argmax); the logits then the
+    separate row argmax (sbq_argmax_rows).  Weights rotate over 2 copies
+    (1.24 GB, beyond the Infinity Cache)."""
+    torch, quant = ctx.torch, ctx.quant
+    layers = [ctx.weights(V, K, 800 + c) for c in range(2)]
+    x = ctx.act(M, K, 801, torch.float32)
+    y = torch.empty((M, V), dtype=torch.float32, device=ctx.dev)
+    idx = torch.empty((M,), dtype=torch.int64, device=ctx.dev)
+    state = quant.argmax_state(ctx.dev)
+    nbytes = gemv_bytes(M, V, K, 4, 4)
+
+    def plain(c):
+        packed, s, _ = layers[c % 2]
+        quant.linear_w8(x, packed, s, None, V, out=y)
+
+    def fused(c):
+        packed, s, _ = layers[c % 2]
+        quant.linear_w8_argmax(x, packed, s, None, V, state, out=y, idx=idx)
+
+    def separate(c):
+        plain(c)
+        quant.greedy_tokens(y)
+
+    res = {"V": V, "K": K, "M": M, "bytes": nbytes}
+    for name, fn in (("logits_us", plain), ("logits_and_token_one_pass_us", fused),
+                     ("logits_then_argmax_us", separate)):
+        res[name] = ctx.time_steps(fn, 4, steps, warmup) * 1e3
+    res["one_pass_extra_us"] = res["logits_and_token_one_pass_us"] - res["logits_us"]
+    res["GBps_one_pass"] = nbytes / (res["logits_and_token_one_pass_us"] * 1e-6) / 1e9
+    return res
+
+
 # ---------------------------------------------------------------------------
 # prefill GEMM and int8-dyn
 # ---------------------------------------------------------------------------
@@ -589,6 +624,7 @@ def main():
                     help="only run the M=2048 prefill GEMM (workload of the prefill counter passes)")
     ap.add_argument("--w8a8-probe", action="store_true",
                     help="only run the M=2048 int8-dyn prefill (workload of the W8A8 counter passes)")
+    ap.add_argument("--only", metavar="NAME", help="run one extra measurement and print it (e.g. lm_head_greedy)")
     ap.add_argument("--gemv-probe", nargs=3, type=int, metavar=("M", "N", "K"),
                     help="only run back-to-back decode GEMV launches in a graph (workload of the gap trace)")
     ap.add_argument("--summarize-gaps", metavar="DIR",
@@ -633,6 +669,10 @@ def main():
         M, N, K = args.gemv_probe
         gemv_probe(ctx, N, K, M)
         return
+    if args.only:
+        fn = {"lm_head_greedy": lm_head_greedy_bench}[args.only]
+        print(json.dumps({args.only: fn(ctx)}), flush=True)
+        return
     log("decode M=1 (headline)")
     head = decode_bench(ctx, 1, args.steps, args.warmup)
     log(f"  {head['GBps']:.0f} GB/s, {head['ms_per_step'] * 1e3:.1f} us/step")
@@ -655,6 +695,8 @@ def main():
         # the reference model's own activations are fp32: staged as fp16 hi + lo planes
         extra["prefill_other_x"] = [prefill_bench(ctx, 2048, xdtype=dt)
                                     for dt in (ctx.torch.bfloat16, ctx.torch.float32)]
+        log("lm_head and its greedy token")
+        extra["lm_head_greedy"] = lm_head_greedy_bench(ctx)
         log("int8-dyn")
         extra["w8a8"] = [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)]
         log("36-layer linear stack")

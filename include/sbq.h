@@ -30,6 +30,8 @@
  *   sbq_argmax_rows           <- spikingbrain_cpu/engine.py:30-31 (greedy sampling,
  *                                int(logits.argmax()) over the lm_head output of
  *                                model.py:447), so the logits need not leave the GPU
+ *   sbq_linear_w8_argmax,     <- spikingbrain_cpu/model.py:445-447 (lm_head) and
+ *   sbq_linear_w8a8_argmax       engine.py:30-31 (its greedy token) in one launch
  */
 #ifndef SBQ_H_
 #define SBQ_H_
@@ -202,6 +204,38 @@ int sbq_linear_w8a8_token(const void* x, int x_dtype, int64_t M, int64_t K, int6
                           const uint8_t* packed, const float* scale, const float* bias, int64_t N,
                           void* y, int y_dtype, int64_t ldy, int32_t* acc_out,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- lm_head and the greedy token in one pass ---------------------------- */
+
+/* Bytes of the argmax state of the two entry points below. */
+#define SBQ_ARGMAX_WS_BYTES 16640
+
+/* Int8Linear.forward over the lm_head weights (model.py:445-447 ->
+ * quant.py:41-53) followed by greedy token selection (engine.py:30-31,
+ * int(logits.argmax())):
+ *   y      = the fp32 logits [M, N] (row stride ldy), as sbq_linear_w8
+ *            computes them;
+ *   idx[m] = the first n with y[m, n] maximal over row m, NaN above every
+ *            number (torch.argmax; the same token sbq_argmax_rows picks on y).
+ * At decode sizes (M <= 16, K % 64 == 0, 16-byte aligned x rows) the token is
+ * picked inside the GEMV launch (its last workgroup decodes it); other shapes
+ * run sbq_linear_w8 (with the optional workspace, as there) and then
+ * sbq_argmax_rows.  argmax_ws: SBQ_ARGMAX_WS_BYTES of device memory, 8-byte
+ * aligned, all zero before the first call; every call leaves it zero again.
+ * Calls that can overlap (other streams) need their own argmax_ws.  idx:
+ * device int64 [M]. */
+int sbq_linear_w8_argmax(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                         const uint8_t* packed, const float* scale, const float* bias, int64_t N,
+                         float* y, int64_t ldy, int64_t* idx,
+                         void* workspace, size_t workspace_bytes, void* argmax_ws, void* stream);
+
+/* The same for DynamicInt8Linear.forward (quant.py:63-66): y as
+ * sbq_linear_w8a8 computes it (bit-exact with fbgemm), then the greedy token.
+ * workspace: as for sbq_linear_w8a8.  argmax_ws: as above. */
+int sbq_linear_w8a8_argmax(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                           const uint8_t* packed, const float* scale, const int32_t* colsum,
+                           const float* bias, int64_t N, float* y, int64_t ldy, int64_t* idx,
+                           void* workspace, size_t workspace_bytes, void* argmax_ws, void* stream);
 
 /* ---- greedy token selection (engine.py:30-31) ---- */
 

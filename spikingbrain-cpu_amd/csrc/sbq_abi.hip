@@ -10,6 +10,7 @@
 
 #include "sbq.h"
 #include "sbq_common.h"
+#include "sbq_gemv_ops.h"
 #include "sbq_launch.h"
 
 namespace {
@@ -101,6 +102,8 @@ int scratch_ptr(void** out) {
   *out = g_scratch_ptr[dev];
   return SBQ_OK;
 }
+
+static_assert(sbq::kArgmaxStateBytes <= SBQ_ARGMAX_WS_BYTES, "argmax state fits the documented size");
 
 }  // namespace
 
@@ -241,6 +244,48 @@ int sbq_linear_w8a8_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, in
   return linear_w8a8_run(x, x_dtype, M, K, ldx, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
                          (float2*)base, (float*)(base + kWsPartialBytes), (int8_t*)(base + kNoAllocHead),
                          (hipStream_t)stream);
+}
+
+int sbq_linear_w8_argmax(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
+                         const float* scale, const float* bias, int64_t N, float* y, int64_t ldy, int64_t* idx,
+                         void* workspace, size_t workspace_bytes, void* argmax_ws, void* stream) {
+  int rc = check_linear(x, x_dtype, M, K, ldx, packed, scale, N, y, SBQ_F32, ldy);
+  if (rc || M == 0) return rc;
+  if (!idx || !argmax_ws) return SBQ_ERR_ARG;
+  if (!aligned(argmax_ws, 8)) return SBQ_ERR_ALIGN;
+  hipStream_t st = (hipStream_t)stream;
+  sbq::GemvArgmaxOut am{(uint8_t*)argmax_ws, idx, false};
+  if (sbq::gemv_supports(M, K, false, x_dtype)) {
+    const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, SBQ_F32, ldy, N);
+    rc = sbq::launch_gemv_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, SBQ_F32, ldy, st, yv, &am);
+  } else {
+    rc = sbq_linear_w8(x, x_dtype, M, K, ldx, packed, scale, bias, N, y, SBQ_F32, ldy, workspace, workspace_bytes,
+                       stream);
+  }
+  if (rc || am.fused) return rc;
+  return sbq::launch_argmax_rows(y, M, N, ldy, idx, st);
+}
+
+int sbq_linear_w8a8_argmax(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
+                           const float* scale, const int32_t* colsum, const float* bias, int64_t N, float* y,
+                           int64_t ldy, int64_t* idx, void* workspace, size_t workspace_bytes, void* argmax_ws,
+                           void* stream) {
+  int rc = check_linear(x, x_dtype, M, K, ldx, packed, scale, N, y, SBQ_F32, ldy);
+  if (rc || M == 0) return rc;
+  if (!colsum || !idx || !argmax_ws) return SBQ_ERR_ARG;
+  if (!aligned(argmax_ws, 8)) return SBQ_ERR_ALIGN;
+  if (!workspace || (int64_t)workspace_bytes < sbq_w8a8_workspace_bytes(M, K)) return SBQ_ERR_WORKSPACE;
+  const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, SBQ_F32, ldy, N);
+  hipStream_t st = (hipStream_t)stream;
+  sbq::GemvArgmaxOut am{(uint8_t*)argmax_ws, idx, false};
+  if (sbq::gemv_supports(M, K, true, x_dtype))
+    rc = sbq::launch_gemv_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, SBQ_F32, ldy, nullptr,
+                               ws_partials(workspace), st, yv, &am);
+  else
+    rc = sbq::launch_gemm_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, SBQ_F32, ldy, nullptr,
+                               ws_partials(workspace), ws_xq(workspace), ws_qp(workspace), st, yv);
+  if (rc || am.fused) return rc;
+  return sbq::launch_argmax_rows(y, M, N, ldy, idx, st);
 }
 
 int sbq_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* idx, void* stream) {

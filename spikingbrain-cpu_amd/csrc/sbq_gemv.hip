@@ -495,9 +495,20 @@ static int launch_gemv_xt(const GemvCfg& c, GemvArgs a, hipStream_t st) {
   return -1;
 }
 
+// The fast-path arguments with the fused greedy token attached when it is
+// asked for and applies (fp32 y, M <= 16).
+static GemvArgs with_argmax(GemvArgs a, const GemvArgmaxOut* am) {
+  if (am && a.yt == XT_F32 && a.M <= 16) {
+    a.flags |= kGemvArgmax;
+    a.am_state = am->state;
+    a.idx = am->idx;
+  }
+  return a;
+}
+
 int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                    const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
-                   bool yvec) {
+                   bool yvec, GemvArgmaxOut* am) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
   const GemvCfg c = pick_gemv(M, Nt, Kc, false, xt);
   if (!c.ok) return -1;
@@ -508,8 +519,12 @@ int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
   a.flags = (xvec ? 1 : 0) | (yvec ? 2 : 0);
   int fid, fks;
   if (pick_gemv_fast(M, K, N, xt, false, xvec, &fid, &fks)) {
-    const int rc = launch_gemv_fast_cfg(fid, fks, a, xt, false, st);
-    if (rc != -1) return rc;
+    const GemvArgs f = with_argmax(a, am);
+    const int rc = launch_gemv_fast_cfg(fid, fks, f, xt, false, st);
+    if (rc != -1) {
+      if (am) am->fused = rc == 0 && (f.flags & kGemvArgmax);
+      return rc;
+    }
   }
   switch (xt) {
     case XT_F16: return launch_gemv_xt<XT_F16, false>(c, a, st);
@@ -521,7 +536,8 @@ int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
 
 int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                      const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
-                     int64_t ldy, int32_t* acc_out, float2* partials, hipStream_t st, bool yvec) {
+                     int64_t ldy, int32_t* acc_out, float2* partials, hipStream_t st, bool yvec,
+                     GemvArgmaxOut* am) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
   const GemvCfg c = pick_gemv(M, Nt, Kc, true, xt);
   if (!c.ok) return -1;
@@ -534,8 +550,12 @@ int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
   const bool fast = pick_gemv_fast(M, K, N, xt, true, xvec, &fid, &fks);
   if (fast) {  // small x: the kernel reduces the activation min/max itself
     a.nparts = 0;
-    const int rc = launch_gemv_fast_cfg(fid, fks, a, xt, true, st);
-    if (rc != -1) return rc;
+    const GemvArgs f = with_argmax(a, am);
+    const int rc = launch_gemv_fast_cfg(fid, fks, f, xt, true, st);
+    if (rc != -1) {
+      if (am) am->fused = rc == 0 && (f.flags & kGemvArgmax);
+      return rc;
+    }
   }
   const int np = minmax_nparts(M, K);
   int rc = launch_minmax_partials(x, xt, M, K, ldx, partials, np, st);
@@ -543,8 +563,12 @@ int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
   a.partials = partials;
   a.nparts = np;
   if (fast) {
-    rc = launch_gemv_fast_cfg(fid, fks, a, xt, true, st);
-    if (rc != -1) return rc;
+    const GemvArgs f = with_argmax(a, am);
+    rc = launch_gemv_fast_cfg(fid, fks, f, xt, true, st);
+    if (rc != -1) {
+      if (am) am->fused = rc == 0 && (f.flags & kGemvArgmax);
+      return rc;
+    }
   }
   switch (xt) {
     case XT_F16: return launch_gemv_xt<XT_F16, true>(c, a, st);

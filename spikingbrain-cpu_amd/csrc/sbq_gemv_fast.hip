@@ -32,6 +32,7 @@
 
 #include "sbq_common.h"
 #include "sbq_gemv_ops.h"
+#include "sbq_index.h"
 #include "sbq_launch.h"
 
 namespace sbq {
@@ -94,6 +95,80 @@ template <int G>
 __host__ __device__ constexpr int red_bytes(int ks) { return ks * G * 64 * 16; }
 __host__ __device__ constexpr int mm_bytes() { return kFastMaxWaves * 8; }
 
+__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+
+// Fused greedy token (kGemvArgmax): `key` is this lane's best argmax_key over
+// the outputs it stored.  The workgroup folds its keys per row (lanes, then
+// its row tiles through `lds`, G * 16 keys) and merges them into the keys of
+// its slot (slot = blockIdx.x % kArgmaxSlots) with an atomic max, then counts
+// itself finished in its slot; the last workgroup of a slot counts the slot
+// finished; the last slot gathers the keys of every slot (one per lane),
+// writes each row's token and leaves the state at zero for the next launch.
+// No workgroup waits for another.  Called by every wave.
+//
+// Every value that crosses workgroups travels through device-scope atomics,
+// which the GPU performs at one point for all its XCDs, so no cache
+// write-back or invalidation is needed (an agent-scope fence per workgroup
+// costs an L2 write-back: measured 4.7x slower on the 151936-row lm_head).
+// Atomics on one address are performed one after another, so the count and
+// the keys are spread over slots (one count for all 4748 workgroups of the
+// lm_head cost 14 us).  What matters is order: a workgroup's key updates
+// are performed before its count, because the wave waits for their returned
+// old values (vmcnt 0) before it issues the count, and each later step is
+// issued only after the count it depends on has returned.
+__device__ __forceinline__ void argmax_epilogue(uint8_t* state, int64_t* idx, unsigned long long key, int ks, int G,
+                                                int M, unsigned long long* lds) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  key = umax64(key, __shfl_xor(key, 16, 64));
+  key = umax64(key, __shfl_xor(key, 32, 64));
+  if (ks < G && g == 0) lds[ks * 16 + r] = key;
+  lds_barrier();
+  if (ks != 0) return;
+  const unsigned nblk = gridDim.x, slot = blockIdx.x % kArgmaxSlots;
+  unsigned long long* const skeys = (unsigned long long*)(state + slot * kArgmaxSlotBytes);
+  unsigned* const scount = (unsigned*)(state + slot * kArgmaxSlotBytes + 128);
+  unsigned* const tcount = (unsigned*)(state + kArgmaxSlots * kArgmaxSlotBytes + 128);
+  unsigned long long prior = 0;
+  if (g == 0 && r < M) {
+    unsigned long long best = 0;
+    for (int j = 0; j < G; ++j) best = umax64(best, lds[j * 16 + r]);
+    prior = __hip_atomic_fetch_max(skeys + r, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  asm volatile("" ::"v"(prior) : "memory");  // the returned old keys are in registers: the updates are performed
+  wait_vm<0>();
+  asm volatile("" ::: "memory");
+  unsigned old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(scount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __shfl(old, 0, 64);
+  if (old != argmax_slot_members(nblk, slot, kArgmaxSlots) - 1) return;  // not the slot's last workgroup
+  if (lane == 0) {
+    __hip_atomic_store(scount, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __hip_atomic_fetch_add(tcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  old = __shfl(old, 0, 64);
+  if (old != argmax_slots_used(nblk, kArgmaxSlots) - 1) return;  // not the last slot
+  // every key is in place: lane l takes slot l's keys (clearing them), the
+  // wave keeps each row's maximum
+  unsigned long long k[16];
+  const unsigned long long* lk = (const unsigned long long*)(state + lane * kArgmaxSlotBytes);
+#pragma unroll
+  for (int row = 0; row < 16; ++row)
+    k[row] = row < M ? __hip_atomic_exchange((unsigned long long*)lk + row, 0ull, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT)
+                     : 0ull;
+#pragma unroll
+  for (int row = 0; row < 16; ++row) {
+    if (row >= M) break;
+    unsigned long long v = k[row];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = umax64(v, __shfl_xor(v, o, 64));
+    if (lane == 0) idx[row] = argmax_key_index(v);
+  }
+  if (lane == 0) __hip_atomic_store(tcount, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
 
 // QM: 0 weight-only; 1 W8A8 with the activation min/max partials of the
@@ -123,6 +198,8 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   constexpr bool kSplitX = XL && XT == XT_F32 && !W8A8;
   uint8_t* xhi = xs + xch * (int)blockDim.x * 16;  // kSplitX: bf16 planes [M][K] after the raw copy
   uint8_t* xlo = xhi + M * K * 2;
+  // end of the x copy and planes: the fused argmax keeps G * 16 keys there
+  const int xend = (XL ? xch * (int)blockDim.x * 16 : 0) + (kSplitX ? M * K * 4 : 0);
 
   // epilogue operands of row tile `ks` (wave ks < G finishes tile ks)
   const int nte = min(nt0 + min(ks, G - 1), a.Nt - 1);
@@ -304,45 +381,58 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
     for (int j = 0; j < G; ++j) red[(ks * G + j) * 64 + lane] = acc[j];
     lds_barrier();
   }
-  if (ks >= G || r >= M) return;
+  // With a fused argmax every lane of every wave reaches the one call of
+  // argmax_epilogue below with the wave reconverged: it holds a barrier and
+  // cross-lane steps, so no lane may leave early or call it from a branch.
+  const bool am = a.flags & kGemvArgmax;
   const int nt = nt0 + ks;
   const int n = nt * 16 + 4 * g;
-  if (nt >= a.Nt || n >= a.N) return;
-  Acc s;
-  if (KS > 1) {
-    s = red[ks * 64 + lane];
-    for (int i = 1; i < KS; ++i) s += red[(i * G + ks) * 64 + lane];
-  } else {
-    s = acc[0];  // one wave implies one row tile (the host keeps KS >= G)
+  const bool live = ks < G && r < M && nt < a.Nt && n < a.N;
+  if (!live && !am) return;
+  unsigned long long key = 0;
+  if (live) {
+    Acc s;
+    if (KS > 1) {
+      s = red[ks * 64 + lane];
+      for (int i = 1; i < KS; ++i) s += red[(i * G + ks) * 64 + lane];
+    } else {
+      s = acc[0];  // one wave implies one row tile (the host keeps KS >= G)
+    }
+    const int nvalid = min(4, a.N - n);
+    f32x4 o;
+    if constexpr (PT) {
+      const float st = a.rscale[r];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (a.acc_out && v < nvalid) a.acc_out[(int64_t)r * a.N + n + v] = s[v];
+        const float mult = st * sc[v];
+        o[v] = a.bias ? __builtin_fmaf((float)s[v], mult, bi[v]) : (float)s[v] * mult;
+      }
+    } else if constexpr (W8A8) {
+      const int corr = 128 - qp.zp;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int av = s[v] + corr * cs[v];
+        if (a.acc_out && v < nvalid) a.acc_out[(int64_t)r * a.N + n + v] = av;
+        const float mult = qp.scale * sc[v];
+        o[v] = a.bias ? __builtin_fmaf((float)av, mult, bi[v]) : (float)av * mult;
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float out = s[v] * sc[v];
+        if (a.bias) out = out + bi[v];
+        o[v] = out;
+      }
+    }
+    store_y4(a.y, a.yt, (int64_t)r * a.ldy + n, o, (a.flags & kGemvYVec) && nvalid == 4, nvalid);
+    if (am) {  // fp32 y: the key of each stored value
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (v < nvalid) key = umax64(key, argmax_key(o[v], n + v));
+    }
   }
-  const int nvalid = min(4, a.N - n);
-  f32x4 o;
-  if constexpr (PT) {
-    const float st = a.rscale[r];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      if (a.acc_out && v < nvalid) a.acc_out[(int64_t)r * a.N + n + v] = s[v];
-      const float mult = st * sc[v];
-      o[v] = a.bias ? __builtin_fmaf((float)s[v], mult, bi[v]) : (float)s[v] * mult;
-    }
-  } else if constexpr (W8A8) {
-    const int corr = 128 - qp.zp;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int av = s[v] + corr * cs[v];
-      if (a.acc_out && v < nvalid) a.acc_out[(int64_t)r * a.N + n + v] = av;
-      const float mult = qp.scale * sc[v];
-      o[v] = a.bias ? __builtin_fmaf((float)av, mult, bi[v]) : (float)av * mult;
-    }
-  } else {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      float out = s[v] * sc[v];
-      if (a.bias) out = out + bi[v];
-      o[v] = out;
-    }
-  }
-  store_y4(a.y, a.yt, (int64_t)r * a.ldy + n, o, (a.flags & 2) && nvalid == 4, nvalid);
+  if (am) argmax_epilogue(a.am_state, a.idx, key, ks, G, M, (unsigned long long*)(xs + xend));
 }
 
 namespace {
@@ -414,6 +504,7 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   const int xch = c.XL ? (int)((xbytes / 16 + T - 1) / T) : 0;
   size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
   if (split) lds += (size_t)a.M * a.K * 4;  // bf16 high / remainder planes
+  if (a.flags & kGemvArgmax) lds += (size_t)c.G * 16 * 8;  // the fused argmax's keys per row tile
   const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
   if (qm == 2 && (xbytes > (int64_t)kFusedChunks * 16 * T || ks < kFusedMinWaves)) return -1;
 #define SBQ_FAST_QM(XT_)                                                  \

@@ -25,8 +25,21 @@ struct GemvArgs {
   const float2* partials;
   int nparts;
   const float* rscale;  // per-token W8A8: s_t [M]
-  int flags;
+  int flags;            // kGemvXVec | kGemvYVec | kGemvArgmax
+  // greedy token of each row (flags & kGemvArgmax; fp32 y): the argmax state
+  // (per-slot keys and counts, zero before the launch and zero again after
+  // it) and the int64 token per row
+  uint8_t* am_state;
+  int64_t* idx;
 };
+// The fused argmax's state: kArgmaxSlots slots of 16 row keys (128 bytes) and
+// a count, kArgmaxSlotBytes apart, then the count of finished slots.
+constexpr int kArgmaxSlots = 64;
+constexpr int kArgmaxSlotBytes = 256;
+constexpr int kArgmaxStateBytes = (kArgmaxSlots + 1) * kArgmaxSlotBytes;
+constexpr int kGemvXVec = 1;     // x rows 16-byte aligned: vector loads
+constexpr int kGemvYVec = 2;     // y rows aligned for 4-element vector stores
+constexpr int kGemvArgmax = 4;   // also pick each row's argmax (fused greedy token)
 
 // ---------------------------------------------------------------------------
 // Raw activations of one lane: x[m][k0 .. k0+15], m = mt*16 + r,

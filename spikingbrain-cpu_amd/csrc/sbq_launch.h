@@ -34,11 +34,21 @@ struct GemvArgs;
 bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks);
 int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, hipStream_t st);
 
+// Fused greedy token of the decode GEMV (fp32 y, M <= 16): the argmax state
+// (kArgmaxStateBytes, zero before a launch, zero again after it) and the
+// int64 token per row.  The launcher sets `fused` when the GEMV it ran also
+// picked the tokens; otherwise the caller picks them from y.
+struct GemvArgmaxOut {
+  uint8_t* state;
+  int64_t* idx;
+  bool fused;
+};
+
 // Weight-only linear.  xvec: x and every row of x start 16-byte aligned (vector
 // loads allowed).  yvec: y rows are 16-byte aligned and N % 4 == 0.
 int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                    const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
-                   bool yvec);
+                   bool yvec, GemvArgmaxOut* am = nullptr);
 // ws: device scratch (nullable, 256-byte aligned) of ws_bytes bytes, laid out
 // by w8_ws_layout.  With enough of it the fp16 GEMM takes its per-row sums of x
 // from a pre-pass, and fp32 / bf16 activations are staged as scaled fp16 planes
@@ -70,7 +80,8 @@ int launch_stage_act(const void* x, int xt, int64_t ldx, int64_t M, int64_t K, _
 // decode fast path reduces a small x in the kernel instead).
 int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                      const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
-                     int64_t ldy, int32_t* acc_out, float2* partials, hipStream_t st, bool yvec);
+                     int64_t ldy, int32_t* acc_out, float2* partials, hipStream_t st, bool yvec,
+                     GemvArgmaxOut* am = nullptr);
 // The GEMM quantizes x once into xq (s8 [M][Kc*64]) and writes (s_x, zp) to
 // qpbuf[0..1] (zp as int bits) before the tiled pipeline reads them.
 int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,

@@ -290,8 +290,9 @@ __global__ __launch_bounds__(256) void stage_act_kernel(const void* __restrict__
   }
 }
 
-// One workgroup per row; each thread keeps four independent running bests so
-// that four vector loads are in flight at a time.
+// One workgroup per row; each thread keeps four independent running bests
+// and has sixteen vector loads in flight at a time (a 151936-wide row is
+// three rounds of loads).
 __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restrict__ y, int N, int64_t ldy,
                                                            int64_t* __restrict__ out, int vec) {
   const float* row = y + (int64_t)blockIdx.x * ldy;
@@ -307,6 +308,15 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restri
   if (vec) {
     const int n4 = N / 4;
     int c = t;
+    for (; c + 15 * T < n4; c += 16 * T) {
+      f32x4 v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = *(const f32x4*)(row + 4 * (c + u * T));
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) arg_take(v[u][j], 4 * (c + u * T) + j, bv[u & 3], bi[u & 3]);
+    }
     for (; c + 3 * T < n4; c += 4 * T) {
       f32x4 v[4];
 #pragma unroll

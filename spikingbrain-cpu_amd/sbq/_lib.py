@@ -13,6 +13,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsbq.so"
 SBQ_OK = 0
 SBQ_F32, SBQ_F16, SBQ_BF16 = 0, 1, 2
 SBQ_NOALLOC_XQ_BYTES = 8 << 20  # include/sbq.h
+SBQ_ARGMAX_WS_BYTES = 16640  # include/sbq.h
 
 # Every entry point declared in include/sbq.h, with its ctypes signature.
 _P = ctypes.c_void_p
@@ -35,6 +36,8 @@ SIGNATURES = {
     "sbq_linear_w8a8_token": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _L, _P, _I, _L, _P, _P, _S, _P]),
     "sbq_linear_w8a8_noalloc": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _L, _P, _I, _L, _P, _P]),
     "sbq_argmax_rows": (_I, [_P, _L, _L, _L, _P, _P]),
+    "sbq_linear_w8_argmax": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _L, _P, _L, _P, _P, _S, _P, _P]),
+    "sbq_linear_w8a8_argmax": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _L, _P, _L, _P, _P, _S, _P, _P]),
 }
 
 _lib = None

@@ -297,6 +297,84 @@ def greedy_tokens(logits: torch.Tensor) -> torch.Tensor:
     return out.reshape(shape[:-1])
 
 
+def argmax_state(device: torch.device) -> torch.Tensor:
+    """The zeroed state (keys and count) of linear_w8_argmax /
+    linear_w8a8_argmax: every call leaves it zero again, so one state serves
+    every call on one stream."""
+    return torch.zeros((_lib.SBQ_ARGMAX_WS_BYTES,), dtype=torch.uint8, device=device)
+
+
+def _check_argmax(fn: str, x2: torch.Tensor, state: torch.Tensor, idx: torch.Tensor | None) -> torch.Tensor:
+    M = x2.shape[0]
+    if (state.dtype != torch.uint8 or state.device != x2.device or not state.is_contiguous()
+            or state.numel() < _lib.SBQ_ARGMAX_WS_BYTES or state.data_ptr() % 8):
+        raise ValueError(f"{fn}: argmax state must come from argmax_state() on {x2.device}")
+    if idx is None:
+        return torch.empty((M,), dtype=torch.int64, device=x2.device)
+    if idx.dtype != torch.int64 or idx.device != x2.device or not idx.is_contiguous() or idx.numel() < M:
+        raise ValueError(f"{fn}: idx must be a contiguous int64 tensor of M={M} elements on {x2.device}")
+    return idx
+
+
+def linear_w8_argmax(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None, N: int,
+                     state: torch.Tensor, out: torch.Tensor | None = None, idx: torch.Tensor | None = None,
+                     workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """lm_head (model.py:445-447) and its greedy token (engine.py:30-31) in one
+    pass: (fp32 logits [M, N], int64 token [M]), the token being the first
+    index of each row's maximum with NaN above every number.  `state` comes
+    from argmax_state() (one per stream).  The logits are linear_w8's (the
+    same workspace rule for prefill sizes)."""
+    x2 = _as_activation(x2)
+    M, K = x2.shape
+    y = out if out is not None else torch.empty((M, N), dtype=torch.float32, device=x2.device)
+    if y.dtype != torch.float32:
+        raise ValueError("linear_w8_argmax: the logits are fp32")
+    ws = workspace
+    if ws is None and M > 16:
+        ws = w8_workspace(M, K, x2.device, x2.dtype)
+    _check_operands("linear_w8_argmax", x2, packed, N, y, (("scale", scale, torch.float32),
+                                                           ("bias", bias, torch.float32)), ws)
+    idx = _check_argmax("linear_w8_argmax", x2, state, idx)
+    with torch.cuda.device(x2.device):
+        _lib.check(_lib.load().sbq_linear_w8_argmax(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
+                                                    _ptr(scale), _ptr(bias), N, _ptr(y), y.stride(0), _ptr(idx),
+                                                    _ptr(ws), _nbytes(ws), _ptr(state), _stream(x2.device)),
+                   "sbq_linear_w8_argmax")
+    return y, idx
+
+
+def linear_w8a8_argmax(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, colsum: torch.Tensor,
+                       bias: torch.Tensor | None, N: int, state: torch.Tensor, workspace: torch.Tensor | None = None,
+                       out: torch.Tensor | None = None,
+                       idx: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """int8-dyn lm_head and its greedy token in one pass (see linear_w8_argmax)."""
+    x2 = _as_activation(x2)
+    M, K = x2.shape
+    y = out if out is not None else torch.empty((M, N), dtype=torch.float32, device=x2.device)
+    if y.dtype != torch.float32:
+        raise ValueError("linear_w8a8_argmax: the logits are fp32")
+    ws = workspace if workspace is not None else w8a8_workspace(M, K, x2.device)
+    _check_operands("linear_w8a8_argmax", x2, packed, N, y, (("scale", scale, torch.float32),
+                                                             ("bias", bias, torch.float32),
+                                                             ("colsum", colsum, torch.int32)), ws)
+    idx = _check_argmax("linear_w8a8_argmax", x2, state, idx)
+    with torch.cuda.device(x2.device):
+        _lib.check(_lib.load().sbq_linear_w8a8_argmax(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
+                                                      _ptr(scale), _ptr(colsum), _ptr(bias), N, _ptr(y),
+                                                      y.stride(0), _ptr(idx), _ptr(ws), _nbytes(ws), _ptr(state),
+                                                      _stream(x2.device)),
+                   "sbq_linear_w8a8_argmax")
+    return y, idx
+
+
+def _greedy_state(module: nn.Module, device: torch.device) -> torch.Tensor:
+    st = module.__dict__.get("_argmax_state")
+    if st is None or st.device != device:
+        st = argmax_state(device)
+        module.__dict__["_argmax_state"] = st
+    return st
+
+
 def act_qparams(x2: torch.Tensor) -> tuple[float, int]:
     """The per-tensor (scale, zero_point) the int8-dyn path uses for x2 [M, K]."""
     x2 = _as_activation(x2)
@@ -404,6 +482,20 @@ class Int8Linear(nn.Module):
         out = _run_on_device(x, self.qweight.device, run)
         return out.reshape(*shape[:-1], -1)
 
+    def forward_greedy(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """forward(x) and the greedy token of each row in one pass, for the
+        lm_head (model.py:445-447, engine.py:30-31): (fp32 logits [..., N],
+        int64 tokens [...]).  x must be on the module's GPU."""
+        _check_in_features(x, self.in_features)
+        self._refresh()
+        if x.device != self.qweight.device:
+            raise ValueError(f"sbq: input on {x.device} but the layer lives on {self.qweight.device}")
+        shape = x.shape
+        bias = None if self.bias is None else self.bias.float()
+        y, idx = linear_w8_argmax(x.reshape(-1, shape[-1]), self.packed, self.scale.float(), bias, self.out_features,
+                                  _greedy_state(self, x.device))
+        return y.reshape(*shape[:-1], -1), idx.reshape(shape[:-1])
+
 
 class _Fp32Buffers:
     """Mixin: the buffers named in ``_fp32_buffers`` keep their fp32 values
@@ -469,6 +561,20 @@ class DynamicInt8Linear(_Fp32Buffers, nn.Module):
 
         out = _run_on_device(x, self.packed.device, run)
         return out.reshape(*shape[:-1], -1)
+
+    def forward_greedy(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """forward(x) and the greedy token of each row in one pass (see
+        Int8Linear.forward_greedy); per-tensor granularity only."""
+        if getattr(self, "granularity", "tensor") != "tensor":
+            raise ValueError("forward_greedy: per-tensor int8-dyn only")
+        _check_in_features(x, self.in_features)
+        if x.device != self.packed.device:
+            raise ValueError(f"sbq: input on {x.device} but the layer lives on {self.packed.device}")
+        shape = x.shape
+        bias = None if self.bias is None else self.bias.float()
+        y, idx = linear_w8a8_argmax(x.reshape(-1, shape[-1]), self.packed, self.scale.float(), self.colsum, bias,
+                                    self.out_features, _greedy_state(self, x.device))
+        return y.reshape(*shape[:-1], -1), idx.reshape(shape[:-1])
 
 
 def _dyn_from_quantized(qweight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None) -> "DynamicInt8Linear":

@@ -325,3 +325,113 @@ def test_loader_swap_inference_mode_and_dtype_moves(dev):
     assert fz.scale.dtype == torch.float32 and fz.bias.dtype == torch.float32
     for a, b in zip(fz(x), fb):
         np.testing.assert_array_equal(a.cpu().numpy(), b)
+
+
+# ---------------------------------------------------------------------------
+# lm_head and its greedy token in one pass (model.py:445-447, engine.py:30-31)
+# ---------------------------------------------------------------------------
+def _check_greedy(y, tok, state=None):
+    """tok must be torch.argmax of the logits the same call returned, and
+    the argmax state must be back at zero."""
+    np.testing.assert_array_equal(tok.cpu().numpy(), torch.argmax(y.cpu(), dim=-1).numpy())
+    if state is not None:
+        assert int(state.cpu().count_nonzero()) == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["int8", "int8-dyn"])
+@pytest.mark.parametrize("M,K,xd", [(1, 4096, "f32"), (1, 4096, "f16"), (8, 4096, "f32"), (3, 2560, "f32"),
+                                    (16, 2560, "f16"), (1, 2560, "bf16")])
+def test_lm_head_greedy_one_pass(dev, fmt, M, K, xd):
+    announce(f"lm_head greedy fmt={fmt} M={M} K={K} x={xd}")
+    V = 151936
+    w = gpu_weight(V, K, 61, dev)
+    lm = quant.make_linear(fmt, w)
+    x = cpu_x(M, K, 62).to(DT[xd]).to(dev)
+    y_plain = lm(x)
+    for _ in range(3):  # repeated calls reuse the state the last one left at zero
+        y, tok = lm.forward_greedy(x)
+        np.testing.assert_array_equal(y.cpu().numpy(), y_plain.cpu().numpy())
+        _check_greedy(y, tok, lm._argmax_state)
+    # against the oracle: its logits over the GPU's 32 best columns and sampled
+    # ones must put their maximum at the GPU's token
+    cand = np.unique(np.concatenate([torch.topk(y, 32, dim=-1).indices.cpu().numpy().ravel(),
+                                     tile_sample(V, 63, cap=64)]))
+    q, s = ref_rows(w, cand)
+    xf = x.float().cpu().numpy()
+    if fmt == "int8":
+        ref = oracle.int8_linear(xf, q, s)
+    else:
+        _, ref = ref_w8a8(xf, np.arange(M), q, s)
+    np.testing.assert_array_equal(cand[np.argmax(ref, axis=-1)], tok.cpu().numpy())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["int8", "int8-dyn"])
+def test_lm_head_greedy_ties_nan_zeros(dev, fmt):
+    """Equal logits far apart (first index wins), NaN logits (the first NaN
+    wins), all-zero logits (index 0), through the fused path at V=151936."""
+    announce(f"lm_head greedy ties/NaN fmt={fmt}")
+    V, K = 151936, 4096
+    x = cpu_x(1, K, 64)
+    w = gpu_weight(V, K, 65, dev)
+    big = 0.1 * torch.sign(x[0]).to(dev)
+    for row in (3, 75000, 151000):  # identical rows, far larger than the rest
+        w[row] = big
+    lm = quant.make_linear(fmt, w)
+    y, tok = lm.forward_greedy(x.to(dev))
+    assert tok.item() == 3 and y[0, 3].item() == y[0, 151000].item()
+    _check_greedy(y, tok, lm._argmax_state)
+    b = torch.zeros(V)
+    b[90000] = b[140000] = float("nan")
+    lmb = quant.make_linear(fmt, w, b.to(dev))
+    y, tok = lmb.forward_greedy(x.to(dev))
+    assert tok.item() == 90000
+    _check_greedy(y, tok, lmb._argmax_state)
+    y, tok = lm.forward_greedy(torch.zeros(2, K, device=dev))
+    assert tok.tolist() == [0, 0] and float(y.abs().max()) == 0.0
+    _check_greedy(y, tok, lm._argmax_state)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(20, 5000, 1024), (40, 3000, 512), (2, 1000, 200)])
+def test_greedy_one_pass_other_shapes(dev, M, N, K):
+    """Shapes the fused GEMV does not take (M > 16, ragged K): the logits
+    kernel and then the row argmax; same tokens."""
+    announce(f"greedy other shapes M={M} N={N} K={K}")
+    for fmt in ("int8", "int8-dyn"):
+        lm = quant.make_linear(fmt, gpu_weight(N, K, 66, dev))
+        x = cpu_x(M, K, 67).to(dev)
+        y, tok = lm.forward_greedy(x)
+        np.testing.assert_array_equal(y.cpu().numpy(), lm(x).cpu().numpy())
+        _check_greedy(y, tok, lm._argmax_state)
+
+
+@pytest.mark.gpu
+def test_greedy_one_pass_graph_replays(dev):
+    """The fused call captured in a HIP graph: every replay (new activations,
+    eager work in between) gives the argmax of its own logits, and leaves the
+    state at zero for the next replay."""
+    announce("greedy graph replays")
+    V, K = 151936, 4096
+    for fmt in ("int8", "int8-dyn"):
+        lm = quant.make_linear(fmt, gpu_weight(V, K, 68, dev))
+        x = cpu_x(1, K, 69).to(dev)
+        lm.forward_greedy(x)  # state and workspace exist before capture
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            lm.forward_greedy(x)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            y, tok = lm.forward_greedy(x)
+        for i in range(4):
+            x.copy_(cpu_x(1, K, 70 + i).to(dev))
+            g.replay()
+            torch.cuda.synchronize()
+            _check_greedy(y, tok, lm._argmax_state)
+            np.testing.assert_array_equal(y.cpu().numpy(), lm(x).cpu().numpy())
+            lm(torch.randn(3, K, device=dev))  # eager work between replays
