@@ -243,6 +243,49 @@ def lm_head_greedy_bench(ctx, V=151936, K=4096, M=1, steps=40, warmup=5):
     return res
 
 
+def device_state_bench(ctx, fmt="int8", H=2048, F=5632, blocks=4, V=32000, heads=16, max_len=512, steps=48):
+    """Greedy decoding with a toy decoder (tests/toy_decoder.py: our own
+    small model of the reference's projection pattern, random weights) in
+    three placements: state on the CPU as the reference model keeps it (every
+    projection copies x up and y back, argmax on the CPU); state on the GPU
+    with eager launches; state on the GPU with one HIP graph replay per token.
+    Reports per-token time and tokens/s (the linears' share is what this path
+    owns; attention and norms are plain torch)."""
+    torch = ctx.torch
+    sys.path.insert(0, str(ROOT / "tests"))
+    from toy_decoder import ToyDecoder, toy_weights
+
+    w, emb = toy_weights(H, F, blocks, V)
+    res = {"fmt": fmt, "H": H, "F": F, "blocks": blocks, "vocab": V, "heads": heads, "max_len": max_len,
+           "steps": steps, "linears_per_token": 7 * blocks + 1}
+
+    def per_token(run, n, sync):
+        run(2)  # warm
+        sync()
+        t0 = time.perf_counter()
+        run(n)
+        sync()
+        return (time.perf_counter() - t0) / n
+
+    cpu = ToyDecoder(fmt, w, emb, heads, max_len, "cpu")
+    cpu.reset(1)
+    t = per_token(lambda n: [cpu.step_cpu_state() for _ in range(n)], min(steps, 16), torch.cuda.synchronize)
+    res["cpu_state_ms_per_token"] = t * 1e3
+    del cpu
+    gpu = ToyDecoder(fmt, w, emb, heads, max_len, ctx.dev)
+    gpu.reset(1)
+    t = per_token(lambda n: [gpu.step_device() for _ in range(n)], steps, torch.cuda.synchronize)
+    res["device_eager_ms_per_token"] = t * 1e3
+    gpu.reset(1)
+    g = ctx.graph(gpu.step_device)
+    gpu.reset(1)
+    t = per_token(lambda n: [g.replay() for _ in range(n)], steps, torch.cuda.synchronize)
+    res["device_graph_ms_per_token"] = t * 1e3
+    for k in ("cpu_state", "device_eager", "device_graph"):
+        res[k + "_tokens_per_s"] = 1e3 / res[k + "_ms_per_token"]
+    return res
+
+
 # ---------------------------------------------------------------------------
 # prefill GEMM and int8-dyn
 # ---------------------------------------------------------------------------
@@ -670,7 +713,7 @@ def main():
         gemv_probe(ctx, N, K, M)
         return
     if args.only:
-        fn = {"lm_head_greedy": lm_head_greedy_bench}[args.only]
+        fn = {"lm_head_greedy": lm_head_greedy_bench, "device_state": device_state_bench}[args.only]
         print(json.dumps({args.only: fn(ctx)}), flush=True)
         return
     log("decode M=1 (headline)")
@@ -697,6 +740,8 @@ def main():
                                     for dt in (ctx.torch.bfloat16, ctx.torch.float32)]
         log("lm_head and its greedy token")
         extra["lm_head_greedy"] = lm_head_greedy_bench(ctx)
+        log("device-resident decode (toy decoder)")
+        extra["device_state"] = device_state_bench(ctx)
         log("int8-dyn")
         extra["w8a8"] = [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)]
         log("36-layer linear stack")

@@ -435,3 +435,60 @@ def test_greedy_one_pass_graph_replays(dev):
             _check_greedy(y, tok, lm._argmax_state)
             np.testing.assert_array_equal(y.cpu().numpy(), lm(x).cpu().numpy())
             lm(torch.randn(3, K, device=dev))  # eager work between replays
+
+
+# ---------------------------------------------------------------------------
+# device-resident model state (the callers on either side of the linears)
+# ---------------------------------------------------------------------------
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["int8", "int8-dyn"])
+def test_device_resident_decode(dev, fmt):
+    """A toy decoder (tests/toy_decoder.py) generating greedily with its state
+    on the GPU: eager steps and one captured HIP graph replayed per token give
+    the same tokens and bit-identical logits; the same decoder with its state
+    on the CPU (the reference's placement), fed the same tokens, gives the
+    same logits to rel-L2 1e-4 (int8) / 5e-3 (int8-dyn: a one-ulp difference
+    in a CPU-computed activation can move one quantization step) and the same
+    greedy token wherever the top two logits are apart."""
+    from toy_decoder import ToyDecoder, toy_weights
+
+    announce(f"device-resident decode fmt={fmt}")
+    H, F, B, V, heads, L, steps, first = 256, 768, 2, 1000, 4, 32, 12, 7
+    w, emb = toy_weights(H, F, B, V)
+    gpu = ToyDecoder(fmt, w, emb, heads, L, dev)
+    gpu.reset(first)
+    eager_logits, eager_tok = [], []
+    for _ in range(steps):
+        eager_logits.append(gpu.step_device().clone())
+        eager_tok.append(int(gpu.tok.item()))
+    # one step captured (the warm-up creates the argmax state and workspaces)
+    gpu.reset(first)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        gpu.step_device()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        logits = gpu.step_device()
+    gpu.reset(first)
+    for i in range(steps):
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(gpu.tok.item()) == eager_tok[i], i
+        np.testing.assert_array_equal(logits.cpu().numpy(), eager_logits[i].cpu().numpy())
+    assert int(gpu.pos.item()) == steps
+    # the reference's placement, teacher-forced with the device's tokens
+    cpu = ToyDecoder(fmt, w, emb, heads, L, "cpu")
+    cpu.reset(first)
+    tol = 1e-4 if fmt == "int8" else 5e-3
+    for i in range(steps):
+        inp = torch.tensor([first if i == 0 else eager_tok[i - 1]])
+        lc = cpu.step_cpu_state(inp)
+        ld = eager_logits[i].cpu()
+        assert lc.device.type == "cpu"
+        assert oracle.rel_l2(lc.numpy(), ld.numpy()) <= tol, i
+        top2 = torch.topk(ld, 2).values
+        if float(top2[0] - top2[1]) > 1e-2 * float(top2[0].abs()):
+            assert int(cpu.tok.item()) == eager_tok[i], i
