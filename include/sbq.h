@@ -131,6 +131,18 @@ int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
  * scratch). */
 int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K, int x_dtype);
 
+/* Workspace bytes that let sbq_linear_w8 (w8a8 = 0) or sbq_linear_w8a8
+ * (w8a8 = 1) run their fastest path for y [M, N] = x [M, K] * W^T with x of
+ * x_dtype: the sizes of sbq_w8_workspace_bytes / sbq_w8a8_workspace_bytes
+ * plus, for prefill shapes whose grid would leave CUs idle, the tile counters
+ * and fp32 / int32 partial tiles of a GEMM that splits K over workgroups (its
+ * last split per tile adds the partials in a fixed order, so results do not
+ * depend on timing).  Those entry points split K only when given this much;
+ * with the smaller sizes they run the same shapes unsplit.  0 for a bad
+ * argument.  No counterpart in the reference (its CPU matmul needs no
+ * scratch). */
+int64_t sbq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8);
+
 /* ---- int8-dyn W8A8 linear (DynamicInt8Linear.forward, quant.py:63-66) ---- */
 
 /* Workspace bytes sbq_linear_w8a8 / sbq_act_qparams need for an [M, K] input:

@@ -61,13 +61,22 @@ inline float* ws_stok(void* workspace, int64_t M, int64_t K) {
 // from a caller's workspace or from the no-allocation array.
 int linear_w8a8_run(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
                     const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int y_dtype,
-                    int64_t ldy, int32_t* acc_out, float2* parts, float* qp, int8_t* xq, hipStream_t st) {
+                    int64_t ldy, int32_t* acc_out, float2* parts, float* qp, int8_t* xq, uint8_t* split,
+                    int64_t split_bytes, hipStream_t st) {
   const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
   if (sbq::gemv_supports(M, K, true, x_dtype))
     return sbq::launch_gemv_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
                                  parts, st, yv);
   return sbq::launch_gemm_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
-                               parts, xq, qp, st, yv);
+                               parts, xq, qp, st, yv, split, split_bytes);
+}
+
+// The split-K area after a W8A8 workspace's layout, and its bytes.
+inline uint8_t* ws_split(void* workspace, int64_t M, int64_t K) {
+  return (uint8_t*)ws_stok(workspace, M, K) + ((M * 4 + 255) & ~(int64_t)255);
+}
+inline int64_t ws_split_bytes(void* workspace, size_t workspace_bytes, int64_t M, int64_t K) {
+  return (int64_t)workspace_bytes - (int64_t)(ws_split(workspace, M, K) - (uint8_t*)workspace);
 }
 
 // ---------------------------------------------------------------------------
@@ -191,6 +200,16 @@ int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K) {
   return 256 + kWsPartialBytes + kWsQpBytes + ((xq + 255) & ~(int64_t)255) + ((M * 4 + 255) & ~(int64_t)255);
 }
 
+int64_t sbq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8) {
+  if (M < 0 || N < 1 || K < 1 || M > kIntMax || N > kIntMax || K > kIntMax || !valid_dtype(x_dtype)) return 0;
+  if (w8a8 != 0 && w8a8 != 1) return 0;
+  const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
+  const int64_t base = w8a8 ? sbq_w8a8_workspace_bytes(M, K) : sbq_w8_workspace_bytes(M, K, x_dtype);
+  if (sbq::gemv_supports(M, K, w8a8 != 0, x_dtype)) return base;
+  // the GEMM's operands are s8 (W8A8) or fp16 (weight-only, fp32 / bf16 staged as fp16 planes)
+  return base + sbq::split_area_bytes(sbq::plan_gemm_dl(w8a8 != 0, 1, M, Nt, Kc, true));
+}
+
 int sbq_act_qparams(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, float* scale_out,
                     int32_t* zp_out, void* workspace, size_t workspace_bytes, void* stream) {
   if (!valid_dtype(x_dtype)) return SBQ_ERR_DTYPE;
@@ -224,7 +243,8 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
   if (!colsum) return SBQ_ERR_ARG;
   if (!workspace || (int64_t)workspace_bytes < sbq_w8a8_workspace_bytes(M, K)) return SBQ_ERR_WORKSPACE;
   return linear_w8a8_run(x, x_dtype, M, K, ldx, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
-                         ws_partials(workspace), ws_qp(workspace), ws_xq(workspace), (hipStream_t)stream);
+                         ws_partials(workspace), ws_qp(workspace), ws_xq(workspace), ws_split(workspace, M, K),
+                         ws_split_bytes(workspace, workspace_bytes, M, K), (hipStream_t)stream);
 }
 
 int sbq_linear_w8a8_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
@@ -242,7 +262,7 @@ int sbq_linear_w8a8_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, in
   // nothing is cleared between calls
   uint8_t* base = (uint8_t*)s;
   return linear_w8a8_run(x, x_dtype, M, K, ldx, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
-                         (float2*)base, (float*)(base + kWsPartialBytes), (int8_t*)(base + kNoAllocHead),
+                         (float2*)base, (float*)(base + kWsPartialBytes), (int8_t*)(base + kNoAllocHead), nullptr, 0,
                          (hipStream_t)stream);
 }
 
@@ -283,7 +303,8 @@ int sbq_linear_w8a8_argmax(const void* x, int x_dtype, int64_t M, int64_t K, int
                                ws_partials(workspace), st, yv, &am);
   else
     rc = sbq::launch_gemm_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, SBQ_F32, ldy, nullptr,
-                               ws_partials(workspace), ws_xq(workspace), ws_qp(workspace), st, yv);
+                               ws_partials(workspace), ws_xq(workspace), ws_qp(workspace), st, yv,
+                               ws_split(workspace, M, K), ws_split_bytes(workspace, workspace_bytes, M, K));
   if (rc || am.fused) return rc;
   return sbq::launch_argmax_rows(y, M, N, ldy, idx, st);
 }

@@ -267,6 +267,10 @@ __device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rs, uint32_
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 
+// Cache policy of buffer accesses that other XCDs read or wrote (sc1: coherent
+// at device scope without an L2 write-back or invalidate).
+constexpr int kCoherent = 16;
+
 // s_waitcnt vmcnt(n) (n < 64) leaving the other counters unconstrained.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -321,6 +325,11 @@ struct GemmArgs {
   int kx;               // activation K tiles (0: Kc); 2 * Kc = two planes over the same weights
   int flags;            // bit 1: x rows vector loads; 2: y rows 4-element vector stores;
                         // 4: W8A8 per-token epilogue; 8: y and ldy 16-byte aligned
+  // split K (gridDim.z > 1): partial tiles [tile][split] of dl_tile_bytes()
+  // each, and one counter per output tile (zeroed by the pre-pass)
+  uint8_t* part;
+  uint32_t* tcount;
+  int splits;
 };
 
 // KG groups of WN x WM waves: group kg streams the K tiles
@@ -355,7 +364,10 @@ constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950: LDS per workgroup
 // barrier; two tiles per stage restore the ratio.  Sub-stage j of a stage holds
 // weight tiles and activation columns of K tile KT * stage + j, laid out as a
 // one-tile stage.
-template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false, int KT = 1>
+// SK: K split over gridDim.z workgroups with the partial-tile fixup (only the
+// configurations the split plan uses are built with it: the fixup's registers
+// would otherwise spill in the large-tile configurations).
+template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false, int KT = 1, bool SK = false>
 __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) void gemm_dl_kernel(const GemmArgs a) {
   typedef GemmOp<XT> Op;
   typedef typename Op::V V;
@@ -400,9 +412,14 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   // stages of activation K tiles: x tile kc meets weight tile kc mod Kc (the
   // host keeps Kc % KT == 0)
   const int KX = (a.kx > 0 ? a.kx : Kc) / KT;
-  const int KW = (KX + KG - 1) / KG;
-  const int kbeg = kg * KW;
-  const int cnt = min(KW, KX - kbeg);  // tiles of this group (<= 0: none)
+  // split K over gridDim.z workgroups: split z takes stage steps [zb, zb + zc)
+  // (the host keeps every split non-empty), its KG groups share them out
+  const int S = SK ? (int)gridDim.z : 1, z = SK ? (int)blockIdx.z : 0;
+  const int KXs = (KX + S - 1) / S;
+  const int zb = z * KXs, zc = min(KXs, KX - zb);
+  const int KW = (zc + KG - 1) / KG;
+  const int kbeg = zb + kg * KW;
+  const int cnt = min(KW, zb + zc - kbeg);  // tiles of this group (<= 0: none)
   const uint8_t* xg = (const uint8_t*)a.x;
   const int64_t xrow = I8 ? a.ldx : a.ldx * 2;  // bytes per activation row
 
@@ -439,7 +456,7 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   const int xslot = __builtin_amdgcn_readfirstlane(WBYTES + w * (XR / GW) * 1024);
   auto issue = [&](int i, int st) {
     // clamped: the surplus stages of a short last group are never multiplied
-    const int ks = KG == 1 ? i : max(0, min(kbeg + min(i, cnt - 1), KX - 1));
+    const int ks = KG == 1 ? zb + i : max(0, min(kbeg + min(i, cnt - 1), KX - 1));
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
       const int kc = ks * KT + j;
@@ -555,6 +572,65 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
         for (int b = 0; b < FM; ++b) acc[t][b] += red[(((k - 1) * GW + w) * FN * FM + t * FM + b) * 64 + lane];
   }
 
+  if constexpr (SK) {
+    // Split K: store this split's partial tile (device-coherent stores), then
+    // count the tile's splits; the last split to arrive adds every split's
+    // partial in split order (the same fp32 sum whichever split is last) and
+    // runs the epilogue.  Each wave waits for its stores (vmcnt 0) before the
+    // workgroup's count is issued, so a count implies the partial is in
+    // place; the last split's loads are issued after its count returned.
+    constexpr uint32_t kTile = GW * FN * FM * 1024;  // bytes of one partial tile
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const __amdgpu_buffer_rsrc_t prs = raw_rsrc(a.part + (size_t)tile * S * kTile, S * kTile);
+    const uint32_t mine = (uint32_t)(w * FN * FM) * 1024u + lane * 16u;
+#pragma unroll
+    for (int t = 0; t < FN; ++t)
+#pragma unroll
+      for (int b = 0; b < FM; ++b)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[t][b]), prs,
+                                               z * kTile + mine + (t * FM + b) * 1024, 0, kCoherent);
+    wait_vmcnt<0>();
+    __syncthreads();  // every wave's partial stores are performed
+    uint32_t* const flag = (uint32_t*)lds;
+    if (w == 0 && lane == 0)
+      *flag = __hip_atomic_fetch_add(a.tcount + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const uint32_t arrived = *flag;
+    if (arrived != (uint32_t)S - 1) return;
+    // every split of the tile has counted: leave the counter at zero (the
+    // pre-pass zeroes it too, for a workspace that holds anything)
+    if (w == 0 && lane == 0) __hip_atomic_store(a.tcount + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    Acc sum[FN][FM];
+#pragma unroll
+    for (int t = 0; t < FN; ++t)
+#pragma unroll
+      for (int b = 0; b < FM; ++b) sum[t][b] = Acc{0, 0, 0, 0};
+    for (int zz = 0; zz < S; ++zz) {
+      if (zz == z) {
+#pragma unroll
+        for (int t = 0; t < FN; ++t)
+#pragma unroll
+          for (int b = 0; b < FM; ++b) sum[t][b] += acc[t][b];
+      } else {
+        u32x4 v[FN][FM];
+#pragma unroll
+        for (int t = 0; t < FN; ++t)
+#pragma unroll
+          for (int b = 0; b < FM; ++b)
+            v[t][b] = __builtin_amdgcn_raw_buffer_load_b128(prs, zz * kTile + mine + (t * FM + b) * 1024, 0, kCoherent);
+#pragma unroll
+        for (int t = 0; t < FN; ++t)
+#pragma unroll
+          for (int b = 0; b < FM; ++b) sum[t][b] += __builtin_bit_cast(Acc, v[t][b]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < FN; ++t)
+#pragma unroll
+      for (int b = 0; b < FM; ++b) acc[t][b] = sum[t][b];
+    __syncthreads();  // the flag's LDS word is free again (the staged epilogue below reuses it)
+  }
+
   const bool yvec = a.flags & 2;
   // I8 per-token symmetric (flags bit 4): no zero point, y = fp32(acc) * fp32(s_t[m] * scale[n])
   const bool ptok = I8 && (a.flags & 4);
@@ -664,15 +740,17 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   }
 }
 
-template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false, int KT = 1>
+template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false, int KT = 1, bool SK = false>
 int launch_dl(const GemmArgs& a, hipStream_t st) {
   if constexpr (dl_lds_bytes<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>() > kMaxLdsBytes) {
     return -1;  // no such kernel: its LDS would not fit (the pickers never ask for it)
   } else {
     if (a.Kc % KT) return -1;
-    const dim3 grid((unsigned)((a.Nt + BN / 16 - 1) / (BN / 16)), (unsigned)((a.M + BM - 1) / BM));
-    hipLaunchKernelGGL((gemm_dl_kernel<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>), grid, dim3(KG * WN * WM * 64), 0,
-                       st, a);
+    if (SK != (a.part != nullptr)) return -1;  // split arguments only for the split instances
+    const dim3 grid((unsigned)((a.Nt + BN / 16 - 1) / (BN / 16)), (unsigned)((a.M + BM - 1) / BM),
+                    (unsigned)(SK ? a.splits : 1));
+    hipLaunchKernelGGL((gemm_dl_kernel<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT, SK>), grid, dim3(KG * WN * WM * 64),
+                       0, st, a);
     return check_launch();
   }
 }
@@ -829,8 +907,20 @@ int launch_dl_i8(int id, const GemmArgs& a, hipStream_t st) {
   return launch_dl_id<true, XT_F16>(id, a, st);
 }
 
+// The split-K instances (128 x 64 blocks; the plan's ids 15 and 3).
+int launch_dl_split(bool i8, const GemmArgs& a, hipStream_t st) {
+  if (i8) {
+    return a.Kc % 2 == 0 ? launch_dl<true, XT_F16, 128, 64, 2, 2, 2, 1, false, 2, true>(a, st)
+                         : launch_dl<true, XT_F16, 128, 64, 2, 2, 2, 1, false, 1, true>(a, st);
+  }
+  if (!a.rsum) return -1;  // fp16 W-only splits need the precomputed row sums
+  return launch_dl<false, XT_F16, 128, 64, 2, 2, 2, 1, true, 1, true>(a, st);
+}
+
 // Launch of direct-to-LDS configuration `id` (tuning entry; -1: no such id).
+// Arguments with a split-K area (a.part) run the split instances.
 int launch_gemm_dl_cfg(int id, bool i8, int xt, const GemmArgs& a, hipStream_t st) {
+  if (a.part) return (id == 15 || id == 3) && (i8 || xt == XT_F16) ? launch_dl_split(i8, a, st) : -1;
   if (i8) return launch_dl_i8(id, a, st);
   // 192 x 64 blocks with K split over 4 wave groups leave no LDS for the
   // in-loop row sums: without precomputed sums the 128 x 64 split runs
@@ -876,6 +966,49 @@ int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt) {
   return 8;
 }
 
+// Split-K plan.  Grids of fewer than 192 blocks of 128 x 64 leave CUs idle
+// (the 128-token W8A8 GEMM at N = 4096 ran 128 workgroups on 256 CUs and read
+// every weight tile twice): those shapes run 128 x 64 blocks with K split over
+// 4 workgroups (2 when K holds fewer than 32 stage steps), each keeping at
+// least 8 stage steps.  Measured on MI355X at N = 4096..12288, K = 4096
+// (whole calls, pre-passes included): 4 splits beat 2 and 8, and save 2.0 to
+// 2.7 us at M <= 64 and 0.6 to 1.3 us at M = 128; at M = 200 and 256 the
+// fixup costs more than the idle CUs did (W-only +1 us), so only M <= 128
+// splits.  Only for operands that need no in-loop row sums: W8A8, and fp16
+// W-only with precomputed row sums (the staged fp32 / bf16 activations
+// included).
+DlPlan plan_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc, bool rsp) {
+  DlPlan p{pick_gemm_dl(i8, xt, M, Nt), 1, 0, 0};
+  if (!i8 && !(xt == XT_F16 && rsp)) return p;
+  const int64_t tiles = ((Nt + 7) / 8) * ((M + 63) / 64);
+  if (tiles >= 192 || M > 128) return p;
+  const int64_t steps = i8 && Kc % 2 == 0 ? Kc / 2 : Kc;  // stage steps of the 128 x 64 configuration
+  const int S = steps >= 32 ? 4 : (steps >= 16 ? 2 : 1);
+  if (S == 1) return p;
+  p.id = i8 ? 15 : 3;
+  p.splits = S;
+  p.tiles = tiles;
+  p.part_bytes = tiles * S * 128 * 64 * 4;  // one fp32 / int32 partial tile per split
+  return p;
+}
+
+// Bytes of the split-K area (tile counters, then partial tiles) of a plan.
+int64_t split_area_bytes(const DlPlan& p) {
+  return p.splits > 1 ? ((p.tiles * 4 + 255) & ~(int64_t)255) + p.part_bytes : 0;
+}
+
+// Attach the split-K area to the GEMM arguments when the caller's scratch
+// holds it; returns the counters the pre-pass must zero (null: no split).
+static uint32_t* attach_split(GemmArgs& a, const DlPlan& p, uint8_t* area, int64_t area_bytes, int* ncount) {
+  *ncount = 0;
+  if (p.splits <= 1 || !area || area_bytes < split_area_bytes(p)) return nullptr;
+  a.tcount = (uint32_t*)area;
+  a.part = area + ((p.tiles * 4 + 255) & ~(int64_t)255);
+  a.splits = p.splits;
+  *ncount = (int)p.tiles;
+  return a.tcount;
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
@@ -913,27 +1046,31 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
     a.x = x; a.ldx = ldx; a.M = (int)M; a.Kc = (int)Kc;
     a.packed = packed; a.scale = scale; a.bias = bias;
     a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.flags = flags;
-    int gxt = xt;
+    const int gxt = staged ? XT_F16 : xt;  // fp32 / bf16 activations are staged as fp16 planes
+    // split K when the grid is small and the scratch after the layout holds the partials
+    const DlPlan plan = plan_gemm_dl(false, gxt, M, Nt, Kc, staged);
+    int ncount = 0;
+    uint32_t* zero = staged ? attach_split(a, plan, (uint8_t*)ws + l.bytes, ws_bytes - l.bytes, &ncount) : nullptr;
+    const int id = zero || plan.splits == 1 ? plan.id : pick_gemm_dl(false, gxt, M, Nt);
     if (staged) {
       uint8_t* w = (uint8_t*)ws;
       float* rowsum = (float*)(w + l.rowsum);
       a.rsum = rowsum;
       if (xt == XT_F16) {
-        const int rc = launch_rowsum_f16(x, ldx, M, K, rowsum, st);
+        const int rc = launch_rowsum_f16(x, ldx, M, K, rowsum, st, zero, ncount);
         if (rc) return rc;
       } else {
         // fp32 / bf16: scaled fp16 planes [hi | lo] per row, then the fp16 GEMM
         const int np = xt == XT_F32 ? 2 : 1;
         _Float16* planes = (_Float16*)(w + l.planes);
         float* rscale = (float*)(w + l.rscale);
-        const int rc = launch_stage_act(x, xt, ldx, M, K, planes, rowsum, rscale, st);
+        const int rc = launch_stage_act(x, xt, ldx, M, K, planes, rowsum, rscale, st, zero, ncount);
         if (rc) return rc;
         a.x = planes; a.ldx = np * K; a.kx = (int)(np * Kc); a.rscale = rscale;
         a.flags = flags | 1;
-        gxt = XT_F16;
       }
     }
-    return launch_gemm_dl_cfg(pick_gemm_dl(false, gxt, M, Nt), false, gxt, a, st);
+    return launch_gemm_dl_cfg(id, false, gxt, a, st);
   }
   dim3 grid((unsigned)((Nt + kBN / 16 - 1) / (kBN / 16)), (unsigned)((M + kBM - 1) / kBM)), block(kWN * kWM * 64);
   switch (xt) {
@@ -948,11 +1085,16 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
 int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                      const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
                      int64_t ldy, int32_t* acc_out, float2* partials, int8_t* xq, float* qpbuf, hipStream_t st,
-                     bool yvec) {
+                     bool yvec, uint8_t* split, int64_t split_bytes) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64, Kp = Kc * 64;
   if (Kp > ((int64_t)1 << 21)) return -1;  // 32-bit block offsets of the direct-to-LDS GEMM
+  GemmArgs a{};
+  const DlPlan plan = plan_gemm_dl(true, XT_F16, M, Nt, Kc, true);
+  int ncount = 0;
+  uint32_t* zero = attach_split(a, plan, split, split_bytes, &ncount);
+  const int id = zero || plan.splits == 1 ? plan.id : pick_gemm_dl(true, XT_F16, M, Nt);
   const int nparts = minmax_nparts(M, K);
-  const int prc = launch_minmax_partials(x, xt, M, K, ldx, partials, nparts, st);
+  const int prc = launch_minmax_partials(x, xt, M, K, ldx, partials, nparts, st, zero, ncount);
   if (prc) return prc;
   const int flags = (xvec ? 1 : 0) | (yvec ? 2 : 0) | y16_flag(y, yt, ldy);
   const int64_t chunks = M * (Kp / 16);
@@ -985,12 +1127,11 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
 #undef SBQ_QUANT_LAUNCH1
   int rc = check_launch();
   if (rc) return rc;
-  GemmArgs a{};
   a.x = xq; a.ldx = Kp; a.M = (int)M; a.Kc = (int)Kc;
   a.packed = packed; a.scale = scale; a.bias = bias; a.colsum = colsum;
   a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.acc_out = acc_out; a.qpbuf = qpbuf;
   a.flags = flags;
-  return launch_gemm_dl_cfg(pick_gemm_dl(true, XT_F16, M, Nt), true, XT_F16, a, st);
+  return launch_gemm_dl_cfg(id, true, XT_F16, a, st);
 }
 
 // Per-token symmetric W8A8: xq [M, Kp] s8 and s_t [M] from the row quantizer,

@@ -19,8 +19,10 @@ int launch_repack(const int8_t* q, int64_t N, int64_t K, int64_t ldq, uint8_t* p
 int launch_unpack(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_t ldq, hipStream_t st);
 
 int minmax_nparts(int64_t M, int64_t K);
+// zero / nzero (optional): counters the pre-pass zeroes for the split-K GEMM
+// launched after it on the same stream.
 int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, float2* partials,
-                           int nparts, hipStream_t st);
+                           int nparts, hipStream_t st, uint32_t* zero = nullptr, int nzero = 0);
 int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t* zp_out, hipStream_t st);
 int launch_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* out, hipStream_t st);
 
@@ -56,6 +58,19 @@ int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
 int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                    const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, void* ws,
                    int64_t ws_bytes, hipStream_t st, bool yvec);
+// split: scratch after the workspace's layout (split_area_bytes of the plan;
+// a shorter or null one runs the shape without splitting K).
+// Direct-to-LDS GEMM plan: block configuration id and K splits (1: none);
+// with splits, `tiles` output blocks of 128 x 64 and their partial tiles.
+struct DlPlan {
+  int id, splits;
+  int64_t tiles, part_bytes;
+};
+DlPlan plan_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc, bool rsp);
+// Bytes of a plan's split-K scratch (0 without splits): tile counters, then
+// the partial tiles; the GEMM launchers take it after their other scratch.
+int64_t split_area_bytes(const DlPlan& p);
+
 // W-only prefill scratch: [rowsum: M floats][rscale: M floats][fp16 planes: M x NP x K],
 // each part 256-byte aligned; NP = 2 for fp32 x, 1 for bf16, 0 for fp16.
 struct W8Ws {
@@ -70,10 +85,11 @@ int launch_gemm_w8a8_token(const void* x, int xt, int64_t M, int64_t K, int64_t 
 int launch_quantize_rows_sym(const void* x, int xt, int64_t ldx, bool xvec, int64_t M, int64_t K, int64_t Kp,
                              int8_t* xq, float* s_out, hipStream_t st);
 // Per-row sums in fp32 of fp16 x [M, K] (K % 8 == 0, 16-byte aligned rows).
-int launch_rowsum_f16(const void* x, int64_t ldx, int64_t M, int64_t K, float* out, hipStream_t st);
+int launch_rowsum_f16(const void* x, int64_t ldx, int64_t M, int64_t K, float* out, hipStream_t st,
+                      uint32_t* zero = nullptr, int nzero = 0);
 // fp32 / bf16 x [M, K] -> scaled fp16 planes, row sums and row scales.
 int launch_stage_act(const void* x, int xt, int64_t ldx, int64_t M, int64_t K, _Float16* xs, float* rowsum,
-                     float* rscale, hipStream_t st);
+                     float* rscale, hipStream_t st, uint32_t* zero = nullptr, int nzero = 0);
 
 // W8A8 (fbgemm dynamic semantics).  Both launch the activation min/max
 // pre-pass into `partials` (>= kMinMaxPartials float2) when they need it (the
@@ -87,6 +103,6 @@ int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
 int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                      const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
                      int64_t ldy, int32_t* acc_out, float2* partials, int8_t* xq, float* qpbuf, hipStream_t st,
-                     bool yvec);
+                     bool yvec, uint8_t* split = nullptr, int64_t split_bytes = 0);
 
 }  // namespace sbq

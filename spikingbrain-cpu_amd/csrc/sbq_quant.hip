@@ -86,10 +86,19 @@ __global__ __launch_bounds__(256) void colsum_kernel(const int8_t* __restrict__ 
 
 // Per-block (min, max) of x [M, K]; block b covers flat rows/columns
 // b, b + gridDim.x, ... in 256-element strides.
+// Zero the split-K tile counters of the GEMM that follows a pre-pass (the
+// pre-pass runs first on the same stream, so the GEMM sees them zeroed).
+__device__ __forceinline__ void zero_counters(uint32_t* c, int n) {
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < n; i += blockDim.x) c[i] = 0u;
+}
+
 template <int XT>
 __global__ __launch_bounds__(1024) void minmax_partial_kernel(const void* __restrict__ xv, int M, int K, int64_t ldx,
-                                                              float2* __restrict__ partials, int vec) {
+                                                              float2* __restrict__ partials, int vec,
+                                                              uint32_t* __restrict__ zero, int nzero) {
   typedef typename XElem<XT>::T T;
+  zero_counters(zero, nzero);
   // 8-element chunks, row by row; block b covers chunks b, b + nparts, ...
   const int cpr = (K + 7) / 8;
   const int64_t nch = (int64_t)M * cpr;
@@ -184,7 +193,9 @@ __device__ __forceinline__ void rowsum_acc(u32x4 v, float& s0, float& s1) {
 }
 
 __global__ __launch_bounds__(256) void rowsum_f16_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, int K,
-                                                         float* __restrict__ out) {
+                                                         float* __restrict__ out, uint32_t* __restrict__ zero,
+                                                         int nzero) {
+  zero_counters(zero, nzero);
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= M) return;
   const _Float16* p = x + (int64_t)row * ldx;
@@ -251,7 +262,9 @@ __global__ __launch_bounds__(256) void quantize_rows_sym_kernel(const void* __re
 template <int XT, int NP>
 __global__ __launch_bounds__(256) void stage_act_kernel(const void* __restrict__ xv, int64_t ldx, int M, int K,
                                                         _Float16* __restrict__ xs, float* __restrict__ rowsum,
-                                                        float* __restrict__ rscale) {
+                                                        float* __restrict__ rscale, uint32_t* __restrict__ zero,
+                                                        int nzero) {
+  zero_counters(zero, nzero);
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= M) return;
   float mx = 0.0f;
@@ -397,7 +410,7 @@ int minmax_nparts(int64_t M, int64_t K) {
 }
 
 int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, float2* partials,
-                           int nparts, hipStream_t st) {
+                           int nparts, hipStream_t st, uint32_t* zero, int nzero) {
   const int esz = xt == XT_F32 ? 4 : 2;
   const int vec = ((uintptr_t)x % 16 == 0) && ((ldx * esz) % 16 == 0);
   // smaller workgroups for small x (measured at K = 4096: M = 128 3.4 -> 2.8 us,
@@ -406,9 +419,9 @@ int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t 
   const int threads = total <= ((int64_t)1 << 19) ? 256 : (total <= ((int64_t)1 << 21) ? 512 : 1024);
   dim3 grid((unsigned)nparts), block(threads);
   switch (xt) {
-    case XT_F32: hipLaunchKernelGGL(minmax_partial_kernel<XT_F32>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec); break;
-    case XT_F16: hipLaunchKernelGGL(minmax_partial_kernel<XT_F16>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec); break;
-    case XT_BF16: hipLaunchKernelGGL(minmax_partial_kernel<XT_BF16>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec); break;
+    case XT_F32: hipLaunchKernelGGL(minmax_partial_kernel<XT_F32>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec, zero, nzero); break;
+    case XT_F16: hipLaunchKernelGGL(minmax_partial_kernel<XT_F16>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec, zero, nzero); break;
+    case XT_BF16: hipLaunchKernelGGL(minmax_partial_kernel<XT_BF16>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec, zero, nzero); break;
     default: return -2;
   }
   return check_launch();
@@ -419,19 +432,22 @@ int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t
   return check_launch();
 }
 
-int launch_rowsum_f16(const void* x, int64_t ldx, int64_t M, int64_t K, float* out, hipStream_t st) {
+int launch_rowsum_f16(const void* x, int64_t ldx, int64_t M, int64_t K, float* out, hipStream_t st, uint32_t* zero,
+                      int nzero) {
   hipLaunchKernelGGL(rowsum_f16_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, (const _Float16*)x, ldx, (int)M,
-                     (int)K, out);
+                     (int)K, out, zero, nzero);
   return check_launch();
 }
 
 int launch_stage_act(const void* x, int xt, int64_t ldx, int64_t M, int64_t K, _Float16* xs, float* rowsum,
-                     float* rscale, hipStream_t st) {
+                     float* rscale, hipStream_t st, uint32_t* zero, int nzero) {
   const dim3 grid((unsigned)((M + 3) / 4)), block(256);
   if (xt == XT_F32)
-    hipLaunchKernelGGL((stage_act_kernel<XT_F32, 2>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale);
+    hipLaunchKernelGGL((stage_act_kernel<XT_F32, 2>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale,
+                       zero, nzero);
   else if (xt == XT_BF16)
-    hipLaunchKernelGGL((stage_act_kernel<XT_BF16, 1>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale);
+    hipLaunchKernelGGL((stage_act_kernel<XT_BF16, 1>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale,
+                       zero, nzero);
   else
     return -2;
   return check_launch();

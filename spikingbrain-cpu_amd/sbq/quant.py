@@ -171,9 +171,13 @@ def unpack(packed: torch.Tensor, N: int, K: int) -> torch.Tensor:
     return q
 
 
-def w8_workspace(M: int, K: int, device: torch.device, dtype: torch.dtype = torch.float16) -> torch.Tensor:
-    """Scratch for linear_w8's prefill path with [M, K] activations of `dtype`."""
-    n = _lib.load().sbq_w8_workspace_bytes(M, K, _code(dtype))
+def w8_workspace(M: int, K: int, device: torch.device, dtype: torch.dtype = torch.float16,
+                 N: int | None = None) -> torch.Tensor:
+    """Scratch for linear_w8's prefill path with [M, K] activations of `dtype`;
+    with N, also the split-K partials of shapes that need them."""
+    L = _lib.load()
+    n = L.sbq_w8_workspace_bytes(M, K, _code(dtype)) if N is None else L.sbq_linear_workspace_bytes(
+        M, N, K, _code(dtype), 0)
     return torch.empty((n,), dtype=torch.uint8, device=device)
 
 
@@ -190,7 +194,7 @@ def linear_w8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias:
     y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x2.device)
     ws = workspace
     if ws is None and M > 16:  # decode sizes run the GEMV, which needs none
-        ws = w8_workspace(M, K, x2.device, x2.dtype)
+        ws = w8_workspace(M, K, x2.device, x2.dtype, N)
     _check_operands("linear_w8", x2, packed, N, y, (("scale", scale, torch.float32), ("bias", bias, torch.float32)),
                     ws)
     with torch.cuda.device(x2.device):
@@ -201,8 +205,12 @@ def linear_w8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias:
     return y
 
 
-def w8a8_workspace(M: int, K: int, device: torch.device) -> torch.Tensor:
-    n = _lib.load().sbq_w8a8_workspace_bytes(M, K)
+def w8a8_workspace(M: int, K: int, device: torch.device, N: int | None = None,
+                   dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """Scratch for the int8-dyn paths; with N, also the split-K partials of
+    prefill shapes that need them."""
+    L = _lib.load()
+    n = L.sbq_w8a8_workspace_bytes(M, K) if N is None else L.sbq_linear_workspace_bytes(M, N, K, _code(dtype), 1)
     return torch.empty((n,), dtype=torch.uint8, device=device)
 
 
@@ -214,7 +222,7 @@ def linear_w8a8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, col
     x2 = _as_activation(x2)
     M, K = x2.shape
     y = out if out is not None else torch.empty((M, N), dtype=out_dtype, device=x2.device)
-    ws = workspace if workspace is not None else w8a8_workspace(M, K, x2.device)
+    ws = workspace if workspace is not None else w8a8_workspace(M, K, x2.device, N, x2.dtype)
     if acc_out is not None and (acc_out.dtype != torch.int32 or tuple(acc_out.shape) != (M, N)
                                 or not acc_out.is_contiguous() or acc_out.device != x2.device):
         raise ValueError("acc_out must be a contiguous int32 [M, N] tensor on the input's device")
@@ -331,7 +339,7 @@ def linear_w8_argmax(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor
         raise ValueError("linear_w8_argmax: the logits are fp32")
     ws = workspace
     if ws is None and M > 16:
-        ws = w8_workspace(M, K, x2.device, x2.dtype)
+        ws = w8_workspace(M, K, x2.device, x2.dtype, N)
     _check_operands("linear_w8_argmax", x2, packed, N, y, (("scale", scale, torch.float32),
                                                            ("bias", bias, torch.float32)), ws)
     idx = _check_argmax("linear_w8_argmax", x2, state, idx)
@@ -353,7 +361,7 @@ def linear_w8a8_argmax(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tens
     y = out if out is not None else torch.empty((M, N), dtype=torch.float32, device=x2.device)
     if y.dtype != torch.float32:
         raise ValueError("linear_w8a8_argmax: the logits are fp32")
-    ws = workspace if workspace is not None else w8a8_workspace(M, K, x2.device)
+    ws = workspace if workspace is not None else w8a8_workspace(M, K, x2.device, N, x2.dtype)
     _check_operands("linear_w8a8_argmax", x2, packed, N, y, (("scale", scale, torch.float32),
                                                              ("bias", bias, torch.float32),
                                                              ("colsum", colsum, torch.int32)), ws)

@@ -492,3 +492,119 @@ def test_device_resident_decode(dev, fmt):
         top2 = torch.topk(ld, 2).values
         if float(top2[0] - top2[1]) > 1e-2 * float(top2[0].abs()):
             assert int(cpu.tok.item()) == eager_tok[i], i
+
+
+# ---------------------------------------------------------------------------
+# prefill GEMM with K split over workgroups (grids that would leave CUs idle)
+# ---------------------------------------------------------------------------
+SPLIT_CASES = [  # (M, N, K): 128 x 64 blocks, K split 2 or 4 ways (M <= 128 only)
+    (33, 1000, 2048), (64, 4096, 4096), (100, 2048, 4096), (128, 4096, 4096), (120, 1024, 2560),
+    (128, 6144, 4096), (128, 4096, 4160), (48, 256, 12288),
+]
+
+
+def _split_bytes(M, N, K, xd, w8a8):
+    from sbq import _lib
+
+    L = _lib.load()
+    code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[xd]
+    base = L.sbq_w8a8_workspace_bytes(M, K) if w8a8 else L.sbq_w8_workspace_bytes(M, K, code)
+    return L.sbq_linear_workspace_bytes(M, N, K, code, 1 if w8a8 else 0), base
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", SPLIT_CASES)
+def test_w8a8_split_k_bitexact(dev, M, N, K):
+    """int8-dyn with K split over workgroups: int32 accumulators and outputs
+    bit-exact against the oracle and equal to the unsplit GEMM (the workspace
+    without the split area); repeated calls give the same bits."""
+    announce(f"w8a8 split-K M={M} N={N} K={K}")
+    full, base = _split_bytes(M, N, K, torch.float16, True)
+    assert full > base  # the shape splits
+    w = gpu_weight(N, K, 81, dev)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(82)).to(dev)
+    lin = quant.DynamicInt8Linear(w, b)
+    cols = tile_sample(N, 83)
+    q, s = ref_rows(w, cols)
+    for xd in (torch.float16, torch.float32):
+        x = cpu_x(M, K, 84, outliers=True).to(xd)
+        xg = x.to(dev)
+        outs = []
+        for ws in (torch.empty(full, dtype=torch.uint8, device=dev), torch.empty(base, dtype=torch.uint8, device=dev)):
+            for _ in range(2):
+                acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+                y = quant.linear_w8a8(xg, lin.packed, lin.scale, lin.colsum, lin.bias, N, acc_out=acc, workspace=ws)
+                outs.append((acc.cpu().numpy(), y.cpu().numpy()))
+        for o in outs[1:]:
+            np.testing.assert_array_equal(o[0], outs[0][0])
+            np.testing.assert_array_equal(o[1], outs[0][1])
+        acc_ref, y_ref = ref_w8a8(x.float().numpy(), np.arange(M), q, s, b.cpu().numpy()[cols])
+        np.testing.assert_array_equal(outs[0][0][:, cols], acc_ref)
+        np.testing.assert_array_equal(outs[0][1][:, cols], y_ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", SPLIT_CASES[:6])
+def test_w8_split_k_matches_oracle(dev, M, N, K):
+    """Weight-only with K split over workgroups (fp16 x, and fp32 / bf16 x
+    staged as fp16 planes): within the tolerance of the oracle, equal across
+    repeated calls (the partials are added in split order), and within fp32
+    summation order of the unsplit GEMM."""
+    announce(f"w8 split-K M={M} N={N} K={K}")
+    w = gpu_weight(N, K, 85, dev)
+    lin = quant.Int8Linear(w, None)
+    cols = tile_sample(N, 86)
+    q, s = ref_rows(w, cols)
+    for xd in (torch.float16, torch.bfloat16, torch.float32):
+        full, base = _split_bytes(M, N, K, xd, False)
+        assert full > base
+        x = cpu_x(M, K, 87).to(xd)
+        xg = x.to(dev)
+        ys = []
+        for ws in (torch.empty(full, dtype=torch.uint8, device=dev), torch.empty(full, dtype=torch.uint8, device=dev),
+                   torch.empty(base, dtype=torch.uint8, device=dev)):
+            ys.append(quant.linear_w8(xg, lin.packed, lin.scale, None, N, workspace=ws).cpu().numpy())
+        np.testing.assert_array_equal(ys[0], ys[1])
+        assert oracle.rel_l2(ys[0], ys[2]) <= 2e-6
+        ref = oracle.int8_linear(x.float().numpy(), q, s)
+        tol = W8_TOL if xd == torch.float32 else W8_TOL_EXACT_X
+        assert oracle.rel_l2(ys[0][:, cols], ref) <= tol, str(xd)
+
+
+@pytest.mark.gpu
+def test_split_k_graph_replays(dev):
+    """Split-K GEMMs captured in a HIP graph: every replay (new activations,
+    eager work between) equals the eager call; the counters are zeroed by the
+    pre-pass inside each replay."""
+    announce("split-K graph replays")
+    M, N, K = 128, 4096, 4096
+    w = gpu_weight(N, K, 88, dev)
+    dyn = quant.DynamicInt8Linear(w, None)
+    lin = quant.Int8Linear(w, None)
+    x = cpu_x(M, K, 89).half().to(dev)
+    ws8a8 = quant.w8a8_workspace(M, K, dev, N)
+    ws8 = quant.w8_workspace(M, K, dev, torch.float16, N)
+    y1 = torch.empty((M, N), device=dev)
+    y2 = torch.empty((M, N), device=dev)
+
+    def run():
+        quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N, workspace=ws8a8, out=y1)
+        quant.linear_w8(x, lin.packed, lin.scale, None, N, workspace=ws8, out=y2)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    for i in range(4):
+        x.copy_(cpu_x(M, K, 90 + i).half().to(dev))
+        g.replay()
+        torch.cuda.synchronize()
+        e1 = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N, workspace=quant.w8a8_workspace(M, K, dev, N))
+        e2 = quant.linear_w8(x, lin.packed, lin.scale, None, N, workspace=quant.w8_workspace(M, K, dev, torch.float16, N))
+        np.testing.assert_array_equal(y1.cpu().numpy(), e1.cpu().numpy())
+        np.testing.assert_array_equal(y2.cpu().numpy(), e2.cpu().numpy())
