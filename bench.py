@@ -478,7 +478,7 @@ def prefill_probe(ctx, M=2048, N=12288, K=4096, launches=100):
     packed, s, _ = ctx.weights(N, K, 900)
     x = ctx.act(M, K, 901)
     y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
-    ws = quant.w8_workspace(M, K, ctx.dev, x.dtype)
+    ws = quant.w8_workspace(M, K, ctx.dev, x.dtype, N)
     torch.cuda.synchronize()
     for _ in range(launches):
         quant.linear_w8(x, packed, s, None, N, out=y, workspace=ws)
@@ -494,7 +494,7 @@ def w8a8_probe(ctx, M=2048, N=12288, K=4096, launches=100):
     packed, s, cs = ctx.weights(N, K, 950, colsum=True)
     x = ctx.act(M, K, 951, outliers=True)
     y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
-    ws = quant.w8a8_workspace(M, K, ctx.dev)
+    ws = quant.w8a8_workspace(M, K, ctx.dev, N)
     torch.cuda.synchronize()
     for _ in range(launches):
         quant.linear_w8a8(x, packed, s, cs, None, N, torch.float16, workspace=ws, out=y)
@@ -680,10 +680,10 @@ def main():
     ap.add_argument("--summarize-trace", metavar="DIR", help="print a markdown summary of a rocprofv3 kernel trace")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the traffic JSON from FETCH_SIZE and WRITE_SIZE passes over --traffic-probe")
-    ap.add_argument("--prefill-probe", action="store_true",
-                    help="only run the M=2048 prefill GEMM (workload of the prefill counter passes)")
-    ap.add_argument("--w8a8-probe", action="store_true",
-                    help="only run the M=2048 int8-dyn prefill (workload of the W8A8 counter passes)")
+    ap.add_argument("--prefill-probe", nargs="*", type=int, metavar="M N K",
+                    help="only run the weight-only GEMM, M=2048 N=12288 K=4096 unless given (counter passes)")
+    ap.add_argument("--w8a8-probe", nargs="*", type=int, metavar="M N K",
+                    help="only run the int8-dyn linear, M=2048 N=12288 K=4096 unless given (counter passes)")
     ap.add_argument("--only", metavar="NAME", help="run one extra measurement and print it (e.g. lm_head_greedy)")
     ap.add_argument("--gemv-probe", nargs=3, type=int, metavar=("M", "N", "K"),
                     help="only run back-to-back decode GEMV launches in a graph (workload of the gap trace)")
@@ -719,11 +719,11 @@ def main():
     if args.traffic_probe:
         traffic_probe(ctx)
         return
-    if args.prefill_probe:
-        prefill_probe(ctx)
+    if args.prefill_probe is not None:
+        prefill_probe(ctx, *(args.prefill_probe or (2048, 12288, 4096)))
         return
-    if args.w8a8_probe:
-        w8a8_probe(ctx)
+    if args.w8a8_probe is not None:
+        w8a8_probe(ctx, *(args.w8a8_probe or (2048, 12288, 4096)))
         return
     if args.gemv_probe:
         M, N, K = args.gemv_probe

@@ -165,13 +165,25 @@ __device__ __forceinline__ int row_scale_exp(float mx) {
 // ---------------------------------------------------------------------------
 // Output element store
 // ---------------------------------------------------------------------------
+// fp32 -> 2-byte conversion of a computed output.  The empty asm hides how the
+// value was produced, so the compiler cannot fuse the final fma / add with the
+// conversion into one mixed-precision instruction (v_fma_mixlo_f16) that
+// rounds the exact result once to 16 bits: a 2-byte output is the fp32 result
+// rounded again, as converting the reference's fp32 output is.
+__device__ __forceinline__ float fp32_rounded(float v) {
+  asm("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ _Float16 out_f16(float v) { return (_Float16)fp32_rounded(v); }
+__device__ __forceinline__ __bf16 out_bf16(float v) { return (__bf16)fp32_rounded(v); }
+
 __device__ __forceinline__ void store_y(void* y, int ytype, int64_t idx, float v) {
   if (ytype == XT_F32) {
     ((float*)y)[idx] = v;
   } else if (ytype == XT_F16) {
-    ((_Float16*)y)[idx] = (_Float16)v;
+    ((_Float16*)y)[idx] = out_f16(v);
   } else {
-    ((__bf16*)y)[idx] = (__bf16)v;
+    ((__bf16*)y)[idx] = out_bf16(v);
   }
 }
 
@@ -191,11 +203,11 @@ __device__ __forceinline__ void store_y4(void* y, int ytype, int64_t idx, f32x4 
       *(f32x4*)((float*)y + idx) = v;
     } else if (ytype == XT_F16) {
       typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-      h4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+      h4 h = {out_f16(v.x), out_f16(v.y), out_f16(v.z), out_f16(v.w)};
       *(h4*)((_Float16*)y + idx) = h;
     } else {
       typedef __bf16 b4 __attribute__((ext_vector_type(4)));
-      b4 h = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+      b4 h = {out_bf16(v.x), out_bf16(v.y), out_bf16(v.z), out_bf16(v.w)};
       *(b4*)((__bf16*)y + idx) = h;
     }
   } else {

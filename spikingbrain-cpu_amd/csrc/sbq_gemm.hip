@@ -343,17 +343,26 @@ struct GemmArgs {
 template <int BN, int BM, int WN, int WM>
 constexpr int dl_min_waves() { return (BN / WN) * (BM / WM) > 64 * 64 ? 2 : 4; }
 
+// Bytes of the epilogue operand table: per block column its scale, bias and
+// (W8A8) column sum, per block row its row sum and row scale, and the two
+// activation quantization words.
+constexpr int dl_epi_table_bytes(int BN, int BM) { return ((3 * BN + 2 * BM + 2) * 4 + 15) & ~15; }
+
 // LDS bytes of one workgroup: the stage rings (or, after the K loop, the
 // cross-group reduction buffer / the staged output tile), plus the in-loop row
-// sums of fp16 W-only blocks without precomputed sums.
+// sums of fp16 W-only blocks without precomputed sums, plus the epilogue
+// operand table where the stage bytes left free after the K loop cannot hold it.
 template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP, int KT>
 constexpr int dl_lds_bytes() {
   const int stage = KT * ((BN / 16) * 1024 + BM * (I8 ? 64 : 128));
   const int red = (KG - 1) * WN * WM * (BN / WN / 16) * (BM / WM / 16) * 1024;
   const int ldsb = KG * NS * stage > red ? KG * NS * stage : red;
   const int epi = KG == 1 ? BM * (BN * 2 + 32) : 0;
+  const int ldsa = epi > ldsb ? epi : ldsb;
   const bool rsk = !I8 && XT == XT_F16 && !RSP;
-  return (epi > ldsb ? epi : ldsb) + (rsk ? KG * BM * 4 : 0);
+  const int post = KG == 1 ? epi : red;  // bytes from offset 0 in use after the K loop
+  const int epb = dl_epi_table_bytes(BN, BM);
+  return ldsa + (rsk ? KG * BM * 4 : 0) + (post + epb <= ldsa ? 0 : epb);
 }
 constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950: LDS per workgroup
 
@@ -397,11 +406,22 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   constexpr bool LEPI = KG == 1;
   constexpr int ERS = BN * 2 + 32;  // bytes per padded row of the LDS output tile
   constexpr int LDSA = (LEPI && BM * ERS > LDSB) ? BM * ERS : LDSB;
+  // Epilogue operand table (EPB bytes at EPO): the stage bytes beyond the
+  // output tile / reduction buffer when they are free after the K loop, else
+  // appended after the in-loop row sums.
+  constexpr int EPB = dl_epi_table_bytes(BN, BM);
+  constexpr int POST = LEPI ? BM * ERS : RED;
+  constexpr bool EPIN = POST + EPB <= LDSA;
+  constexpr int EPO = EPIN ? LDSA - EPB : LDSA + (RSK ? KG * BM * 4 : 0);
   // one LDS object: with a second one the compiler waits for every stage DMA in
   // flight before any LDS read of the main loop (it cannot tell them apart)
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDSA + (RSK ? KG * BM * 4 : 0)];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDSA + (RSK ? KG * BM * 4 : 0) + (EPIN ? 0 : EPB)];
   static_assert(sizeof(lds) == dl_lds_bytes<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>(), "launcher's LDS model");
   float* const rsum_lds = (float*)(lds + LDSA);
+  // table: scale [BN], bias [BN], column sums [BN] (int), row sums [BM], row
+  // scales [BM], the two activation quantization words
+  float* const ept = (float*)(lds + EPO);
+  constexpr int EP_BI = BN, EP_CS = 2 * BN, EP_RS = 3 * BN, EP_RF = 3 * BN + BM, EP_QP = 3 * BN + 2 * BM;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r = lane & 15, g = lane >> 4;
@@ -482,6 +502,32 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
 #pragma unroll
   for (int j = 0; j < RF; ++j) rs[j] = 0.0f;
 
+  // Epilogue operands, loaded before the first stage so that their latency
+  // hides behind the K loop (loaded at its end they cost a full memory round
+  // trip per block: 2-3.5 us of a 13 us small-M launch): thread t holds block
+  // column min(t, BN-1) and block row min(t, BM-1), indexes clamped so every
+  // load is unconditional.  They are the oldest loads in flight, so the first
+  // stage wait covers them.
+  constexpr int NTH = KG * GW * 64;
+  static_assert(NTH >= BN && NTH >= BM, "one thread per block column and row");
+  const bool ptok = I8 && (a.flags & 4);  // I8 per-token symmetric (flags bit 4)
+  const int ecol = min(nt0 * 16 + min(tid, BN - 1), a.N - 1);
+  const int erow = min(m0 + min(tid, BM - 1), M - 1);
+  const float e_sc = a.scale[ecol];
+  const float e_bi = a.bias ? a.bias[ecol] : -0.0f;  // -0: adding it changes no value
+  int e_cs = 0;
+  float e_q = 0.0f;
+  if constexpr (I8) {
+    if (!ptok) {
+      e_cs = a.colsum[ecol];
+      e_q = a.qpbuf[tid & 1];
+    }
+  }
+  float e_rs = 0.0f, e_rf = 1.0f;
+  if constexpr (OFS && !RSK) e_rs = a.rsum[erow];
+  if constexpr (RSP || I8)
+    if (a.rscale) e_rf = a.rscale[erow];
+
 #pragma unroll
   for (int i = 0; i < NS - 1; ++i)
     if (i < KW) issue(i, i);
@@ -542,6 +588,21 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
     // issue after the next step's barrier, which every wave reaches after its
     // reads of this stage have returned (their MFMAs consumed them).
   }
+
+  // Every wave is past its last stage (its final wait was vmcnt(0)) and its
+  // LDS reads have returned: the epilogue operands move into their table.
+  __syncthreads();
+  if (tid < BN) {
+    ept[tid] = e_sc;
+    ept[EP_BI + tid] = e_bi;
+    ((int*)ept)[EP_CS + tid] = e_cs;
+  }
+  if (tid < BM) {
+    ept[EP_RS + tid] = e_rs;
+    ept[EP_RF + tid] = e_rf;
+  }
+  if (tid < 2) ept[EP_QP + tid] = e_q;
+  __syncthreads();
 
   if constexpr (RSK) {
     // sum the 4 K-column groups of each row, then publish the block's row sums
@@ -632,8 +693,7 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   }
 
   const bool yvec = a.flags & 2;
-  // I8 per-token symmetric (flags bit 4): no zero point, y = fp32(acc) * fp32(s_t[m] * scale[n])
-  const bool ptok = I8 && (a.flags & 4);
+  // I8 per-token symmetric (ptok): no zero point, y = fp32(acc) * fp32(s_t[m] * scale[n])
   // every wave is past the K loop and no stage DMA is in flight (the last wait
   // was vmcnt(0)): the stage buffers become the output tile
   const bool lepi = LEPI && a.yt != XT_F32;
@@ -642,72 +702,114 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) 
   int corr = 0;
   if constexpr (I8) {
     if (!ptok) {
-      sx = a.qpbuf[0];
-      corr = 128 - __float_as_int(a.qpbuf[1]);
+      sx = ept[EP_QP];
+      corr = 128 - __float_as_int(ept[EP_QP + 1]);
     }
   }
+  // Straight-line epilogue: every table entry is valid (rows >= M and columns
+  // >= N hold the last row / column, and are never stored), a missing bias is
+  // -0 (x + -0 and fma(x, f, -0) equal x and x * f bit for bit) and a missing
+  // row scale 1, so no operand read or output value depends on a branch.
   // OFS: acc = 2^-24 * sum (q + 128) x, so y = (acc - 2^-17 * rowsum) * (scale * 2^24)
   // (* rscale[m] for staged fp32 / bf16 activations)
   float rc[FM], rf[FM];
 #pragma unroll
   for (int b = 0; b < FM; ++b) {
+    const int rl = wm * TM + b * 16 + r;  // block row of the table
     rc[b] = 0.0f;
-    rf[b] = 1.0f;
-    if constexpr (RSP)
-      if (a.rscale) rf[b] = a.rscale[min(m0 + wm * TM + b * 16 + r, M - 1)];
+    rf[b] = RSP || I8 ? ept[EP_RF + rl] : 1.0f;
     if constexpr (RSK) {
       float t2 = 0.0f;
 #pragma unroll
-      for (int k = 0; k < KG; ++k) t2 += rsum_lds[k * BM + wm * TM + b * 16 + r];
+      for (int k = 0; k < KG; ++k) t2 += rsum_lds[k * BM + rl];
       rc[b] = t2 * 0x1p-17f;
     } else if constexpr (OFS) {
-      rc[b] = a.rsum[min(m0 + wm * TM + b * 16 + r, M - 1)] * 0x1p-17f;
+      rc[b] = ept[EP_RS + rl] * 0x1p-17f;
     }
   }
+  // per-column operands of wave tile column t (lane columns cl0 .. cl0 + 3)
+  auto col_ops = [&](int t, f32x4& sc, f32x4& bi, i32x4& cs) {
+    const int cl0 = (wn * FN + t) * 16 + 4 * g;
+    const f32x4 scv = *(const f32x4*)(ept + cl0);
+    bi = *(const f32x4*)(ept + EP_BI + cl0);
+    cs = (i32x4){0, 0, 0, 0};
+    if constexpr (I8) cs = *(const i32x4*)(ept + EP_CS + cl0);
 #pragma unroll
-  for (int t = 0; t < FN; ++t) {
-    const int n = (nt0 + wn * FN + t) * 16 + 4 * g;
-    if (n >= a.N) continue;
-    const int nvalid = min(4, a.N - n);
-    f32x4 sc, bi;
-    int cs[4];
+    for (int v = 0; v < 4; ++v) sc[v] = I8 ? (ptok ? scv[v] : sx * scv[v]) : (OFS ? scv[v] * 0x1p24f : scv[v]);
+  };
+  auto out4 = [&](int t, int b, const f32x4& sc, const f32x4& bi, const i32x4& cs) {
+    f32x4 o;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int nn = min(n + v, a.N - 1);
-      sc[v] = I8 ? (ptok ? a.scale[nn] : sx * a.scale[nn]) : (OFS ? a.scale[nn] * 0x1p24f : a.scale[nn]);
-      bi[v] = a.bias ? a.bias[nn] : 0.0f;
-      cs[v] = I8 && !ptok ? a.colsum[nn] : 0;
-    }
-#pragma unroll
-    for (int b = 0; b < FM; ++b) {
-      const int m = m0 + wm * TM + b * 16 + r;
-      if (m >= M) continue;
-      f32x4 o;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        if constexpr (I8) {
-          const int av = acc[t][b][v] + corr * cs[v];
-          if (a.acc_out && v < nvalid) a.acc_out[(int64_t)m * a.N + n + v] = av;
-          const float f = ptok ? a.rscale[m] * sc[v] : sc[v];
-          o[v] = a.bias ? __builtin_fmaf((float)av, f, bi[v]) : (float)av * f;
-        } else {
-          float out = OFS ? ((acc[t][b][v] - rc[b]) * sc[v]) * rf[b] : acc[t][b][v] * sc[v];
-          if (a.bias) out = out + bi[v];
-          o[v] = out;
-        }
+      if constexpr (I8) {
+        const int av = acc[t][b][v] + corr * cs[v];
+        const float f = ptok ? rf[b] * sc[v] : sc[v];
+        o[v] = __builtin_fmaf((float)av, f, bi[v]);
+      } else {
+        const float out = OFS ? ((acc[t][b][v] - rc[b]) * sc[v]) * rf[b] : acc[t][b][v] * sc[v];
+        o[v] = out + bi[v];
       }
-      if (lepi) {
+    }
+    return o;
+  };
+  // the whole tile into LDS (rows >= M / columns >= N are never copied out),
+  // one straight loop per output type
+  auto tile_to_lds = [&](auto f16y) {
+#pragma unroll
+    for (int t = 0; t < FN; ++t) {
+      f32x4 sc, bi;
+      i32x4 cs;
+      col_ops(t, sc, bi, cs);
+#pragma unroll
+      for (int b = 0; b < FM; ++b) {
+        const f32x4 o = out4(t, b, sc, bi, cs);
         uint32_t lo, hi;
-        if (a.yt == XT_F16) {
-          lo = pack_h2((_Float16)o[0], (_Float16)o[1]);
-          hi = pack_h2((_Float16)o[2], (_Float16)o[3]);
+        if constexpr (decltype(f16y)::value) {
+          lo = pack_h2(out_f16(o[0]), out_f16(o[1]));
+          hi = pack_h2(out_f16(o[2]), out_f16(o[3]));
         } else {
-          lo = pack_b2((__bf16)o[0], (__bf16)o[1]);
-          hi = pack_b2((__bf16)o[2], (__bf16)o[3]);
+          lo = pack_b2(out_bf16(o[0]), out_bf16(o[1]));
+          hi = pack_b2(out_bf16(o[2]), out_bf16(o[3]));
         }
         *(u32x2*)(lds + (wm * TM + b * 16 + r) * ERS + ((wn * FN + t) * 16 + 4 * g) * 2) = (u32x2){lo, hi};
-      } else {
-        store_y4(a.y, a.yt, (int64_t)m * a.ldy + n, o, yvec && nvalid == 4, nvalid);
+      }
+    }
+  };
+  if (lepi) {
+    if (a.yt == XT_F16)
+      tile_to_lds(std::true_type{});
+    else
+      tile_to_lds(std::false_type{});
+  } else {
+#pragma unroll
+    for (int t = 0; t < FN; ++t) {
+      const int n = (nt0 + wn * FN + t) * 16 + 4 * g;
+      const int nvalid = min(4, a.N - n);
+      f32x4 sc, bi;
+      i32x4 cs;
+      col_ops(t, sc, bi, cs);
+#pragma unroll
+      for (int b = 0; b < FM; ++b) {
+        const int m = m0 + wm * TM + b * 16 + r;
+        const f32x4 o = out4(t, b, sc, bi, cs);
+        if (m < M && n < a.N) store_y4(a.y, a.yt, (int64_t)m * a.ldy + n, o, yvec && nvalid == 4, nvalid);
+      }
+    }
+  }
+  if constexpr (I8) {
+    if (a.acc_out) {  // int32 accumulators with the zero-point correction (tests and tools)
+#pragma unroll
+      for (int t = 0; t < FN; ++t) {
+        const int cl0 = (wn * FN + t) * 16 + 4 * g;
+        const int n = nt0 * 16 + cl0;
+        const i32x4 cs = *(const i32x4*)(ept + EP_CS + cl0);
+#pragma unroll
+        for (int b = 0; b < FM; ++b) {
+          const int m = m0 + wm * TM + b * 16 + r;
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (m < M && n + v < a.N) a.acc_out[(int64_t)m * a.N + n + v] = acc[t][b][v] + corr * cs[v];
+        }
       }
     }
   }

@@ -964,28 +964,53 @@ LEPI_CASES = [(2048, 12288, 128), (2048, 4096, 192), (1024, 4096, 256), (100, 10
 
 @pytest.mark.parametrize("M,N,K", LEPI_CASES)
 def test_gemm_2byte_outputs_equal_rounded_fp32(dev, M, N, K):
+    """Also with a bias: the last fma of the epilogue must round to fp32 before
+    the 16-bit conversion (a fused fma-to-fp16 rounds once and differs in about
+    one output in 20000)."""
     announce(f"gemm 2-byte outputs M={M} N={N} K={K}")
     w = make_weights(N, K, 4100 + N + K)
     x = make_x(M, K, 4200 + M + K, outliers=True).half().to(dev)
     lin = quant.Int8Linear(w, None)
     dyn = quant.DynamicInt8Linear(w, None)
-    y32 = quant.linear_w8(x, lin.packed, lin.scale, None, N)
-    d32 = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N)
-    t32 = quant.linear_w8a8_token(x, dyn.packed, dyn.scale, None, N)
-    for od in (torch.float16, torch.bfloat16):
-        wide = torch.empty((M, N + 3), dtype=od, device=dev)
-        for out in (None, wide[:, :N]):  # dense rows; rows with an odd stride (no 16-byte stores)
-            got = quant.linear_w8(x, lin.packed, lin.scale, None, N, od, out=out)
-            np.testing.assert_array_equal(_bits(got), _bits(y32.to(od)))
-            got = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N, od, out=out)
-            np.testing.assert_array_equal(_bits(got), _bits(d32.to(od)))
-            got = quant.linear_w8a8_token(x, dyn.packed, dyn.scale, None, N, od, out=out)
-            np.testing.assert_array_equal(_bits(got), _bits(t32.to(od)))
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(4300 + N)).to(dev)
+    for b in (None, bias):
+        y32 = quant.linear_w8(x, lin.packed, lin.scale, b, N)
+        d32 = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, b, N)
+        t32 = quant.linear_w8a8_token(x, dyn.packed, dyn.scale, b, N)
+        for od in (torch.float16, torch.bfloat16):
+            wide = torch.empty((M, N + 3), dtype=od, device=dev)
+            for out in (None, wide[:, :N]):  # dense rows; rows with an odd stride (no 16-byte stores)
+                got = quant.linear_w8(x, lin.packed, lin.scale, b, N, od, out=out)
+                np.testing.assert_array_equal(_bits(got), _bits(y32.to(od)))
+                got = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, b, N, od, out=out)
+                np.testing.assert_array_equal(_bits(got), _bits(d32.to(od)))
+                got = quant.linear_w8a8_token(x, dyn.packed, dyn.scale, b, N, od, out=out)
+                np.testing.assert_array_equal(_bits(got), _bits(t32.to(od)))
     xb = x.to(torch.bfloat16)  # bf16 activations without a workspace: the bf16 kernel
     ref = quant.linear_w8(xb, lin.packed, lin.scale, None, N, workspace=torch.empty(0, dtype=torch.uint8, device=dev))
     got = quant.linear_w8(xb, lin.packed, lin.scale, None, N, torch.bfloat16,
                           workspace=torch.empty(0, dtype=torch.uint8, device=dev))
     np.testing.assert_array_equal(_bits(got), _bits(ref.to(torch.bfloat16)))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (4, 6144, 4096), (16, 1000, 2560), (24, 4096, 4096), (1, 4096, 12288)])
+def test_gemv_2byte_outputs_equal_rounded_fp32(dev, M, N, K):
+    """Decode GEMVs (fast path for M <= 16, general kernel beyond): fp16 /
+    bf16 outputs, with and without a bias, equal the fp32 output rounded."""
+    announce(f"gemv 2-byte outputs M={M} N={N} K={K}")
+    w = make_weights(N, K, 4400 + N + K)
+    x = make_x(M, K, 4500 + M + K, outliers=True).half().to(dev)
+    lin = quant.Int8Linear(w, None)
+    dyn = quant.DynamicInt8Linear(w, None)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(4600 + N)).to(dev)
+    for b in (None, bias):
+        y32 = quant.linear_w8(x, lin.packed, lin.scale, b, N)
+        d32 = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, b, N)
+        for od in (torch.float16, torch.bfloat16):
+            got = quant.linear_w8(x, lin.packed, lin.scale, b, N, od)
+            np.testing.assert_array_equal(_bits(got), _bits(y32.to(od)))
+            got = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, b, N, od)
+            np.testing.assert_array_equal(_bits(got), _bits(d32.to(od)))
 
 
 def test_graph_replays_lds_epilogue(dev):
