@@ -357,22 +357,52 @@ def hybrid_stack_shapes(H=4096, F=12288, heads=32, kv_heads=8, d=128, routers=4,
     return shapes
 
 
-def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False):
+def grouped_stack_launches(H=4096, heads=32, d=128):
+    """The fused stack's launches with the independent pairs of each hybrid
+    layer grouped (sbq_linear_w8_grouped): lora_q[1] + lora_k[1] (two inputs
+    of K = 128) and sse_o + swa_o (two attention outputs of K = 4096).  Each
+    launch is a list of (N, K); the weight bytes are the fused stack's."""
+    pair_lora = [(heads * d, d), (heads * d, d)]
+    pair_o = [(H, heads * d), (H, heads * d)]
+    shapes = hybrid_stack_shapes(fused=True)
+    out, i = [], 0
+    while i < len(shapes):
+        if shapes[i:i + 2] == pair_lora or shapes[i:i + 2] == pair_o:
+            out.append(shapes[i:i + 2])
+            i += 2
+        else:
+            out.append([shapes[i]])
+            i += 1
+    return out
+
+
+def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False):
     torch, quant = ctx.torch, ctx.quant
-    shapes = hybrid_stack_shapes(fused=fused)
+    launches = grouped_stack_launches() if grouped else [[sh] for sh in hybrid_stack_shapes(fused=fused)]
+    shapes = [sh for grp in launches for sh in grp]
     layers = [ctx.weights(N, K, 2000 + i) for i, (N, K) in enumerate(shapes)]
     wbytes = sum(N * K for N, K in shapes)
-    res = {"linears": len(shapes), "weight_bytes": wbytes}
+    res = {"linears": len(shapes), "launches": len(launches), "weight_bytes": wbytes}
     for M in Ms:
         xs = {}
         for N, K in shapes:
             if K not in xs:
-                xs[K] = ctx.act(M, K, 3000 + K)
+                xs[K] = [ctx.act(M, K, 3000 + K), ctx.act(M, K, 3500 + K)]  # a grouped pair reads two inputs
         ys = [torch.empty((M, N), dtype=torch.float16, device=ctx.dev) for N, K in shapes]
+        plan, j = [], 0
+        for grp in launches:
+            plan.append((grp, layers[j:j + len(grp)], ys[j:j + len(grp)]))
+            j += len(grp)
 
         def step():
-            for (packed, s, _), y, (N, K) in zip(layers, ys, shapes):
-                quant.linear_w8(xs[K], packed, s, None, N, out=y)
+            for grp, lays, outs in plan:
+                if len(grp) == 1:
+                    (N, K), (packed, s, _) = grp[0], lays[0]
+                    quant.linear_w8(xs[K][0], packed, s, None, N, out=outs[0])
+                else:
+                    quant.linear_w8_grouped([xs[K][i] for i, (N, K) in enumerate(grp)], [p for p, _, _ in lays],
+                                            [s for _, s, _ in lays], [None] * len(grp), [N for N, _ in grp],
+                                            outs=outs)
 
         g = ctx.graph(step)
         ms = ctx.time_graphs([g], steps, warmup)
@@ -731,6 +761,8 @@ def main():
         return
     if args.only:
         fn = {"lm_head_greedy": lm_head_greedy_bench, "device_state": device_state_bench,
+              "stack_fused": lambda ctx: stack_bench(ctx, fused=True),
+              "stack_grouped": lambda ctx: stack_bench(ctx, grouped=True),
               "cpu_baseline": lambda ctx: cpu_baseline(args.cpu_budget)}[args.only]
         print(json.dumps({args.only: fn(ctx)}), flush=True)
         return
@@ -766,6 +798,8 @@ def main():
         extra["stack"] = stack_bench(ctx)
         log("36-layer linear stack, layers reading the same input fused")
         extra["stack_fused"] = stack_bench(ctx, fused=True)
+        log("36-layer linear stack, fused, independent pairs grouped")
+        extra["stack_grouped"] = stack_bench(ctx, grouped=True)
         torch.cuda.empty_cache()
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)

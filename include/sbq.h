@@ -124,6 +124,27 @@ int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   void* y, int y_dtype, int64_t ldy,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* `count` (1..SBQ_MAX_GROUP) independent weight-only linears that share M, K,
+ * x_dtype and y_dtype, in one launch where the decode path applies: linear i
+ * is y_i = linear(x_i, packed_i, scale_i, bias_i) exactly as sbq_linear_w8
+ * defines it (x_i rows of stride ldx[i], y_i [M, N[i]] of stride ldy[i]).
+ * The arguments are host arrays of `count` device pointers / sizes; `bias`
+ * may be NULL (no biases) or hold NULL entries.  For decode shapes (M <= 16,
+ * K % 64 == 0, 16-byte aligned x rows) the linears run as one GEMV launch:
+ * the launch ramp and tail of a small projection are paid once per group
+ * (two 4096 x 4096 projections of different inputs: 2 x 5.1 us -> 7.5 us).
+ * Otherwise each runs as sbq_linear_w8 without a workspace.  Results may differ
+ * from separate sbq_linear_w8 calls in the fp32 summation order (the group is
+ * tiled as one layer of its summed rows).  No counterpart in the reference:
+ * it is for callers holding several independent projections of one step
+ * (model.py: the two lora up-projections, the SSE and SWA output projections
+ * of a hybrid layer). */
+#define SBQ_MAX_GROUP 4
+int sbq_linear_w8_grouped(int count, const void* const* x, const int64_t* ldx, int x_dtype,
+                          int64_t M, int64_t K, const uint8_t* const* packed,
+                          const float* const* scale, const float* const* bias, const int64_t* N,
+                          void* const* y, const int64_t* ldy, int y_dtype, void* stream);
+
 /* Workspace bytes that let sbq_linear_w8 run its fastest prefill path for an
  * [M, K] input of x_dtype: 2 * M floats (F16), plus M * K * 2 bytes (BF16) or
  * M * K * 4 bytes (F32) of staged activations, plus alignment slack.  0 for a

@@ -193,6 +193,46 @@ int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                              yv);
 }
 
+int sbq_linear_w8_grouped(int count, const void* const* x, const int64_t* ldx, int x_dtype, int64_t M, int64_t K,
+                          const uint8_t* const* packed, const float* const* scale, const float* const* bias,
+                          const int64_t* N, void* const* y, const int64_t* ldy, int y_dtype, void* stream) {
+  if (count < 1 || count > SBQ_MAX_GROUP || !x || !ldx || !packed || !scale || !N || !y || !ldy) return SBQ_ERR_ARG;
+  static_assert(SBQ_MAX_GROUP == sbq::kGemvMaxSeg, "one segment per linear");
+  bool xv = true, yv = true;
+  for (int i = 0; i < count; ++i) {
+    const int rc = check_linear(x[i], x_dtype, M, K, ldx[i], packed[i], scale[i], N[i], y[i], y_dtype, ldy[i]);
+    if (rc) return rc;
+    if (M > 0) {
+      xv = xv && x_vec_ok(x[i], x_dtype, ldx[i]);
+      yv = yv && y_vec_ok(y[i], y_dtype, ldy[i], N[i]);
+    }
+  }
+  if (M == 0) return SBQ_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (count > 1 && sbq::gemv_supports(M, K, false, x_dtype)) {
+    sbq::GemvSeg segs[SBQ_MAX_GROUP] = {};
+    for (int i = 0; i < count; ++i) {
+      segs[i].x = x[i];
+      segs[i].packed = packed[i];
+      segs[i].scale = scale[i];
+      segs[i].bias = bias ? bias[i] : nullptr;
+      segs[i].y = y[i];
+      segs[i].ldx = ldx[i];
+      segs[i].ldy = ldy[i];
+      segs[i].N = (int)N[i];
+      segs[i].Nt = (int)((N[i] + 15) / 16);
+    }
+    const int rc = sbq::launch_gemv_w8_grouped(segs, count, x_dtype, M, K, xv, y_dtype, yv, st);
+    if (rc != -1) return rc;
+  }
+  for (int i = 0; i < count; ++i) {  // one by one: the shapes the grouped launch does not take
+    const int rc = sbq_linear_w8(x[i], x_dtype, M, K, ldx[i], packed[i], scale[i], bias ? bias[i] : nullptr, N[i],
+                                 y[i], y_dtype, ldy[i], nullptr, 0, stream);
+    if (rc) return rc;
+  }
+  return SBQ_OK;
+}
+
 int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K) {
   static_assert(sbq::kMinMaxPartials * sizeof(float2) <= kWsPartialBytes, "partials fit");
   if (M < 0 || K < 0 || M > kIntMax || K > kIntMax) return 0;

@@ -1254,6 +1254,9 @@ int launch_gemm_w8a8_token(const void* x, int xt, int64_t M, int64_t K, int64_t 
     int id = 0, ks = 0;
     if (pick_gemv_fast(M, Kp, N, XT_F16, false, true, &id, &ks)) {
       rc = launch_gemv_fast_cfg(id, ks, g, XT_S8, true, st);
+      // s8 rows load their fragments directly: an x-in-LDS pick (id 0)
+      // runs as its direct-fragment equivalent (id 3, D = 8, G = 1)
+      if (rc == -1 && id == 0) rc = launch_gemv_fast_cfg(3, ks, g, XT_S8, true, st);
       if (rc != -1) return rc;
     }
   }

@@ -534,6 +534,25 @@ int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
   return -2;
 }
 
+// Independent weight-only linears of one M, K and dtypes in one fast-path
+// launch (picked as one linear of their summed rows).  -1: the fast path does
+// not apply; the caller runs them one by one.
+int launch_gemv_w8_grouped(const GemvSeg* segs, int n, int xt, int64_t M, int64_t K, bool xvec, int yt, bool yvec,
+                           hipStream_t st) {
+  if (n < 2 || n > kGemvMaxSeg) return -1;
+  int64_t nt = 0;
+  for (int i = 0; i < n; ++i) nt += segs[i].Nt;
+  int fid, fks;
+  if (!pick_gemv_fast(M, K, nt * 16, xt, false, xvec, &fid, &fks)) return -1;
+  GemvArgs a{};
+  a.M = (int)M; a.K = (int)K; a.Kc = (int)(K / 64);
+  a.yt = yt;
+  a.flags = (xvec ? kGemvXVec : 0) | (yvec ? kGemvYVec : 0);
+  a.nseg = n;
+  for (int i = 0; i < n; ++i) a.seg[i] = segs[i];
+  return launch_gemv_fast_grouped(fid, fks, a, xt, st);
+}
+
 int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                      const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int yt,
                      int64_t ldy, int32_t* acc_out, float2* partials, hipStream_t st, bool yvec,

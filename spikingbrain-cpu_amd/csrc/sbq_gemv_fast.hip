@@ -175,8 +175,33 @@ __device__ __forceinline__ void argmax_epilogue(uint8_t* state, int64_t* idx, un
 // pre-pass; 2 W8A8 that reduces min/max over the whole (small) x itself;
 // 3 per-token symmetric W8A8 on pre-quantized s8 activations (XT_S8) with
 // per-row scales a.rscale.
-template <int XT, int D, int G, bool XL, int QM>
+// GRP: grouped weight-only launch (a.nseg linears, see GemvArgs); a separate
+// instance, so that the single-linear kernels carry no segment lookup.
+template <int XT, int D, int G, bool XL, int QM, bool GRP = false>
 __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs a, int KW, int xch) {
+  static_assert(!GRP || QM == 0, "grouped launches: weight-only");
+  int bid = blockIdx.x;
+  if constexpr (GRP) {
+    {  // this workgroup's linear (uniform); fields read at constant indexes
+       // only: a runtime index into the argument struct would move it to
+       // private memory
+#pragma unroll
+      for (int i = 0; i < kGemvMaxSeg; ++i) {
+        if (i < a.nseg && (int)blockIdx.x >= a.seg[i].wg0) {
+          a.x = a.seg[i].x;
+          a.packed = a.seg[i].packed;
+          a.scale = a.seg[i].scale;
+          a.bias = a.seg[i].bias;
+          a.y = a.seg[i].y;
+          a.ldx = a.seg[i].ldx;
+          a.ldy = a.seg[i].ldy;
+          a.N = a.seg[i].N;
+          a.Nt = a.seg[i].Nt;
+          bid = (int)blockIdx.x - a.seg[i].wg0;
+        }
+      }
+    }
+  }
   constexpr bool W8A8 = QM != 0;
   constexpr bool PT = QM == 3;
   static_assert(!PT || (XT == XT_S8 && !XL), "per-token: s8 fragments loaded directly");
@@ -187,7 +212,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   const int tid = threadIdx.x, lane = tid & 63, ks = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int M = a.M, Kc = a.Kc, K = a.K;
-  const int nt0 = blockIdx.x * G;
+  const int nt0 = bid * G;
   const int kbeg = ks * KW;
   const int cnt = min(KW, Kc - kbeg);  // >= 1: the host sizes KS so that every wave has a tile
   const int mr = min(r, M - 1);
@@ -459,17 +484,17 @@ constexpr FastCfg kFastCfgs[] = {
 };
 constexpr int kNumFastCfgs = sizeof(kFastCfgs) / sizeof(kFastCfgs[0]);
 
-template <int XT, int QM>
+template <int XT, int QM, bool GRP = false>
 int launch_fast_typed(int id, const GemvArgs& a, int ks, int KW, int xch, size_t lds, hipStream_t st) {
   const dim3 block(ks * 64);
   switch (id) {
-#define SBQ_FAST_CASE(ID, D, G, XL)                                                                           \
-  case ID:                                                                                                    \
-    if constexpr (QM != 3 || !XL) {                                                                           \
-      hipLaunchKernelGGL((gemv_fast_kernel<XT, D, G, XL, QM>), dim3((a.Nt + G - 1) / G), block, lds, st, a, KW, \
-                         xch);                                                                                \
-      return check_launch();                                                                                  \
-    }                                                                                                         \
+#define SBQ_FAST_CASE(ID, D, G, XL)                                                                     \
+  case ID:                                                                                              \
+    if constexpr (QM != 3 || !XL) {                                                                     \
+      hipLaunchKernelGGL((gemv_fast_kernel<XT, D, G, XL, QM, GRP>), dim3((a.Nt + G - 1) / G), block, lds, \
+                         st, a, KW, xch);                                                               \
+      return check_launch();                                                                            \
+    }                                                                                                   \
     return -1;
     SBQ_FAST_CONFIGS(SBQ_FAST_CASE)
 #undef SBQ_FAST_CASE
@@ -509,7 +534,9 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   if (qm == 2 && (xbytes > (int64_t)kFusedChunks * 16 * T || ks < kFusedMinWaves)) return -1;
 #define SBQ_FAST_QM(XT_)                                                  \
   switch (qm) {                                                           \
-    case 0: return launch_fast_typed<XT_, 0>(id, a, ks, KW, xch, lds, st); \
+    case 0:                                                               \
+      return a.nseg > 1 ? launch_fast_typed<XT_, 0, true>(id, a, ks, KW, xch, lds, st) \
+                        : launch_fast_typed<XT_, 0>(id, a, ks, KW, xch, lds, st);      \
     case 1: return launch_fast_typed<XT_, 1>(id, a, ks, KW, xch, lds, st); \
     default: return launch_fast_typed<XT_, 2>(id, a, ks, KW, xch, lds, st); \
   }
@@ -520,6 +547,29 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   }
 #undef SBQ_FAST_QM
   return -2;
+}
+
+// Grouped weight-only launch of configuration `id`: a.seg[0 .. a.nseg) hold
+// the linears (x, weights, scales, bias, y, strides, N, Nt); every linear
+// gets ceil(Nt / G) workgroups of the grid, in segment order.  M, K, the
+// dtypes and the flags are shared.  Returns -1 when the configuration cannot
+// run the shape.
+int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, hipStream_t st) {
+  if (id < 0 || id >= kNumFastCfgs || a.nseg < 2 || a.nseg > kGemvMaxSeg) return -1;
+  const int G = kFastCfgs[id].G;
+  int64_t wg = 0;
+  for (int s = 0; s < a.nseg; ++s) {
+    a.seg[s].wg0 = (int)wg;
+    wg += (a.seg[s].Nt + G - 1) / G;
+  }
+  if (wg * G > 0x7fffffff / 16) return -1;
+  // the launch-wide fields describe the whole grid (the kernel takes each
+  // workgroup's operands from its segment)
+  a.Nt = (int)(wg * G);
+  a.N = a.Nt * 16;
+  a.x = a.seg[0].x;
+  a.ldx = a.seg[0].ldx;
+  return launch_gemv_fast_cfg(id, ks, a, xt, false, st);
 }
 
 // Fast-path choice for a shape (false: the general kernel runs).  Measured on
@@ -552,6 +602,25 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     const bool wide = Kc < 128 && Nt >= 384;
     *id = wide ? 4 : 3;  // D=4, G=2 | D=8, G=1
     *ks = 4;
+    if (!w8a8) {
+      // Measured on MI355X at M = 1, 4, 8 (fp16 x, interleaved timings of
+      // every configuration):
+      // * K <= 256: one wave of 4-tile steps (lora_*[1], K = 128: 2.65 ->
+      //   2.39 us at M = 1, 2.92 -> 2.46 at M = 8);
+      // * x in LDS, one row tile per workgroup, when x fits: on layers of
+      //   fewer than 256 row tiles (N = 4 .. 3000: 0.1-0.4 us per launch), and
+      //   on wide layers whose two-tile grid takes more rounds of 256 CUs
+      //   than the one-tile grid (N = 18820: 15.0 -> 14.2 us, N = 10000:
+      //   10.2 -> 9.2 us; N = 6144, 8192, 24576 and 151936 keep two tiles).
+      const auto rounds = [](int64_t wgs) { return (wgs + 255) / 256; };
+      const bool xl = M * K * 2 <= kFastXLdsBytes;
+      if (Kc <= 4) {
+        *id = 2;  // D=4, G=1
+        *ks = 1;
+      } else if (xl && (wide ? rounds(Nt) < 2 * rounds((Nt + 1) / 2) : Nt < 256)) {
+        *id = 0;  // D=8, G=1, x in LDS
+      }
+    }
   } else {
     const bool wide = Kc <= 64 && Nt >= 384;
     *id = wide ? 5 : 3;  // D=8, G=2 | D=8, G=1

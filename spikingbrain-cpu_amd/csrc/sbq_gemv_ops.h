@@ -9,6 +9,19 @@
 namespace sbq {
 
 // Arguments of the decode GEMV kernels (one struct, passed by value).
+// One linear of a grouped decode launch: its operands and the first
+// workgroup of its share of the grid.
+struct GemvSeg {
+  const void* x;
+  const uint8_t* packed;
+  const float* scale;
+  const float* bias;
+  void* y;
+  int64_t ldx, ldy;
+  int N, Nt, wg0, pad;
+};
+constexpr int kGemvMaxSeg = 4;  // linears per grouped launch
+
 struct GemvArgs {
   const void* x;
   int64_t ldx;
@@ -31,6 +44,11 @@ struct GemvArgs {
   // it) and the int64 token per row
   uint8_t* am_state;
   int64_t* idx;
+  // grouped launch (weight-only fast path): nseg > 1 independent linears of
+  // the same M, K and dtypes; workgroup b belongs to the last segment s with
+  // seg[s].wg0 <= b and takes its operands (the fields above describe none)
+  int nseg;
+  GemvSeg seg[kGemvMaxSeg];
 };
 // The fused argmax's state: kArgmaxSlots slots of 16 row keys (128 bytes) and
 // a count, kArgmaxSlotBytes apart, then the count of finished slots.

@@ -33,8 +33,16 @@ bool gemv_supports(int64_t M, int64_t K, bool w8a8, int xt);
 // pick_gemv_fast chooses a configuration id and the waves per workgroup;
 // launch_gemv_fast_cfg returns -1 when that configuration cannot run the shape.
 struct GemvArgs;
+struct GemvSeg;
 bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks);
 int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, hipStream_t st);
+// Grouped weight-only launch: a.seg / a.nseg hold 2..kGemvMaxSeg linears.
+int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, hipStream_t st);
+// n independent weight-only linears sharing M, K and dtypes in one launch
+// (x / weight / scale / bias / y / strides / N / Nt per segment); -1 when the
+// fast path does not apply.
+int launch_gemv_w8_grouped(const GemvSeg* segs, int n, int xt, int64_t M, int64_t K, bool xvec, int yt, bool yvec,
+                           hipStream_t st);
 
 // Fused greedy token of the decode GEMV (fp32 y, M <= 16): the argmax state
 // (kArgmaxStateBytes, zero before a launch, zero again after it) and the

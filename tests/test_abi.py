@@ -97,6 +97,24 @@ def test_argument_validation_without_gpu(lib):
     assert lib.sbq_argmax_rows(dummy, 1, 8, 4, dummy, None) == -1
     assert lib.sbq_argmax_rows(None, 1, 8, 8, dummy, None) == -1
     assert lib.sbq_argmax_rows(None, 0, 8, 8, None, None) == 0
+    # grouped weight-only linears: 1..SBQ_MAX_GROUP linears, each checked as
+    # sbq_linear_w8 checks one; M == 0 is a no-op
+    def arr(ct, vals):
+        return (ct * len(vals))(*vals)
+
+    def grouped(count, M, K, ldx, N, ldy, packed=4096, xdt=0):
+        n = max(count, 1)
+        return lib.sbq_linear_w8_grouped(count, arr(P, [4096] * n), arr(ctypes.c_int64, [ldx] * n), xdt, M, K,
+                                         arr(P, [packed] * n), arr(P, [4096] * n), None, arr(ctypes.c_int64, [N] * n),
+                                         arr(P, [4096] * n), arr(ctypes.c_int64, [ldy] * n), 0, None)
+
+    assert grouped(0, 1, 64, 64, 16, 16) == -1
+    assert grouped(_lib.SBQ_MAX_GROUP + 1, 1, 64, 64, 16, 16) == -1
+    assert grouped(2, 1, 64, 32, 16, 16) == -1        # ldx < K
+    assert grouped(2, 1, 64, 64, 16, 8) == -1         # ldy < N
+    assert grouped(2, 1, 64, 64, 16, 16, xdt=7) == -2
+    assert grouped(2, 1, 64, 64, 16, 16, packed=4097) == -3
+    assert grouped(2, 0, 64, 64, 16, 16) == 0
     # row / column counts beyond 2^31 - 1 are rejected before any launch
     big = 1 << 31
     assert lib.sbq_linear_w8(dummy, 0, big, 64, 64, dummy, dummy, None, 16, dummy, 0, 16, None, 0, None) == -1

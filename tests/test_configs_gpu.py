@@ -608,3 +608,89 @@ def test_split_k_graph_replays(dev):
         e2 = quant.linear_w8(x, lin.packed, lin.scale, None, N, workspace=quant.w8_workspace(M, K, dev, torch.float16, N))
         np.testing.assert_array_equal(y1.cpu().numpy(), e1.cpu().numpy())
         np.testing.assert_array_equal(y2.cpu().numpy(), e2.cpu().numpy())
+
+
+# ---------------------------------------------------------------------------
+# grouped launch of independent weight-only linears (sbq_linear_w8_grouped)
+# ---------------------------------------------------------------------------
+GROUP_CASES = [
+    # (M, K, Ns, x dtype): the hybrid layer's pairs (lora up-projections,
+    # SSE / SWA output projections), mixed and ragged widths, fp32 / bf16 x,
+    # and M > 16 (no grouped kernel: the linears run one by one)
+    (1, 128, (4096, 4096), "f16"),
+    (1, 4096, (4096, 4096), "f16"),
+    (4, 4096, (1000, 64, 4096, 4), "f16"),
+    (16, 4096, (2048, 6144), "bf16"),
+    (1, 4096, (4096, 4096, 4096), "f32"),
+    (1, 12288, (4096, 10), "f16"),
+    (24, 4096, (4096, 1000), "f16"),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,Ns,xd", GROUP_CASES)
+def test_grouped_linears(dev, M, K, Ns, xd):
+    """Each output of a grouped call equals its linear run alone to fp32
+    summation order, and the oracle within the weight-only tolerance; the
+    module helper returns what each layer's forward returns."""
+    announce(f"grouped linears M={M} K={K} Ns={Ns} x={xd}")
+    ws = [gpu_weight(N, K, 900 + i, dev) for i, N in enumerate(Ns)]
+    bs = [torch.randn(N, generator=torch.Generator().manual_seed(920 + i)) if i % 2 else None
+          for i, N in enumerate(Ns)]
+    lins = [quant.Int8Linear(w, None if b is None else b.to(dev)) for w, b in zip(ws, bs)]
+    xs = [cpu_x(M, K, 910 + i).to(DT[xd]) for i in range(len(Ns))]
+    xg = [x.to(dev) for x in xs]
+    biases = [lin.bias for lin in lins]
+    for yd in (torch.float32, torch.float16):
+        got = quant.linear_w8_grouped(xg, [lin.packed for lin in lins], [lin.scale for lin in lins], biases,
+                                      list(Ns), yd)
+        for i, (lin, N) in enumerate(zip(lins, Ns)):
+            sep = quant.linear_w8(xg[i], lin.packed, lin.scale, biases[i], N, yd)
+            g = got[i].float().cpu().numpy()
+            assert g.shape == (M, N)
+            assert oracle.rel_l2(g, sep.float().cpu().numpy()) <= (1e-5 if yd == torch.float32 else 1e-3), (i, yd)
+            cols = tile_sample(N, 930 + i)
+            q, s = ref_rows(ws[i], cols)
+            b = None if bs[i] is None else bs[i].numpy()[cols]
+            ref = oracle.int8_linear(xs[i].float().numpy(), q, s, b)
+            tol = W8_TOL_EXACT_X if (xd != "f32" and yd == torch.float32) else W8_TOL
+            assert oracle.rel_l2(g[:, cols], ref) <= tol, (i, yd)
+    outs = quant.grouped_forward(list(zip(lins, xg)))
+    for lin, x, o in zip(lins, xg, outs):
+        ref = lin(x)
+        assert o.shape == ref.shape and o.dtype == ref.dtype
+        assert oracle.rel_l2(o.cpu().numpy(), ref.cpu().numpy()) <= 1e-5
+
+
+@pytest.mark.gpu
+def test_grouped_linears_graph_replays(dev):
+    """The grouped launch under HIP graph capture: every replay equals the
+    eager result."""
+    announce("grouped linears graph replays")
+    K, Ns = 4096, (4096, 4096)
+    lins = [quant.Int8Linear(gpu_weight(N, K, 940 + i, dev), None) for i, N in enumerate(Ns)]
+    xg = [cpu_x(1, K, 950 + i).half().to(dev) for i in range(len(Ns))]
+    outs = [torch.empty((1, N), dtype=torch.float16, device=dev) for N in Ns]
+
+    def run():
+        quant.linear_w8_grouped(xg, [lin.packed for lin in lins], [lin.scale for lin in lins], [None, None],
+                                list(Ns), outs=outs)
+
+    run()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    for _ in range(3):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e)
