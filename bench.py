@@ -289,20 +289,50 @@ def device_state_bench(ctx, fmt="int8", H=2048, F=5632, blocks=4, V=32000, heads
 # ---------------------------------------------------------------------------
 # prefill GEMM and int8-dyn
 # ---------------------------------------------------------------------------
-def prefill_bench(ctx, M, N=12288, K=4096, steps=20, warmup=5, xdtype=None, per_graph=5):
+def prefill_bench(ctx, M, N=12288, K=4096, steps=20, warmup=5, xdtype=None, per_graph=5, ydtype=None):
     quant = ctx.quant
     packed, s, _ = ctx.weights(N, K, 900)
     x = ctx.act(M, K, 901)
     if xdtype is not None:
         x = x.to(xdtype)
-    y = ctx.torch.empty((M, N), dtype=ctx.torch.float16, device=ctx.dev)
-    ws = quant.w8_workspace(M, K, ctx.dev, x.dtype)  # row-sum scratch: the pre-pass is part of each timed step
+    y = ctx.torch.empty((M, N), dtype=ydtype or ctx.torch.float16, device=ctx.dev)
+    ws = quant.w8_workspace(M, K, ctx.dev, x.dtype, N)  # the pre-passes are part of each timed step
     # per_graph steps per graph replay: the launch gap between replays is not the kernel's
     ms = ctx.time_steps(lambda c: quant.linear_w8(x, packed, s, None, N, out=y, workspace=ws), per_graph, steps,
                         warmup)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-    return {"M": M, "N": N, "K": K, "x": str(x.dtype).replace("torch.", ""), "ms": ms, "TFLOPs": tflops,
-            "mfma_frac": tflops / F16_PEAK_TFLOPS}
+    return {"M": M, "N": N, "K": K, "x": str(x.dtype).replace("torch.", ""), "y": str(y.dtype).replace("torch.", ""),
+            "ms": ms, "TFLOPs": tflops, "mfma_frac": tflops / F16_PEAK_TFLOPS}
+
+
+def midm_bench(ctx, M, N, fmt, K=4096, steps=20, warmup=5):
+    """One mid-sized linear (fp16 x and y): the whole call (pre-passes, GEMM,
+    split-K fixup) with weights rotating over copies beyond the 256 MB
+    Infinity Cache, as a layer-by-layer forward reads them."""
+    torch, quant = ctx.torch, ctx.quant
+    copies = math.ceil(ROTATE_BYTES / (N * K)) + 1
+    layers = [ctx.weights(N, K, 960 + c, colsum=fmt == "int8-dyn") for c in range(copies)]
+    x = ctx.act(M, K, 961, outliers=fmt == "int8-dyn")
+    y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
+    if fmt == "int8-dyn":
+        ws = quant.w8a8_workspace(M, K, ctx.dev, N)
+
+        def step(c):
+            L = layers[c]
+            quant.linear_w8a8(x, L[0], L[1], L[2], None, N, torch.float16, workspace=ws, out=y)
+    else:
+        ws = quant.w8_workspace(M, K, ctx.dev, x.dtype, N)
+
+        def step(c):
+            L = layers[c]
+            quant.linear_w8(x, L[0], L[1], None, N, out=y, workspace=ws)
+
+    ms = ctx.time_steps(step, copies, max(steps, copies), warmup)
+    ops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    peak = I8_PEAK_TOPS if fmt == "int8-dyn" else F16_PEAK_TFLOPS
+    del layers
+    return {"format": fmt, "M": M, "N": N, "K": K, "us": ms * 1e3, "TOPs_or_TFLOPs": ops, "peak_frac": ops / peak,
+            "GBps": gemv_bytes(M, N, K) / (ms * 1e-3) / 1e9}
 
 
 def w8a8_bench(ctx, M, N, K=4096, steps=20, warmup=5):
@@ -314,7 +344,7 @@ def w8a8_bench(ctx, M, N, K=4096, steps=20, warmup=5):
     layers = [ctx.weights(N, K, 950 + c, colsum=True) for c in range(ncopy)]
     x = ctx.act(M, K, 951, outliers=True)
     y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
-    ws = quant.w8a8_workspace(M, K, ctx.dev)
+    ws = quant.w8a8_workspace(M, K, ctx.dev, N)
     def step(c):
         L = layers[c % ncopy]
         quant.linear_w8a8(x, L[0], L[1], L[2], None, N, torch.float16, workspace=ws, out=y)
@@ -762,6 +792,10 @@ def main():
     if args.only:
         fn = {"lm_head_greedy": lm_head_greedy_bench, "device_state": device_state_bench,
               "stack_fused": lambda ctx: stack_bench(ctx, fused=True),
+              "mid_m": lambda ctx: [midm_bench(ctx, M, N, fmt) for fmt in ("int8", "int8-dyn") for M in (64, 128, 256)
+                                    for N in (4096, 12288)],
+              "prefill_fp32_y": lambda ctx: [prefill_bench(ctx, M, xdtype=xd, ydtype=ctx.torch.float32)
+                                             for M in (512, 2048) for xd in (ctx.torch.float16, ctx.torch.float32)],
               "stack_grouped": lambda ctx: stack_bench(ctx, grouped=True),
               "cpu_baseline": lambda ctx: cpu_baseline(args.cpu_budget)}[args.only]
         print(json.dumps({args.only: fn(ctx)}), flush=True)
@@ -788,6 +822,13 @@ def main():
         # the reference model's own activations are fp32: staged as fp16 hi + lo planes
         extra["prefill_other_x"] = [prefill_bench(ctx, 2048, xdtype=dt)
                                     for dt in (ctx.torch.bfloat16, ctx.torch.float32)]
+        # fp32 outputs (the reference returns fp32), with fp16 and fp32 activations
+        f32 = ctx.torch.float32
+        extra["prefill_fp32_y"] = [prefill_bench(ctx, M, xdtype=xd, ydtype=f32)
+                                   for M in (512, 2048) for xd in (ctx.torch.float16, f32)]
+        log("mid-sized M (whole calls, weights rotating)")
+        extra["mid_m"] = [midm_bench(ctx, M, N, fmt) for fmt in ("int8", "int8-dyn") for M in (64, 128, 256)
+                          for N in (4096, 12288)]
         log("lm_head and its greedy token")
         extra["lm_head_greedy"] = lm_head_greedy_bench(ctx)
         log("device-resident decode (toy decoder)")
