@@ -449,10 +449,14 @@ def linear_w8a8_argmax(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tens
 
 
 def _greedy_state(module: nn.Module, device: torch.device) -> torch.Tensor:
-    st = module.__dict__.get("_argmax_state")
-    if st is None or st.device != device:
-        st = argmax_state(device)
-        module.__dict__["_argmax_state"] = st
+    """The module's fused-argmax state for the current stream on `device`:
+    calls on one stream run one after another and leave the state zero, so
+    they share it; calls on another stream get their own."""
+    states = module.__dict__.setdefault("_argmax_states", {})
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    st = states.get(key)
+    if st is None:
+        st = states[key] = argmax_state(device)
     return st
 
 

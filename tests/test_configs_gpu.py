@@ -330,12 +330,16 @@ def test_loader_swap_inference_mode_and_dtype_moves(dev):
 # ---------------------------------------------------------------------------
 # lm_head and its greedy token in one pass (model.py:445-447, engine.py:30-31)
 # ---------------------------------------------------------------------------
-def _check_greedy(y, tok, state=None):
+def _check_greedy(y, tok, module=None):
     """tok must be torch.argmax of the logits the same call returned, and
-    the argmax state must be back at zero."""
+    every argmax state of the module (one per stream it ran on) must be back
+    at zero."""
     np.testing.assert_array_equal(tok.cpu().numpy(), torch.argmax(y.cpu(), dim=-1).numpy())
-    if state is not None:
-        assert int(state.cpu().count_nonzero()) == 0
+    if module is not None:
+        states = module.__dict__.get("_argmax_states", {})
+        assert states
+        for st in states.values():
+            assert int(st.cpu().count_nonzero()) == 0
 
 
 @pytest.mark.gpu
@@ -352,7 +356,7 @@ def test_lm_head_greedy_one_pass(dev, fmt, M, K, xd):
     for _ in range(3):  # repeated calls reuse the state the last one left at zero
         y, tok = lm.forward_greedy(x)
         np.testing.assert_array_equal(y.cpu().numpy(), y_plain.cpu().numpy())
-        _check_greedy(y, tok, lm._argmax_state)
+        _check_greedy(y, tok, lm)
     # against the oracle: its logits over the GPU's 32 best columns and sampled
     # ones must put their maximum at the GPU's token
     cand = np.unique(np.concatenate([torch.topk(y, 32, dim=-1).indices.cpu().numpy().ravel(),
@@ -381,16 +385,16 @@ def test_lm_head_greedy_ties_nan_zeros(dev, fmt):
     lm = quant.make_linear(fmt, w)
     y, tok = lm.forward_greedy(x.to(dev))
     assert tok.item() == 3 and y[0, 3].item() == y[0, 151000].item()
-    _check_greedy(y, tok, lm._argmax_state)
+    _check_greedy(y, tok, lm)
     b = torch.zeros(V)
     b[90000] = b[140000] = float("nan")
     lmb = quant.make_linear(fmt, w, b.to(dev))
     y, tok = lmb.forward_greedy(x.to(dev))
     assert tok.item() == 90000
-    _check_greedy(y, tok, lmb._argmax_state)
+    _check_greedy(y, tok, lmb)
     y, tok = lm.forward_greedy(torch.zeros(2, K, device=dev))
     assert tok.tolist() == [0, 0] and float(y.abs().max()) == 0.0
-    _check_greedy(y, tok, lm._argmax_state)
+    _check_greedy(y, tok, lm)
 
 
 @pytest.mark.gpu
@@ -404,7 +408,7 @@ def test_greedy_one_pass_other_shapes(dev, M, N, K):
         x = cpu_x(M, K, 67).to(dev)
         y, tok = lm.forward_greedy(x)
         np.testing.assert_array_equal(y.cpu().numpy(), lm(x).cpu().numpy())
-        _check_greedy(y, tok, lm._argmax_state)
+        _check_greedy(y, tok, lm)
 
 
 @pytest.mark.gpu
@@ -432,9 +436,31 @@ def test_greedy_one_pass_graph_replays(dev):
             x.copy_(cpu_x(1, K, 70 + i).to(dev))
             g.replay()
             torch.cuda.synchronize()
-            _check_greedy(y, tok, lm._argmax_state)
+            _check_greedy(y, tok, lm)
             np.testing.assert_array_equal(y.cpu().numpy(), lm(x).cpu().numpy())
             lm(torch.randn(3, K, device=dev))  # eager work between replays
+
+
+@pytest.mark.gpu
+def test_greedy_one_pass_two_streams(dev):
+    """One lm_head module used on two streams at once: each stream has its own
+    argmax state, so the tokens of both calls are right."""
+    announce("greedy two streams")
+    V, K = 32000, 4096
+    lm = quant.make_linear("int8", gpu_weight(V, K, 71, dev))
+    xs = [cpu_x(1, K, 72 + i).to(dev) for i in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    outs = []
+    for _ in range(3):
+        for st, x in zip(streams, xs):
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                outs.append(lm.forward_greedy(x))
+        torch.cuda.synchronize()
+    for y, tok in outs:
+        _check_greedy(y, tok, lm)
+    assert len(lm.__dict__["_argmax_states"]) >= 2
 
 
 # ---------------------------------------------------------------------------
