@@ -714,7 +714,8 @@ def cpu_baseline(budget_s):
     best = max(sweep, key=sweep.get)
     r = cb.decode_step_baseline(DECODE_SHAPES, 1, best, per, fmt="int8-dyn")
     dyn_gbs = r["bytes_per_step"] / r["seconds_per_step"] / 1e9
-    prefill = [cb.prefill_baseline(M, 12288, 4096, best, per, fmt) for fmt in ("int8", "int8-dyn") for M in (512, 2048)]
+    # prefill GEMMs are large enough to use every core: all host threads there
+    prefill = [cb.prefill_baseline(M, 12288, 4096, host, per, fmt) for fmt in ("int8", "int8-dyn") for M in (512, 2048)]
     torch.set_num_threads(host)
     return {"value": sweep[best], "unit": "GB/s", "cores": best, "kind": "port",
             "sample": (f"int8 block loop of quant.py:46-53 (torch CPU restatement) over the same M=1 decode step "
