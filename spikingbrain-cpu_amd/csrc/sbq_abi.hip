@@ -181,6 +181,10 @@ int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
   if (rc || M == 0) return rc;
   const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
   hipStream_t st = (hipStream_t)stream;
+  if (M > 16 && M <= 64) {  // several 16-row tiles of x against streamed weights
+    const int rc = sbq::launch_gemv_w8_mt(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
+    if (rc != -1) return rc;
+  }
   if (sbq::gemv_supports(M, K, false, x_dtype)) return sbq::launch_gemv_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
   // optional scratch of the prefill GEMM (row sums, staged activations), 256-byte aligned
   void* ws = nullptr;

@@ -460,6 +460,139 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   if (am) argmax_epilogue(a.am_state, a.idx, key, ks, G, M, (unsigned long long*)(xs + xend));
 }
 
+// Weight-only decode GEMV over MT 16-row tiles of x (16 < M <= 16 * MT,
+// fp16 / bf16 activations with 16-byte aligned rows, 64 | K): the fast path's
+// streaming of D weight tiles per step per wave, with MT activation fragments
+// per tile (loaded directly from L2, D steps ahead like the weights).  Each
+// weight tile is converted once and multiplied into MT accumulators; per-wave
+// partials are summed through LDS in wave order, and wave j < G finishes
+// weight tile j for every row tile.  The x bytes each workgroup reads grow
+// with MT (all rows of x against its G weight tiles), so this pays up to
+// M = 64; larger M runs the tiled GEMM.
+template <int XT, int D, int G, int MT>
+__global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_mt_kernel(GemvArgs a, int KW) {
+  static_assert(XT == XT_F16 || XT == XT_BF16, "fp16 / bf16 activations");
+  typedef typename std::conditional<XT == XT_F16, f16x8, bf16x8>::type V;
+  constexpr int EB = 2;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int KS = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, ks = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int M = a.M, Kc = a.Kc;
+  const int nt0 = blockIdx.x * G;
+  const int kbeg = ks * KW;
+  const int cnt = min(KW, Kc - kbeg);  // >= 1: the host sizes KS so that every wave has a tile
+  f32x4* red = (f32x4*)smem;           // [KS][G][MT][64] partial tiles
+
+  // epilogue operands of weight tile `ks` (wave ks < G finishes tile ks)
+  const int nte = min(nt0 + min(ks, G - 1), a.Nt - 1);
+  const int ne = nte * 16 + 4 * g;
+  f32x4 sc = {0.f, 0.f, 0.f, 0.f}, bi = {0.f, 0.f, 0.f, 0.f};
+  if (ks < G) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int nn = min(ne + v, a.N - 1);
+      sc[v] = a.scale[nn];
+      if (a.bias) bi[v] = a.bias[nn];
+    }
+  }
+
+  // first D tiles and fragments (indexes clamped: no load is guarded)
+  const uint8_t* wp[G];
+#pragma unroll
+  for (int j = 0; j < G; ++j) wp[j] = a.packed + ((int64_t)min(nt0 + j, a.Nt - 1) * Kc + kbeg) * 1024 + lane * 16;
+  const uint8_t* xp[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xp[mt] = (const uint8_t*)a.x + (int64_t)min(mt * 16 + r, M - 1) * a.ldx * EB + ((int64_t)kbeg * 64 + g * 16) * EB;
+  u32x4 w[D][G];
+  XRaw<XT> xd[D][MT];
+#pragma unroll
+  for (int p = 0; p < D; ++p) {
+    const int kt = min(p, cnt - 1);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) load_frag<XT>(xd[p][mt], xp[mt] + kt * 64 * EB);
+#pragma unroll
+    for (int j = 0; j < G; ++j) w[p][j] = load_tile_nt(wp[j] + kt * 1024);
+  }
+
+  f32x4 acc[G][MT];
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto step = [&](int p) {
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      V w0, w1;
+      if constexpr (XT == XT_F16)
+        u8x16_to_f16(w[p][j], w0, w1);
+      else
+        u8x16_to_bf16(w[p][j], w0, w1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (XT == XT_F16) {
+          acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w0, xd[p][mt].a, acc[j][mt], 0, 0, 0);
+          acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1, xd[p][mt].b, acc[j][mt], 0, 0, 0);
+        } else {
+          acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xd[p][mt].a, acc[j][mt], 0, 0, 0);
+          acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xd[p][mt].b, acc[j][mt], 0, 0, 0);
+        }
+      }
+    }
+  };
+  int t = 0;
+  for (; t + D < cnt; t += D) {
+#pragma unroll
+    for (int p = 0; p < D; ++p) {
+      step(p);
+      const int kt = min(t + D + p, cnt - 1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) load_frag<XT>(xd[p][mt], xp[mt] + kt * 64 * EB);
+#pragma unroll
+      for (int j = 0; j < G; ++j) w[p][j] = load_tile_nt(wp[j] + kt * 1024);
+      __builtin_amdgcn_sched_barrier(0);  // keep each refill next to the step that freed its registers
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < D; ++p)
+    if (t + p < cnt) step(p);
+
+  // cross-wave sum in wave order; wave j < G finishes weight tile j
+  if (KS > 1) {
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[((ks * G + j) * MT + mt) * 64 + lane] = acc[j][mt];
+    lds_barrier();
+  }
+  const int nt = nt0 + ks;
+  const int n = nt * 16 + 4 * g;
+  if (ks >= G || nt >= a.Nt || n >= a.N) return;
+  const int nvalid = min(4, a.N - n);
+  const bool yvec = (a.flags & kGemvYVec) && nvalid == 4;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    f32x4 s;
+    if (KS > 1) {
+      s = red[(ks * MT + mt) * 64 + lane];
+      for (int i = 1; i < KS; ++i) s += red[((i * G + ks) * MT + mt) * 64 + lane];
+    } else {
+      s = acc[0][mt];  // one wave implies one weight tile (the host keeps KS >= G)
+    }
+    const int m = mt * 16 + r;
+    if (m >= M) continue;
+    f32x4 o;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float out = s[v] * sc[v];
+      if (a.bias) out = out + bi[v];
+      o[v] = out;
+    }
+    store_y4(a.y, a.yt, (int64_t)m * a.ldy + n, o, yvec, nvalid);
+  }
+}
+
 namespace {
 
 // Instances: (D, G, XL).  XL uses LDS-resident x; direct modes keep D
@@ -570,6 +703,42 @@ int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, hipStream_t st)
   a.x = a.seg[0].x;
   a.ldx = a.seg[0].ldx;
   return launch_gemv_fast_cfg(id, ks, a, xt, false, st);
+}
+
+// Weight-only decode over several 16-row tiles of x (gemv_mt_kernel):
+// fp16 / bf16 x with aligned rows, 16 < M <= 64, 64 | K.  -1: not this path.
+// Every workgroup reads all of x, and the launch time grows with the x bytes
+// its grid reads from L2 (MI355X: about 0.13-0.16 us per MB beyond a 2-5 us
+// base), so the path is taken up to 120 MB of them, where it beats the
+// general GEMV (M <= 32) and the tiled GEMM: N = 4096, M = 24 / 33 / 48:
+// 10.4 / 20.1 / 20.1 -> 9.4 / 12.0 / 15.1 us; N = 12288, M = 24 / 32:
+// 28.7 / 30.7 -> 18.3 / 21.1 us (M = 48 and 64 there, 151 and 201 MB, run
+// the GEMM: 25.5 and 26.0 us against 28.7 and 36.7).
+int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st) {
+  if (!(xt == XT_F16 || xt == XT_BF16) || a.M <= 16 || a.M > 64 || a.K != a.Kc * 64 || !(a.flags & kGemvXVec))
+    return -1;
+  const int mt = (a.M + 15) / 16;
+  const bool wide = a.Kc < 128 && a.Nt >= 384;
+  const int G = wide ? 2 : 1;
+  const int64_t x_grid_bytes = (int64_t)a.M * a.K * 2 * ((a.Nt + G - 1) / G);
+  if (x_grid_bytes > ((int64_t)120 << 20)) return -1;
+  int ks = 4;
+  const int KW = (a.Kc + ks - 1) / ks;
+  ks = (a.Kc + KW - 1) / KW;  // every wave gets at least one K tile
+  if (ks < G) return -1;
+  const size_t lds = (size_t)ks * G * mt * 64 * 16;
+  const dim3 grid((unsigned)((a.Nt + G - 1) / G)), block(ks * 64);
+#define SBQ_MT_CASE(XT_, G_, MT_)                                                                \
+  if (xt == XT_ && G == G_ && mt == MT_) {                                                      \
+    hipLaunchKernelGGL((gemv_mt_kernel<XT_, 4, G_, MT_>), grid, block, lds, st, a, KW);         \
+    return check_launch();                                                                      \
+  }
+  SBQ_MT_CASE(XT_F16, 1, 2) SBQ_MT_CASE(XT_F16, 1, 3) SBQ_MT_CASE(XT_F16, 1, 4)
+  SBQ_MT_CASE(XT_F16, 2, 2) SBQ_MT_CASE(XT_F16, 2, 3) SBQ_MT_CASE(XT_F16, 2, 4)
+  SBQ_MT_CASE(XT_BF16, 1, 2) SBQ_MT_CASE(XT_BF16, 1, 3) SBQ_MT_CASE(XT_BF16, 1, 4)
+  SBQ_MT_CASE(XT_BF16, 2, 2) SBQ_MT_CASE(XT_BF16, 2, 3) SBQ_MT_CASE(XT_BF16, 2, 4)
+#undef SBQ_MT_CASE
+  return -1;
 }
 
 // Fast-path choice for a shape (false: the general kernel runs).  Measured on

@@ -720,3 +720,36 @@ def test_grouped_linears_graph_replays(dev):
         torch.cuda.synchronize()
         for o, e in zip(outs, eager):
             assert torch.equal(o, e)
+
+
+# ---------------------------------------------------------------------------
+# decode GEMV over several 16-row tiles of x (16 < M <= 64, weight-only)
+# ---------------------------------------------------------------------------
+MT_CASES = [  # (M, N, K, x dtype): ragged M, narrow / wide (two weight tiles per workgroup) / odd N, short and
+    # long K; each within the path's 120 MB of x reads over the grid
+    (17, 4096, 4096, "f16"), (24, 1000, 4096, "f16"), (32, 6144, 4096, "bf16"), (26, 18820, 4096, "f16"),
+    (18, 4096, 12288, "f16"), (47, 4096, 4096, "bf16"), (64, 6144, 4096, "f16"), (64, 4096, 128, "f16"),
+    (64, 10, 4096, "f16"),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,xd", MT_CASES)
+def test_w8_gemv_row_tiles(dev, M, N, K, xd):
+    """fp16 / bf16 x at 16 < M <= 64: within fp32 summation order of the
+    oracle for exactly representable inputs (fp32 y), one output rounding for
+    2-byte y, with a bias and with strided x rows."""
+    announce(f"w8 gemv row tiles M={M} N={N} K={K} x={xd}")
+    w = gpu_weight(N, K, 960, dev)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(961))
+    lin = quant.Int8Linear(w, b.to(dev))
+    cols = tile_sample(N, 962)
+    q, s = ref_rows(w, cols)
+    x = cpu_x(M, K, 963).to(DT[xd])
+    ref = oracle.int8_linear(x.float().numpy(), q, s, b.numpy()[cols])
+    wide = torch.zeros((M, K + 64), dtype=DT[xd], device=dev)
+    for xg in (x.to(dev), wide[:, :K].copy_(x.to(dev))):  # dense rows; rows 128 bytes apart beyond K
+        y = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N)
+        assert oracle.rel_l2(y.cpu().numpy()[:, cols], ref) <= W8_TOL_EXACT_X
+        yh = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N, torch.float16)
+        np.testing.assert_array_equal(yh.cpu().numpy(), y.half().cpu().numpy())
