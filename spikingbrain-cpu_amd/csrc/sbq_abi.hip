@@ -64,7 +64,10 @@ int linear_w8a8_run(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
                     int64_t ldy, int32_t* acc_out, float2* parts, float* qp, int8_t* xq, uint8_t* split,
                     int64_t split_bytes, hipStream_t st) {
   const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
-  if (sbq::gemv_supports(M, K, true, x_dtype))
+  // 16 < M <= 64 with small enough x: the pre-passes, then the row-tile GEMV on
+  // the s8 rows (inside launch_gemm_w8a8) instead of the general GEMV
+  const bool mt = M > 16 && sbq::gemv_mt_applies(M, ((K + 63) / 64) * 64, N, sbq::XT_S8);
+  if (!mt && sbq::gemv_supports(M, K, true, x_dtype))
     return sbq::launch_gemv_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
                                  parts, st, yv);
   return sbq::launch_gemm_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,

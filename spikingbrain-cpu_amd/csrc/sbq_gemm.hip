@@ -1229,6 +1229,15 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
 #undef SBQ_QUANT_LAUNCH1
   int rc = check_launch();
   if (rc) return rc;
+  if (M > 16 && gemv_mt_applies(M, Kp, N, XT_S8)) {  // small M: the row-tile GEMV on the s8 rows
+    GemvArgs g{};
+    g.x = xq; g.ldx = Kp; g.M = (int)M; g.K = (int)Kp; g.Kc = (int)Kc;
+    g.packed = packed; g.scale = scale; g.bias = bias; g.colsum = colsum;
+    g.N = (int)N; g.Nt = (int)Nt; g.y = y; g.yt = yt; g.ldy = ldy; g.acc_out = acc_out; g.qpbuf = qpbuf;
+    g.flags = kGemvXVec | (yvec ? kGemvYVec : 0);
+    rc = launch_gemv_mt(g, XT_S8, st);
+    if (rc != -1) return rc;
+  }
   a.x = xq; a.ldx = Kp; a.M = (int)M; a.Kc = (int)Kc;
   a.packed = packed; a.scale = scale; a.bias = bias; a.colsum = colsum;
   a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.acc_out = acc_out; a.qpbuf = qpbuf;

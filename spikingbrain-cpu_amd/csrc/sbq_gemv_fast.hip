@@ -460,8 +460,10 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   if (am) argmax_epilogue(a.am_state, a.idx, key, ks, G, M, (unsigned long long*)(xs + xend));
 }
 
-// Weight-only decode GEMV over MT 16-row tiles of x (16 < M <= 16 * MT,
-// fp16 / bf16 activations with 16-byte aligned rows, 64 | K): the fast path's
+// Decode GEMV over MT 16-row tiles of x (16 < M <= 16 * MT, 64 | K, 16-byte
+// aligned rows): weight-only on fp16 / bf16 activations, or int8-dyn (XT_S8)
+// on the s8 rows xq - 128 of the quantize pre-pass with its (s_x, zp) and
+// the GEMM's per-tensor epilogue.  The fast path's
 // streaming of D weight tiles per step per wave, with MT activation fragments
 // per tile (loaded directly from L2, D steps ahead like the weights).  Each
 // weight tile is converted once and multiplied into MT accumulators; per-wave
@@ -471,9 +473,11 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
 // M = 64; larger M runs the tiled GEMM.
 template <int XT, int D, int G, int MT>
 __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_mt_kernel(GemvArgs a, int KW) {
-  static_assert(XT == XT_F16 || XT == XT_BF16, "fp16 / bf16 activations");
+  static_assert(XT == XT_F16 || XT == XT_BF16 || XT == XT_S8, "fp16 / bf16 activations or s8 rows");
+  constexpr bool I8 = XT == XT_S8;
   typedef typename std::conditional<XT == XT_F16, f16x8, bf16x8>::type V;
-  constexpr int EB = 2;
+  typedef typename std::conditional<I8, i32x4, f32x4>::type Acc;
+  constexpr int EB = I8 ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int KS = blockDim.x >> 6;
   const int tid = threadIdx.x, lane = tid & 63, ks = tid >> 6;
@@ -482,18 +486,20 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_mt_kernel(GemvArgs a,
   const int nt0 = blockIdx.x * G;
   const int kbeg = ks * KW;
   const int cnt = min(KW, Kc - kbeg);  // >= 1: the host sizes KS so that every wave has a tile
-  f32x4* red = (f32x4*)smem;           // [KS][G][MT][64] partial tiles
+  Acc* red = (Acc*)smem;               // [KS][G][MT][64] partial tiles
 
   // epilogue operands of weight tile `ks` (wave ks < G finishes tile ks)
   const int nte = min(nt0 + min(ks, G - 1), a.Nt - 1);
   const int ne = nte * 16 + 4 * g;
   f32x4 sc = {0.f, 0.f, 0.f, 0.f}, bi = {0.f, 0.f, 0.f, 0.f};
+  i32x4 cs = {0, 0, 0, 0};
   if (ks < G) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int nn = min(ne + v, a.N - 1);
       sc[v] = a.scale[nn];
       if (a.bias) bi[v] = a.bias[nn];
+      if constexpr (I8) cs[v] = a.colsum[nn];
     }
   }
 
@@ -516,27 +522,35 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_mt_kernel(GemvArgs a,
     for (int j = 0; j < G; ++j) w[p][j] = load_tile_nt(wp[j] + kt * 1024);
   }
 
-  f32x4 acc[G][MT];
+  Acc acc[G][MT];
 #pragma unroll
   for (int j = 0; j < G; ++j)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt) acc[j][mt] = Acc{0, 0, 0, 0};
   auto step = [&](int p) {
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      V w0, w1;
-      if constexpr (XT == XT_F16)
-        u8x16_to_f16(w[p][j], w0, w1);
-      else
-        u8x16_to_bf16(w[p][j], w0, w1);
+      if constexpr (I8) {
+        const i32x4 wf = tile_to_s8(w[p][j]);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        if constexpr (XT == XT_F16) {
-          acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w0, xd[p][mt].a, acc[j][mt], 0, 0, 0);
-          acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1, xd[p][mt].b, acc[j][mt], 0, 0, 0);
-        } else {
-          acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xd[p][mt].a, acc[j][mt], 0, 0, 0);
-          acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xd[p][mt].b, acc[j][mt], 0, 0, 0);
+        for (int mt = 0; mt < MT; ++mt)
+          acc[j][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, __builtin_bit_cast(i32x4, xd[p][mt].v), acc[j][mt], 0,
+                                                             0, 0);
+      } else {
+        V w0, w1;
+        if constexpr (XT == XT_F16)
+          u8x16_to_f16(w[p][j], w0, w1);
+        else
+          u8x16_to_bf16(w[p][j], w0, w1);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          if constexpr (XT == XT_F16) {
+            acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w0, xd[p][mt].a, acc[j][mt], 0, 0, 0);
+            acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(w1, xd[p][mt].b, acc[j][mt], 0, 0, 0);
+          } else {
+            acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, xd[p][mt].a, acc[j][mt], 0, 0, 0);
+            acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, xd[p][mt].b, acc[j][mt], 0, 0, 0);
+          }
         }
       }
     }
@@ -571,9 +585,15 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_mt_kernel(GemvArgs a,
   if (ks >= G || nt >= a.Nt || n >= a.N) return;
   const int nvalid = min(4, a.N - n);
   const bool yvec = (a.flags & kGemvYVec) && nvalid == 4;
+  float sx = 0.0f;
+  int corr = 0;
+  if constexpr (I8) {
+    sx = a.qpbuf[0];
+    corr = 128 - __float_as_int(a.qpbuf[1]);
+  }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    f32x4 s;
+    Acc s;
     if (KS > 1) {
       s = red[(ks * MT + mt) * 64 + lane];
       for (int i = 1; i < KS; ++i) s += red[((i * G + ks) * MT + mt) * 64 + lane];
@@ -585,9 +605,16 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_mt_kernel(GemvArgs a,
     f32x4 o;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      float out = s[v] * sc[v];
-      if (a.bias) out = out + bi[v];
-      o[v] = out;
+      if constexpr (I8) {  // the per-tensor epilogue of the i8 GEMM
+        const int av = s[v] + corr * cs[v];
+        if (a.acc_out && v < nvalid) a.acc_out[(int64_t)m * a.N + n + v] = av;
+        const float mult = sx * sc[v];
+        o[v] = a.bias ? __builtin_fmaf((float)av, mult, bi[v]) : (float)av * mult;
+      } else {
+        float out = s[v] * sc[v];
+        if (a.bias) out = out + bi[v];
+        o[v] = out;
+      }
     }
     store_y4(a.y, a.yt, (int64_t)m * a.ldy + n, o, yvec, nvalid);
   }
@@ -705,23 +732,32 @@ int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, hipStream_t st)
   return launch_gemv_fast_cfg(id, ks, a, xt, false, st);
 }
 
-// Weight-only decode over several 16-row tiles of x (gemv_mt_kernel):
-// fp16 / bf16 x with aligned rows, 16 < M <= 64, 64 | K.  -1: not this path.
-// Every workgroup reads all of x, and the launch time grows with the x bytes
+// Decode over several 16-row tiles of x (gemv_mt_kernel): weight-only on fp16
+// / bf16 x, or int8-dyn on the s8 rows of the quantize pre-pass (xt XT_S8,
+// a.qpbuf and a.colsum set); aligned rows, 16 < M <= 64, 64 | K.  -1: not
+// this path.  Every workgroup reads all of x, and the launch time grows with the x bytes
 // its grid reads from L2 (MI355X: about 0.13-0.16 us per MB beyond a 2-5 us
 // base), so the path is taken up to 120 MB of them, where it beats the
 // general GEMV (M <= 32) and the tiled GEMM: N = 4096, M = 24 / 33 / 48:
 // 10.4 / 20.1 / 20.1 -> 9.4 / 12.0 / 15.1 us; N = 12288, M = 24 / 32:
 // 28.7 / 30.7 -> 18.3 / 21.1 us (M = 48 and 64 there, 151 and 201 MB, run
 // the GEMM: 25.5 and 26.0 us against 28.7 and 36.7).
+bool gemv_mt_applies(int64_t M, int64_t K, int64_t N, int xt) {
+  if (!(xt == XT_F16 || xt == XT_BF16 || xt == XT_S8) || M <= 16 || M > 64 || K % 64 != 0) return false;
+  const int64_t Nt = (N + 15) / 16, Kc = K / 64;
+  const int G = Kc < 128 && Nt >= 384 ? 2 : 1;
+  const int64_t x_grid_bytes = M * K * (xt == XT_S8 ? 1 : 2) * ((Nt + G - 1) / G);
+  // s8 rows: 90 MB (int8-dyn, N = 12288: M = 48 at 75 MB 29.9 -> 27.1 us, M = 64 at
+  // 100 MB 31.4 against 29.8 for the GEMM)
+  return x_grid_bytes <= ((int64_t)(xt == XT_S8 ? 90 : 120) << 20);
+}
+
 int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st) {
-  if (!(xt == XT_F16 || xt == XT_BF16) || a.M <= 16 || a.M > 64 || a.K != a.Kc * 64 || !(a.flags & kGemvXVec))
-    return -1;
+  if (a.K != a.Kc * 64 || !(a.flags & kGemvXVec) || !gemv_mt_applies(a.M, a.K, a.N, xt)) return -1;
+  if (xt == XT_S8 && (!a.qpbuf || !a.colsum)) return -1;
   const int mt = (a.M + 15) / 16;
   const bool wide = a.Kc < 128 && a.Nt >= 384;
   const int G = wide ? 2 : 1;
-  const int64_t x_grid_bytes = (int64_t)a.M * a.K * 2 * ((a.Nt + G - 1) / G);
-  if (x_grid_bytes > ((int64_t)120 << 20)) return -1;
   int ks = 4;
   const int KW = (a.Kc + ks - 1) / ks;
   ks = (a.Kc + KW - 1) / KW;  // every wave gets at least one K tile
@@ -737,6 +773,8 @@ int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st) {
   SBQ_MT_CASE(XT_F16, 2, 2) SBQ_MT_CASE(XT_F16, 2, 3) SBQ_MT_CASE(XT_F16, 2, 4)
   SBQ_MT_CASE(XT_BF16, 1, 2) SBQ_MT_CASE(XT_BF16, 1, 3) SBQ_MT_CASE(XT_BF16, 1, 4)
   SBQ_MT_CASE(XT_BF16, 2, 2) SBQ_MT_CASE(XT_BF16, 2, 3) SBQ_MT_CASE(XT_BF16, 2, 4)
+  SBQ_MT_CASE(XT_S8, 1, 2) SBQ_MT_CASE(XT_S8, 1, 3) SBQ_MT_CASE(XT_S8, 1, 4)
+  SBQ_MT_CASE(XT_S8, 2, 2) SBQ_MT_CASE(XT_S8, 2, 3) SBQ_MT_CASE(XT_S8, 2, 4)
 #undef SBQ_MT_CASE
   return -1;
 }

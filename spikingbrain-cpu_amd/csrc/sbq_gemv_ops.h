@@ -38,6 +38,7 @@ struct GemvArgs {
   const float2* partials;
   int nparts;
   const float* rscale;  // per-token W8A8: s_t [M]
+  const float* qpbuf;   // W8A8 on pre-quantized rows: (s_x, zp bits) from the quantize pre-pass
   int flags;            // kGemvXVec | kGemvYVec | kGemvArgmax
   // greedy token of each row (flags & kGemvArgmax; fp32 y): the argmax state
   // (per-slot keys and counts, zero before the launch and zero again after

@@ -36,7 +36,9 @@ struct GemvArgs;
 struct GemvSeg;
 bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks);
 int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, hipStream_t st);
-// Weight-only decode over several 16-row tiles of x (16 < M <= 64).
+// Decode over several 16-row tiles of x (16 < M <= 64): weight-only on fp16 /
+// bf16 x, or int8-dyn on pre-quantized s8 rows (xt XT_S8).
+bool gemv_mt_applies(int64_t M, int64_t K, int64_t N, int xt);
 int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st);
 int launch_gemv_w8_mt(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                       const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,

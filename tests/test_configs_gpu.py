@@ -753,3 +753,29 @@ def test_w8_gemv_row_tiles(dev, M, N, K, xd):
         assert oracle.rel_l2(y.cpu().numpy()[:, cols], ref) <= W8_TOL_EXACT_X
         yh = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N, torch.float16)
         np.testing.assert_array_equal(yh.cpu().numpy(), y.half().cpu().numpy())
+
+
+MT8_CASES = [  # (M, N, K): int8-dyn on the s8 rows of the quantize pre-pass, within the path's x-read cap
+    (17, 4096, 4096), (32, 1000, 4096), (33, 6144, 4096), (48, 12288, 4096), (64, 4096, 4096), (40, 4096, 192),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", MT8_CASES)
+def test_w8a8_gemv_row_tiles(dev, M, N, K):
+    """int8-dyn at 16 < M <= 64 through the row-tile GEMV: int32 accumulators
+    and outputs bit-exact against the oracle, with and without a bias."""
+    announce(f"w8a8 gemv row tiles M={M} N={N} K={K}")
+    w = gpu_weight(N, K, 970, dev)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(971))
+    rows = np.arange(M)
+    cols = tile_sample(N, 972)
+    q, s = ref_rows(w, cols)
+    x = cpu_x(M, K, 973, outliers=True)
+    for bias in (None, b):
+        lin = quant.DynamicInt8Linear(w, None if bias is None else bias.to(dev))
+        acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+        y = quant.linear_w8a8(x.to(dev), lin.packed, lin.scale, lin.colsum, lin.bias, N, acc_out=acc)
+        acc_ref, y_ref = ref_w8a8(x.numpy(), rows, q, s, None if bias is None else bias.numpy()[cols])
+        np.testing.assert_array_equal(pick(acc, rows, cols).astype(np.int64), acc_ref.astype(np.int64))
+        np.testing.assert_array_equal(pick(y, rows, cols), y_ref)
