@@ -338,11 +338,6 @@ struct GemmArgs {
 // summed through LDS in group order at the end.  Splitting K inside the
 // workgroup multiplies the waves per SIMD (latency hiding) for grids too small
 // to fill the chip, without extra HBM traffic.
-// Occupancy hint: 4 waves per SIMD (128 VGPRs) unless a wave's accumulator
-// tile exceeds 64 x 64 (then 2 waves per SIMD, 256 VGPRs).
-template <int BN, int BM, int WN, int WM>
-constexpr int dl_min_waves() { return (BN / WN) * (BM / WM) > 64 * 64 ? 2 : 4; }
-
 // Bytes of the epilogue operand table: per block column its scale, bias and
 // (W8A8) column sum, per block row its row sum and row scale, and the two
 // activation quantization words.
@@ -364,7 +359,19 @@ constexpr int dl_lds_bytes() {
   const int epb = dl_epi_table_bytes(BN, BM);
   return ldsa + (rsk ? KG * BM * 4 : 0) + (post + epb <= ldsa ? 0 : epb);
 }
-constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950: LDS per workgroup
+constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950: LDS per workgroup (and per CU)
+
+// Occupancy hint (waves per SIMD): what the LDS leaves room for, at most 4
+// (128 VGPRs), or 2 (256 VGPRs) when a wave's accumulator tile exceeds 64 x 64.
+// A workgroup's KG * WN * WM waves spread over the CU's 4 SIMDs, and
+// kMaxLdsBytes / dl_lds_bytes workgroups fit a CU; asking for more waves
+// than the LDS admits would only tighten the register budget.
+template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP, int KT>
+constexpr int dl_min_waves() {
+  const int regs = (BN / WN) * (BM / WM) > 64 * 64 ? 2 : 4;
+  const int lds = kMaxLdsBytes / dl_lds_bytes<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>() * KG * WN * WM / 4;
+  return lds < 1 ? 1 : (lds < regs ? lds : regs);
+}
 
 // RSP (fp16 W-only): the per-row sums of x come precomputed in a.rsum instead
 // of being accumulated in the K loop.
@@ -377,7 +384,7 @@ constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950: LDS per workgroup
 // configurations the split plan uses are built with it: the fixup's registers
 // would otherwise spill in the large-tile configurations).
 template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false, int KT = 1, bool SK = false>
-__global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<BN, BM, WN, WM>())) void gemm_dl_kernel(const GemmArgs a) {
+__global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>())) void gemm_dl_kernel(const GemmArgs a) {
   typedef GemmOp<XT> Op;
   typedef typename Op::V V;
   typedef typename std::conditional<I8, i32x4, f32x4>::type Acc;

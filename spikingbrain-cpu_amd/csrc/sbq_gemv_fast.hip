@@ -160,11 +160,12 @@ __device__ __forceinline__ void argmax_epilogue(uint8_t* state, int64_t* idx, un
                      : 0ull;
 #pragma unroll
   for (int row = 0; row < 16; ++row) {
-    if (row >= M) break;
-    unsigned long long v = k[row];
+    if (row < M) {  // uniform; a break here would keep the loop (and k[]) from unrolling
+      unsigned long long v = k[row];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = umax64(v, __shfl_xor(v, o, 64));
-    if (lane == 0) idx[row] = argmax_key_index(v);
+      for (int o = 32; o > 0; o >>= 1) v = umax64(v, __shfl_xor(v, o, 64));
+      if (lane == 0) idx[row] = argmax_key_index(v);
+    }
   }
   if (lane == 0) __hip_atomic_store(tcount, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
