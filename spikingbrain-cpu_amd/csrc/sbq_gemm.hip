@@ -1048,7 +1048,7 @@ int launch_gemm_dl_cfg(int id, bool i8, int xt, const GemmArgs& a, hipStream_t s
 // 12288, M = 256..4096, N = 2048..24576: the best of 10 (fp16) / 11 (W8A8)
 // configurations, or within 4% of it, at every point.  bf16 W-only keeps
 // 64 x 128 wave tiles on the largest grids (half the conversion work per MFMA).
-int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt) {
+int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc) {
   const int64_t t256 = ((Nt + 15) / 16) * ((M + 127) / 128);
   const int64_t t128x64 = ((Nt + 7) / 8) * ((M + 63) / 64);
   if (i8) {
@@ -1057,7 +1057,12 @@ int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt) {
     if (t256 >= 320) return 19;                                   // 192 x 128
     if (t256 >= 224) return 14;                                   // 128 x 128
     if (t256 >= 160) return 20;                                   // 192 x 64
-    if (t256 >= 80) return 15;                                    // 128 x 64
+    // 128 x 64 also from 64 blocks of 256 x 128 up while K is short: there the
+    // 64 x 64 K-split grid (2 workgroups per CU) overflows its first round
+    // (M = 384, N = 6144: 576 workgroups, 32.2 -> 22.6 us; M = 512, N = 4096:
+    // 22.3 -> 20.5 us), while at K = 12288 the in-workgroup K split wins
+    // (M = 512, N = 4096: 49.6 against 55.5 us)
+    if (t256 >= 80 || (t256 >= 64 && Kc <= 96)) return 15;       // 128 x 64
     return 8;                                                     // 64 x 64, K split over 4 wave groups
   }
   if (xt == XT_F16) {
@@ -1087,7 +1092,7 @@ int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt) {
 // W-only with precomputed row sums (the staged fp32 / bf16 activations
 // included).
 DlPlan plan_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc, bool rsp) {
-  DlPlan p{pick_gemm_dl(i8, xt, M, Nt), 1, 0, 0};
+  DlPlan p{pick_gemm_dl(i8, xt, M, Nt, Kc), 1, 0, 0};
   if (!i8 && !(xt == XT_F16 && rsp)) return p;
   const int64_t tiles = ((Nt + 7) / 8) * ((M + 63) / 64);
   if (tiles >= 192 || M > 128) return p;
@@ -1160,7 +1165,7 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
     const DlPlan plan = plan_gemm_dl(false, gxt, M, Nt, Kc, staged);
     int ncount = 0;
     uint32_t* zero = staged ? attach_split(a, plan, (uint8_t*)ws + l.bytes, ws_bytes - l.bytes, &ncount) : nullptr;
-    const int id = zero || plan.splits == 1 ? plan.id : pick_gemm_dl(false, gxt, M, Nt);
+    const int id = zero || plan.splits == 1 ? plan.id : pick_gemm_dl(false, gxt, M, Nt, Kc);
     if (staged) {
       uint8_t* w = (uint8_t*)ws;
       float* rowsum = (float*)(w + l.rowsum);
@@ -1201,7 +1206,7 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
   const DlPlan plan = plan_gemm_dl(true, XT_F16, M, Nt, Kc, true);
   int ncount = 0;
   uint32_t* zero = attach_split(a, plan, split, split_bytes, &ncount);
-  const int id = zero || plan.splits == 1 ? plan.id : pick_gemm_dl(true, XT_F16, M, Nt);
+  const int id = zero || plan.splits == 1 ? plan.id : pick_gemm_dl(true, XT_F16, M, Nt, Kc);
   const int nparts = minmax_nparts(M, K);
   const int prc = launch_minmax_partials(x, xt, M, K, ldx, partials, nparts, st, zero, ncount);
   if (prc) return prc;
@@ -1281,7 +1286,7 @@ int launch_gemm_w8a8_token(const void* x, int xt, int64_t M, int64_t K, int64_t 
   a.packed = packed; a.scale = scale; a.bias = bias;
   a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.acc_out = acc_out; a.rscale = s_t;
   a.flags = (yvec ? 2 : 0) | 4 | y16_flag(y, yt, ldy);
-  return launch_gemm_dl_cfg(pick_gemm_dl(true, XT_F16, M, Nt), true, XT_F16, a, st);
+  return launch_gemm_dl_cfg(pick_gemm_dl(true, XT_F16, M, Nt, Kc), true, XT_F16, a, st);
 }
 
 }  // namespace sbq

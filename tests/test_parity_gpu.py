@@ -357,11 +357,13 @@ def test_w8a8_bitexact(dev, M, N, K, xd):
 # the output takes (short K keeps the oracle fast): 256x256 blocks with two K
 # tiles per stage (t256 >= 1024) and its one-tile fallback for an odd tile
 # count; 192x128 with three stages (t256 = 768 and 384); 128x128 (256),
-# 192x64 (192) and 128x64 (128) with two K tiles per stage and their odd-count
-# fallbacks; 64x64 with K split over 4 wave groups (64); ragged M and N.
+# 192x64 (192) and 128x64 (128, and 64 or 72 with short K) with two K tiles per
+# stage and their odd-count fallbacks; 64x64 with K split over 4 wave groups
+# (32, and 64 with long K); ragged M and N.
 W8A8_GEMM_CFG = [(2048, 24576, 128), (2048, 24576, 192), (2048, 12288, 128), (1024, 12288, 256), (1024, 8192, 256),
                  (1024, 8192, 320), (512, 12288, 256), (512, 12288, 320), (512, 8192, 256), (512, 8192, 448),
-                 (256, 8192, 448), (1000, 12290, 256), (500, 12300, 192)]
+                 (256, 8192, 448), (384, 6144, 256), (256, 4096, 448), (448, 4096, 6208), (1000, 12290, 256),
+                 (500, 12300, 192)]
 
 
 @pytest.mark.parametrize("M,N,K", W8A8_GEMM_CFG)
