@@ -1048,6 +1048,8 @@ int launch_gemm_dl_cfg(int id, bool i8, int xt, const GemmArgs& a, hipStream_t s
 // 12288, M = 256..4096, N = 2048..24576: the best of 10 (fp16) / 11 (W8A8)
 // configurations, or within 4% of it, at every point.  bf16 W-only keeps
 // 64 x 128 wave tiles on the largest grids (half the conversion work per MFMA).
+constexpr int64_t kCUs = 256;  // MI355X compute units
+
 int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc) {
   const int64_t t256 = ((Nt + 15) / 16) * ((M + 127) / 128);
   const int64_t t128x64 = ((Nt + 7) / 8) * ((M + 63) / 64);
@@ -1063,16 +1065,29 @@ int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc) {
     // 22.3 -> 20.5 us), while at K = 12288 the in-workgroup K split wins
     // (M = 512, N = 4096: 49.6 against 55.5 us)
     if (t256 >= 80 || (t256 >= 64 && Kc <= 96)) return 15;       // 128 x 64
-    return 8;                                                     // 64 x 64, K split over 4 wave groups
+    // 64 x 64, K split over 4 wave groups, while its grid fits one round of two
+    // workgroups per CU (else 128 x 64)
+    return ((Nt + 3) / 4) * ((M + 63) / 64) <= 2 * kCUs ? 8 : 15;
   }
   if (xt == XT_F16) {
     if (t256 >= 448 || (t256 >= 224 && t256 < 320)) return 0;  // 256 x 128
     if (t256 >= 320) return 18;                                 // 192 x 128
     if (t256 >= 160) return 16;                                 // 192 x 64
     if (t256 >= 112) return 3;                                  // 128 x 64
-    if (t256 >= 80) return 17;                                  // 192 x 64, K split over 4 wave groups
-    if (t256 >= 40) return 5;                                   // 128 x 64, K split over 4 wave groups
-    return 8;                                                   // 64 x 64, K split over 4 wave groups
+    // K split over 4 wave groups (one workgroup per CU): 192 x 64 (t256 >= 80),
+    // 128 x 64 (>= 40) or 64 x 64 blocks.  When that grid needs a second round
+    // of the 256 CUs, the largest of the three grids that fits one round runs,
+    // else 128 x 64 blocks without the split (M = 384, N = 6144: 128 x 64 split
+    // 288 workgroups 42.6 us, 192 x 64 split 28.1 us; M = 768, N = 4096: 192 x 64
+    // split 264 workgroups 53.6 us, unsplit 128 x 64 34.7 us)
+    const int64_t rb = (M + 63) / 64;
+    const int64_t g8 = ((Nt + 3) / 4) * rb, g5 = ((Nt + 7) / 8) * rb, g17 = ((Nt + 11) / 12) * rb;
+    const int id = t256 >= 80 ? 17 : (t256 >= 40 ? 5 : 8);
+    if ((id == 17 ? g17 : (id == 5 ? g5 : g8)) <= kCUs) return id;
+    if (g8 <= kCUs) return 8;
+    if (g5 <= kCUs) return 5;
+    if (g17 <= kCUs) return 17;
+    return 3;
   }
   if (t256 >= 1536) return 10;
   if (t256 >= 256 || t128x64 >= 512) return 0;
