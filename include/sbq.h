@@ -164,6 +164,16 @@ int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K, int x_dtype);
  * scratch). */
 int64_t sbq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8);
 
+/* Plan of the tiled prefill GEMM for y [M, N] = x [M, K] * W^T with x of
+ * x_dtype, as sbq_linear_w8 (w8a8 = 0) and sbq_linear_w8a8 (w8a8 = 1) run it
+ * when given sbq_linear_workspace_bytes of workspace: returns the block
+ * configuration id (>= 0) and stores in *splits (if not NULL) the number of
+ * workgroups K is split over.  It describes the calls that reach that GEMM;
+ * small M runs the decode GEMV paths instead.  Host-only: needs no GPU.
+ * SBQ_ERR_ARG / SBQ_ERR_DTYPE for a bad argument.  No counterpart in the
+ * reference (diagnostics and tests of the configuration choice). */
+int sbq_gemm_config(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8, int* splits);
+
 /* ---- int8-dyn W8A8 linear (DynamicInt8Linear.forward, quant.py:63-66) ---- */
 
 /* Workspace bytes sbq_linear_w8a8 / sbq_act_qparams need for an [M, K] input:

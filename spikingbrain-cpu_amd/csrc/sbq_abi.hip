@@ -257,6 +257,17 @@ int64_t sbq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype,
   return base + sbq::split_area_bytes(sbq::plan_gemm_dl(w8a8 != 0, 1, M, Nt, Kc, true));
 }
 
+int sbq_gemm_config(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8, int* splits) {
+  if (!valid_dtype(x_dtype)) return SBQ_ERR_DTYPE;
+  if (M < 1 || N < 1 || K < 1 || M > kIntMax || N > kIntMax || K > kIntMax || (w8a8 != 0 && w8a8 != 1))
+    return SBQ_ERR_ARG;
+  // with that workspace every activation dtype reaches the GEMM as fp16 (W-only:
+  // fp32 / bf16 staged as fp16 planes, row sums precomputed) or s8 (W8A8)
+  const sbq::DlPlan p = sbq::plan_gemm_dl(w8a8 != 0, sbq::XT_F16, M, (N + 15) / 16, (K + 63) / 64, true);
+  if (splits) *splits = p.splits;
+  return p.id;
+}
+
 int sbq_act_qparams(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, float* scale_out,
                     int32_t* zp_out, void* workspace, size_t workspace_bytes, void* stream) {
   if (!valid_dtype(x_dtype)) return SBQ_ERR_DTYPE;

@@ -360,6 +360,7 @@ constexpr int dl_lds_bytes() {
   return ldsa + (rsk ? KG * BM * 4 : 0) + (post + epb <= ldsa ? 0 : epb);
 }
 constexpr int kMaxLdsBytes = 160 * 1024;  // gfx950: LDS per workgroup (and per CU)
+constexpr int kXCDs = 8;                  // MI355X: accelerator complex dies, each with its own L2
 
 // Occupancy hint (waves per SIMD): what the LDS leaves room for, at most 4
 // (128 VGPRs), or 2 (256 VGPRs) when a wave's accumulator tile exceeds 64 x 64.
@@ -434,7 +435,25 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<I8, XT, BN, BM, WN, 
   const int r = lane & 15, g = lane >> 4;
   const int kg = wave / GW, w = __builtin_amdgcn_readfirstlane(wave % GW);  // wave-uniform: LDS targets stay scalar
   const int wn = w / WM, wm = w % WM;
-  const int nt0 = blockIdx.x * WT, m0 = blockIdx.y * BM;
+  // Block order.  Workgroup L = x + gridDim.x * y runs on XCD L % 8, so when
+  // the grid is a multiple of 8 blocks wide every row block of a weight
+  // column block lands on one XCD and shares its L2.  Other widths would
+  // spread each column block over the XCDs (its weights fetched into up to 8
+  // L2s): there each XCD takes a contiguous column-major range of blocks
+  // instead (measured: the fastest configuration 2.4% (fp16) / 4.0% (W8A8)
+  // faster over 31 such shapes, up to 15%; no configuration more than 5% slower).
+  int bx = blockIdx.x, by = blockIdx.y;
+  if constexpr (!SK) {
+    const int gx = gridDim.x;
+    if (gx % kXCDs != 0) {
+      const int gy = gridDim.y, T = gx * gy, L = bx + gx * by;
+      const int q = T / kXCDs, rr = T % kXCDs, xcd = L % kXCDs;
+      const int Lp = (xcd < rr ? xcd * (q + 1) : rr * (q + 1) + (xcd - rr) * q) + L / kXCDs;
+      bx = Lp / gy;
+      by = Lp - bx * gy;
+    }
+  }
+  const int nt0 = bx * WT, m0 = by * BM;
   const int M = a.M, Kc = a.Kc, Nt = a.Nt;
   // stages of activation K tiles: x tile kc meets weight tile kc mod Kc (the
   // host keeps Kc % KT == 0)
@@ -1038,19 +1057,82 @@ int launch_gemm_dl_cfg(int id, bool i8, int xt, const GemmArgs& a, hipStream_t s
   return -2;
 }
 
-// Configuration for a shape, by the number of 256 x 128 blocks the output
-// takes (t256).  A CU's throughput is about the same with one or two
-// workgroups of a configuration, so the kernel time follows the busiest CU's
-// share of the grid: each range below picks the block shape whose grid splits
-// most evenly over the 256 CUs (192-row blocks turn 1.5 blocks per CU into 2,
-// 0.75 into 1), and grids too small for two workgroups per CU split K over 4
-// wave groups inside the workgroup.  Measured on MI355X over K = 4096 and
-// 12288, M = 256..4096, N = 2048..24576: the best of 10 (fp16) / 11 (W8A8)
-// configurations, or within 4% of it, at every point.  bf16 W-only keeps
-// 64 x 128 wave tiles on the largest grids (half the conversion work per MFMA).
 constexpr int64_t kCUs = 256;  // MI355X compute units
 
+// Kernel-time model of one configuration (M > 128): its grid of G workgroups
+// puts B = ceil(G / 256) on the busiest CU, which runs them in rounds of up to
+// `occ` at once (occ: what LDS and registers admit per CU).  A round with j
+// workgroups costs round[j-1] us per 64-wide K tile, and the kernel time is the
+// busiest CU's rounds plus kc * Kc + c0.  The coefficients are least-squares
+// fits (relative error) to GEMM-alone timings of every configuration on
+// MI355X over 255 shapes: M = 192 .. 4096 (17 values) by N = 2048 .. 24576
+// (11 values, 18820 among them) at K = 4096, and by N = 2048 .. 8192 at
+// K = 12288.  Median error of the fitted times: 3.4% (fp16) / 3.5% (W8A8).
+// Picking the smallest predicted time costs 0.1% (fp16) / 0.6% (W8A8) over the
+// sum of those shapes against the fastest configuration of each, worst shape
+// 1.06x / 1.17x (fitted on half of the shapes, it picks the other half within
+// 0.1% / 0.7%).  The t256 ranges it replaced cost 3.4% / 9.2% there, with 17 /
+// 42 shapes beyond 1.2x (W8A8 M = 640, N = 24576: 107.8 -> 64.1 us; fp16
+// M = 1536, N = 8192: 118.4 -> 83.9 us).
+struct PickCost {
+  int id, wt, bm, occ;  // configuration, weight tiles (BN / 16) and rows per block, workgroups per CU
+  float round[4], kc, c0;
+};
+constexpr PickCost kPickF16[] = {
+    {0, 16, 128, 2, {0.8752f, 1.4950f, 0.0f, 0.0f}, -0.1906f, 7.419f},
+    {2, 8, 128, 3, {0.5755f, 0.8307f, 1.2199f, 0.0f}, -0.0736f, 5.284f},
+    {3, 8, 64, 4, {0.4421f, 0.4948f, 0.7084f, 0.9441f}, -0.0194f, 3.905f},
+    {5, 8, 64, 1, {0.3427f, 0.0f, 0.0f, 0.0f}, -0.1125f, 8.834f},
+    {8, 4, 64, 1, {0.2727f, 0.0f, 0.0f, 0.0f}, -0.1025f, 7.759f},
+    {10, 16, 128, 2, {0.9332f, 1.5313f, 0.0f, 0.0f}, -0.1631f, 8.066f},
+    {16, 12, 64, 4, {0.5219f, 0.6684f, 0.9792f, 1.2787f}, -0.0636f, 5.479f},
+    {17, 12, 64, 1, {0.4311f, 0.0f, 0.0f, 0.0f}, -0.1362f, 9.805f},
+    {18, 12, 128, 2, {0.8151f, 1.1780f, 0.0f, 0.0f}, -0.1713f, 8.224f},
+};
+constexpr PickCost kPickI8[] = {
+    {0, 16, 128, 2, {0.6566f, 0.9437f, 0.0f, 0.0f}, -0.1356f, 5.191f},
+    {1, 16, 128, 2, {0.6630f, 0.9696f, 0.0f, 0.0f}, -0.1773f, 7.038f},
+    {2, 8, 128, 4, {0.4266f, 0.5184f, 0.7281f, 1.1083f}, 0.0164f, 1.486f},
+    {3, 8, 64, 4, {0.4108f, 0.5000f, 0.5503f, 0.7116f}, -0.0362f, 0.290f},
+    {8, 4, 64, 2, {0.2242f, 0.2806f, 0.0f, 0.0f}, -0.0666f, 6.374f},
+    {12, 16, 256, 1, {0.9305f, 0.0f, 0.0f, 0.0f}, -0.2353f, 9.484f},
+    {13, 16, 256, 1, {0.9188f, 0.0f, 0.0f, 0.0f}, -0.2204f, 9.060f},
+    {14, 8, 128, 2, {0.3916f, 0.5393f, 0.0f, 0.0f}, -0.0723f, 5.289f},
+    {15, 8, 64, 3, {0.2710f, 0.3348f, 0.5245f, 0.0f}, -0.0161f, 3.097f},
+    {16, 12, 64, 4, {0.4147f, 0.4938f, 0.5822f, 0.9175f}, 0.0121f, 1.729f},
+    {18, 12, 128, 2, {0.6125f, 0.7382f, 0.0f, 0.0f}, -0.1509f, 6.635f},
+    {19, 12, 128, 2, {0.5758f, 0.7368f, 0.0f, 0.0f}, -0.1529f, 7.688f},
+    {20, 12, 64, 2, {0.3710f, 0.4474f, 0.0f, 0.0f}, -0.0664f, 4.588f},
+};
+
+template <int N>
+static int model_pick(const PickCost (&tab)[N], int64_t M, int64_t Nt, int64_t Kc) {
+  int best = tab[0].id;
+  double best_t = 0.0;
+  for (int i = 0; i < N; ++i) {
+    const PickCost& c = tab[i];
+    const int64_t G = ((Nt + c.wt - 1) / c.wt) * ((M + c.bm - 1) / c.bm);
+    const int64_t B = (G + kCUs - 1) / kCUs;  // workgroups on the busiest CU
+    const int64_t full = B / c.occ, rem = B % c.occ;
+    const double k = (double)Kc;
+    const double t = (double)full * c.round[c.occ - 1] * k + (rem ? c.round[rem - 1] * k : 0.0) + c.kc * k + c.c0;
+    if (i == 0 || t < best_t) {
+      best = c.id;
+      best_t = t;
+    }
+  }
+  return best;
+}
+
+// Configuration for a shape.  M > 128 (fp16 W-only, W8A8): the model above.
+// Smaller M, and bf16 W-only, by the number t256 of 256 x 128 blocks the
+// output takes: the block shape whose grid splits most evenly over the 256
+// CUs, and grids too small for two workgroups per CU split K over 4 wave
+// groups inside the workgroup.  bf16 W-only keeps 64 x 128 wave tiles on the
+// largest grids (half the conversion work per MFMA).
 int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc) {
+  if (M > 128 && i8) return model_pick(kPickI8, M, Nt, Kc);
+  if (M > 128 && xt == XT_F16) return model_pick(kPickF16, M, Nt, Kc);
   const int64_t t256 = ((Nt + 15) / 16) * ((M + 127) / 128);
   const int64_t t128x64 = ((Nt + 7) / 8) * ((M + 63) / 64);
   if (i8) {
@@ -1059,11 +1141,8 @@ int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc) {
     if (t256 >= 320) return 19;                                   // 192 x 128
     if (t256 >= 224) return 14;                                   // 128 x 128
     if (t256 >= 160) return 20;                                   // 192 x 64
-    // 128 x 64 also from 64 blocks of 256 x 128 up while K is short: there the
-    // 64 x 64 K-split grid (2 workgroups per CU) overflows its first round
-    // (M = 384, N = 6144: 576 workgroups, 32.2 -> 22.6 us; M = 512, N = 4096:
-    // 22.3 -> 20.5 us), while at K = 12288 the in-workgroup K split wins
-    // (M = 512, N = 4096: 49.6 against 55.5 us)
+    // 128 x 64 also from 64 blocks of 256 x 128 up while K is short (there
+    // the 64 x 64 K-split grid ran slower); long K keeps the in-workgroup split
     if (t256 >= 80 || (t256 >= 64 && Kc <= 96)) return 15;       // 128 x 64
     // 64 x 64, K split over 4 wave groups, while its grid fits one round of two
     // workgroups per CU (else 128 x 64)
@@ -1077,9 +1156,8 @@ int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc) {
     // K split over 4 wave groups (one workgroup per CU): 192 x 64 (t256 >= 80),
     // 128 x 64 (>= 40) or 64 x 64 blocks.  When that grid needs a second round
     // of the 256 CUs, the largest of the three grids that fits one round runs,
-    // else 128 x 64 blocks without the split (M = 384, N = 6144: 128 x 64 split
-    // 288 workgroups 42.6 us, 192 x 64 split 28.1 us; M = 768, N = 4096: 192 x 64
-    // split 264 workgroups 53.6 us, unsplit 128 x 64 34.7 us)
+    // else 128 x 64 blocks without the split (a second round nearly doubled
+    // the time)
     const int64_t rb = (M + 63) / 64;
     const int64_t g8 = ((Nt + 3) / 4) * rb, g5 = ((Nt + 7) / 8) * rb, g17 = ((Nt + 11) / 12) * rb;
     const int id = t256 >= 80 ? 17 : (t256 >= 40 ? 5 : 8);

@@ -278,6 +278,18 @@ def grouped_forward(pairs):
     return [y.reshape(*shape0[:-1], -1) for y in ys]
 
 
+def gemm_config(M: int, N: int, K: int, dtype: torch.dtype = torch.float16, w8a8: bool = False) -> tuple[int, int]:
+    """(configuration id, K splits) of the tiled prefill GEMM for y [M, N] =
+    x [M, K] * W^T as the int8 (w8a8=False) / int8-dyn linears run it with
+    their default workspace (sbq_gemm_config; host-only, needs no GPU)."""
+    L = _lib.load()
+    splits = ctypes.c_int(0)
+    rc = L.sbq_gemm_config(M, N, K, _code(dtype), int(bool(w8a8)), ctypes.byref(splits))
+    if rc < 0:
+        raise ValueError(f"gemm_config: {L.sbq_status_string(rc).decode()} (M={M}, N={N}, K={K})")
+    return rc, splits.value
+
+
 def w8a8_workspace(M: int, K: int, device: torch.device, N: int | None = None,
                    dtype: torch.dtype = torch.float16) -> torch.Tensor:
     """Scratch for the int8-dyn paths; with N, also the split-K partials of

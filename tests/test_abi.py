@@ -132,3 +132,36 @@ def test_python_binding_maps_status_to_exceptions():
         _lib.check(-2, "x")
     with pytest.raises(_lib.SbqError, match="launch failed"):
         _lib.check(-5, "x")
+
+
+# Prefill GEMM configuration choices (host-only, no GPU): M > 128 runs the
+# fitted kernel-time model, M <= 128 the grid rules with K split over
+# workgroups for small grids.  One shape per configuration the picker uses;
+# the GPU tests run these same shapes against the oracle.
+PICKS_W8 = [(264, 19648, 4096, 0), (648, 10816, 4096, 2), (136, 16384, 4096, 3), (136, 5504, 4096, 5),
+            (136, 256, 4096, 8), (136, 21824, 4096, 16), (136, 10944, 4096, 17), (392, 20992, 4096, 18),
+            (2048, 12288, 4096, 0), (512, 12288, 4096, 16), (8192, 12288, 4096, 0)]
+PICKS_W8A8 = [(520, 21824, 4096, 0), (648, 16384, 4096, 2), (328, 16384, 4096, 3), (136, 256, 4096, 8),
+              (1536, 8192, 12288, 12), (520, 19648, 4096, 13), (264, 19648, 4096, 14), (136, 5504, 4096, 15),
+              (264, 21824, 4096, 16), (392, 20992, 4096, 18), (648, 22336, 4096, 19), (136, 21824, 4096, 20),
+              (2048, 12288, 4096, 18), (512, 12288, 4096, 20)]
+
+
+@pytest.mark.parametrize("w8a8,cases", [(0, PICKS_W8), (1, PICKS_W8A8)])
+def test_gemm_config_picks(lib, w8a8, cases):
+    splits = ctypes.c_int(-1)
+    for M, N, K, cfg in cases:
+        for dt in (0, 1, 2):  # every activation dtype reaches the GEMM as fp16 / s8
+            assert lib.sbq_gemm_config(M, N, K, dt, w8a8, ctypes.byref(splits)) == cfg, (M, N, K, dt)
+            assert splits.value == 1
+
+
+def test_gemm_config_split_plans_and_errors(lib):
+    splits = ctypes.c_int(-1)
+    assert lib.sbq_gemm_config(128, 4096, 4096, 1, 1, ctypes.byref(splits)) == 15 and splits.value == 4
+    assert lib.sbq_gemm_config(128, 4096, 4096, 1, 0, ctypes.byref(splits)) == 3 and splits.value == 4
+    assert lib.sbq_gemm_config(128, 4096, 1024, 1, 1, None) == 8  # too few K steps to split; splits may be NULL
+    assert lib.sbq_gemm_config(0, 4096, 4096, 1, 0, None) == -1
+    assert lib.sbq_gemm_config(128, 0, 4096, 1, 0, None) == -1
+    assert lib.sbq_gemm_config(128, 4096, 4096, 1, 2, None) == -1
+    assert lib.sbq_gemm_config(128, 4096, 4096, 7, 0, None) == -2
