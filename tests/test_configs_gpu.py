@@ -218,6 +218,52 @@ def test_w8a8_gemm_picked_configs(dev, M, N, K, cfg):
     np.testing.assert_array_equal(pick(y, rows, cols), y_ref)
 
 
+def _random_prefill_cases(n, seed):
+    """Seeded prefill shapes at the model's K (4096, 12288, and 4032 for an odd
+    K-tile count): M 129..2048, ragged N (most grids then not a multiple of 8
+    blocks wide), every activation dtype, with and without a bias."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        K = int(rng.choice([4032, 4096, 4096, 12288]))
+        N = int(rng.integers(2048, 8193 if K == 12288 else 24577))
+        out.append((i, int(rng.integers(129, 2049)), N, K, str(rng.choice(["f16", "bf16", "f32"])), bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i,M,N,K,xd,has_bias", _random_prefill_cases(20, 2027))
+def test_random_prefill_picks_match_oracle(dev, i, M, N, K, xd, has_bias):
+    """Whatever configuration and block order the library picks for the shape:
+    W-only within the GEMM's fp16 bar (fp16 / bf16 inputs) or 1e-3 (fp32), W8A8
+    acc and y bit-exact, on sampled rows and output channels."""
+    cfg8, _ = quant.gemm_config(M, N, K, DT[xd])
+    cfg88, _ = quant.gemm_config(M, N, K, DT[xd], w8a8=True)
+    announce(f"random prefill pick {i}: M={M} N={N} K={K} x={xd} bias={has_bias} configs {cfg8} / {cfg88}")
+    w = gpu_weight(N, K, 1300 + i, dev)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(1400 + i)) if has_bias else None
+    bd = None if b is None else b.to(dev)
+    lin = quant.Int8Linear(w, bd)
+    dyn = quant.DynamicInt8Linear(w, bd)
+    cols = tile_sample(N, 1500 + i, cap=96)
+    q, s = ref_rows(w, cols)
+    del w
+    x = cpu_x(M, K, 1600 + i, outliers=True).to(DT[xd])
+    xv = x.float().numpy()
+    xg = x.to(dev)
+    rows = tile_sample(M, 1700 + i)
+    bc = None if b is None else b.numpy()[cols]
+    y = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N)
+    ref = oracle.int8_linear(xv[rows], q, s, bc)
+    assert oracle.rel_l2(pick(y, rows, cols), ref) <= (W8_TOL if xd == "f32" else W8_TOL_GEMM_F16)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y8 = quant.linear_w8a8(xg, dyn.packed, dyn.scale, dyn.colsum, dyn.bias, N, acc_out=acc)
+    acc_ref, y_ref = ref_w8a8(xv, rows, q, s, bc)
+    r_, c_ = torch.from_numpy(rows).to(dev), torch.from_numpy(cols).to(dev)
+    np.testing.assert_array_equal(acc[r_][:, c_].cpu().numpy(), acc_ref)
+    np.testing.assert_array_equal(pick(y8, rows, cols), y_ref)
+
+
 # ---------------------------------------------------------------------------
 # the fused hybrid "reads-x" group (N = 18820)
 # ---------------------------------------------------------------------------
