@@ -445,12 +445,12 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<I8, XT, BN, BM, WN, 
   int bx = blockIdx.x, by = blockIdx.y;
   if constexpr (!SK) {
     const int gx = gridDim.x;
-    if (gx % kXCDs != 0) {
-      const int gy = gridDim.y, T = gx * gy, L = bx + gx * by;
-      const int q = T / kXCDs, rr = T % kXCDs, xcd = L % kXCDs;
-      const int Lp = (xcd < rr ? xcd * (q + 1) : rr * (q + 1) + (xcd - rr) * q) + L / kXCDs;
-      bx = Lp / gy;
-      by = Lp - bx * gy;
+    if (gx % kXCDs != 0) {  // 64-bit: gx * gridDim.y need not fit an int
+      const int64_t gy = gridDim.y, T = gx * gy, L = bx + gx * (int64_t)by;
+      const int64_t q = T / kXCDs, rr = T % kXCDs, xcd = L % kXCDs;
+      const int64_t Lp = (xcd < rr ? xcd * (q + 1) : rr * (q + 1) + (xcd - rr) * q) + L / kXCDs;
+      bx = (int)(Lp / gy);
+      by = (int)(Lp - bx * gy);
     }
   }
   const int nt0 = bx * WT, m0 = by * BM;

@@ -44,6 +44,21 @@ def test_library_picks_are_the_model_argmin(lib, fmt):
         assert got == fit.pick(fmt, coef, r["M"], r["N"], r["K"]), r
 
 
+@pytest.mark.parametrize("fmt,bar", [("w8", 1.01), ("w8a8", 1.03)])
+def test_library_picks_on_held_out_checkpoint_shapes(lib, fmt, bar):
+    """The real checkpoint's prefill projections (hidden 2560, FFN 9728; K = 128,
+    2560, 4096, 9728; M = 137 .. 512, the reference's prompt chunk, and lm_head
+    at M = 512), timed on MI355X and not used in the fit."""
+    _, rows = fit.load(TUNE / f"sweep_mi355x_checkpoint_{fmt}.jsonl")
+    assert len(rows) == 37
+    picked = best = 0.0
+    for r in rows:
+        t = {int(k): v for k, v in r["t"].items()}
+        picked += t[lib.sbq_gemm_config(r["M"], r["N"], r["K"], 1, int(fmt == "w8a8"), None)]
+        best += min(t.values())
+    assert picked / best < bar, picked / best
+
+
 def test_occupancy_matches_the_kernel_lds_model():
     # two worked cases of dl_lds_bytes: 192x128 fp16 (two 28 KiB stages; the
     # 52 KiB output tile and the operand table fit in them) and 256x256 W8A8
