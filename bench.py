@@ -12,7 +12,8 @@ graph holding one step per weight copy.
 
 Also reported (``extra``): M=4/16 decode, the 4096x4096 single GEMV (fp32 and
 fp16 activations), the prefill GEMM at M=512/2048/8192 (N=12288, K=4096,
-TFLOP/s vs the 2.5 PFLOP/s dense fp16 peak), int8-dyn at M=1/128/2048, and
+TFLOP/s vs the 2.5 PFLOP/s dense fp16 peak), int8-dyn at M=1/128/512/2048
+(and the opt-in per-token symmetric scheme at M=1/128/2048), and
 one decode step through all 539 linears of a random-init 36-layer hybrid
 model (hidden 4096, FFN 12288, vocab 151936) at M=1 and M=8, unfused and with
 the layers that read the same input fused (223 launches, same weight bytes).
@@ -335,7 +336,10 @@ def midm_bench(ctx, M, N, fmt, K=4096, steps=20, warmup=5):
             "GBps": gemv_bytes(M, N, K) / (ms * 1e-3) / 1e9}
 
 
-def w8a8_bench(ctx, M, N, K=4096, steps=20, warmup=5):
+def w8a8_bench(ctx, M, N, K=4096, steps=20, warmup=5, token=False):
+    """int8-dyn linear, whole call (activation quantization included): fbgemm's
+    per-tensor asymmetric scheme, or with token=True the opt-in per-token
+    symmetric one (row quantizer, then the s8 GEMV / GEMM)."""
     torch, quant = ctx.torch, ctx.quant
     wbytes = N * K
     # decode sizes rotate weight copies (HBM-bound); prefill sizes reuse one copy, 5 steps per graph replay
@@ -347,7 +351,10 @@ def w8a8_bench(ctx, M, N, K=4096, steps=20, warmup=5):
     ws = quant.w8a8_workspace(M, K, ctx.dev, N)
     def step(c):
         L = layers[c % ncopy]
-        quant.linear_w8a8(x, L[0], L[1], L[2], None, N, torch.float16, workspace=ws, out=y)
+        if token:
+            quant.linear_w8a8_token(x, L[0], L[1], None, N, torch.float16, workspace=ws, out=y)
+        else:
+            quant.linear_w8a8(x, L[0], L[1], L[2], None, N, torch.float16, workspace=ws, out=y)
 
     ms = ctx.time_steps(step, copies, max(steps, copies), warmup)
     res = {"M": M, "N": N, "K": K, "ms": ms}
@@ -793,6 +800,8 @@ def main():
     if args.only:
         fn = {"lm_head_greedy": lm_head_greedy_bench, "device_state": device_state_bench,
               "stack_fused": lambda ctx: stack_bench(ctx, fused=True),
+              "w8a8_token": lambda ctx: [w8a8_bench(ctx, M, N, token=True) for M in (1, 128, 2048)
+                                         for N in (4096, 12288)],
               "mid_m": lambda ctx: [midm_bench(ctx, M, N, fmt) for fmt in ("int8", "int8-dyn") for M in (64, 128, 256)
                                     for N in (4096, 12288)],
               "prefill_fp32_y": lambda ctx: [prefill_bench(ctx, M, xdtype=xd, ydtype=ctx.torch.float32)
@@ -836,6 +845,8 @@ def main():
         extra["device_state"] = device_state_bench(ctx)
         log("int8-dyn")
         extra["w8a8"] = [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)]
+        log("int8-dyn, per-token symmetric activations (opt-in)")
+        extra["w8a8_token"] = [w8a8_bench(ctx, M, N, token=True) for M in (1, 128, 2048) for N in (4096, 12288)]
         log("36-layer linear stack")
         extra["stack"] = stack_bench(ctx)
         log("36-layer linear stack, layers reading the same input fused")
