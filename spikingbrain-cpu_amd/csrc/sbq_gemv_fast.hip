@@ -807,7 +807,10 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     *id = wide1 ? 6 : (xl ? 0 : (Kc >= 128 ? 3 : (Nt >= 384 ? 4 : 2)));
     *ks = wide1 ? 8 : 4;
   } else if (M <= 8) {
-    const bool wide = Kc < 128 && Nt >= 384;
+    // two row tiles per workgroup for wide layers; weight-only also from 257
+    // row tiles, where one tile per workgroup needs a second round of the 256
+    // CUs (M = 1, N = 5120, K = 4096: 7.06 -> 5.87 us)
+    const bool wide = Kc < 128 && (Nt >= 384 || (!w8a8 && Nt > 256));
     *id = wide ? 4 : 3;  // D=4, G=2 | D=8, G=1
     *ks = 4;
     if (!w8a8) {

@@ -271,9 +271,11 @@ def test_w8_bias_and_strided_input(dev):
 
 FAST_CASES = [
     # decode fast path (M <= 16, K % 64 == 0, aligned rows): odd tile counts
-    # with two row tiles per wave, ragged N, M on both sides of 4, long K
+    # with two row tiles per wave, ragged N, M on both sides of 4, long K;
+    # 257..383 row tiles, which take two row tiles per wave for weight-only
+    # (the checkpoint's grouped 2 x 2560 x 4096 output projections among them)
     (1, 6152, 4096), (3, 6160, 4096), (5, 6144, 4096), (8, 4100, 12288), (16, 6152, 2560), (2, 24, 64),
-    (1, 4, 128),
+    (1, 4, 128), (1, 5120, 4096), (4, 4610, 2560), (7, 6100, 4096),
 ]
 
 
