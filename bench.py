@@ -16,7 +16,9 @@ TFLOP/s vs the 2.5 PFLOP/s dense fp16 peak), int8-dyn at M=1/128/512/2048
 (and the opt-in per-token symmetric scheme at M=1/128/2048), and
 one decode step through all 539 linears of a random-init 36-layer hybrid
 model (hidden 4096, FFN 12288, vocab 151936) at M=1 and M=8, unfused and with
-the layers that read the same input fused (223 launches, same weight bytes).
+the layers that read the same input fused (223 launches, same weight bytes),
+and fused and grouped (171 launches) at this model's and at the real
+checkpoint's sizes (hidden 2560, FFN 9728).
 
 ``roofline`` covers the dominant kernel (the gate+up GEMV launch): its average
 duration is measured with HIP events around a graph of back-to-back launches
@@ -394,14 +396,14 @@ def hybrid_stack_shapes(H=4096, F=12288, heads=32, kv_heads=8, d=128, routers=4,
     return shapes
 
 
-def grouped_stack_launches(H=4096, heads=32, d=128):
+def grouped_stack_launches(H=4096, F=12288, heads=32, d=128):
     """The fused stack's launches with the independent pairs of each hybrid
     layer grouped (sbq_linear_w8_grouped): lora_q[1] + lora_k[1] (two inputs
     of K = 128) and sse_o + swa_o (two attention outputs of K = 4096).  Each
     launch is a list of (N, K); the weight bytes are the fused stack's."""
     pair_lora = [(heads * d, d), (heads * d, d)]
     pair_o = [(H, heads * d), (H, heads * d)]
-    shapes = hybrid_stack_shapes(fused=True)
+    shapes = hybrid_stack_shapes(H=H, F=F, fused=True)
     out, i = [], 0
     while i < len(shapes):
         if shapes[i:i + 2] == pair_lora or shapes[i:i + 2] == pair_o:
@@ -413,9 +415,13 @@ def grouped_stack_launches(H=4096, heads=32, d=128):
     return out
 
 
-def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False):
+def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, H=4096, F=12288):
+    """One decode step through every quantized linear of the 36-layer hybrid
+    model (hidden H, FFN F; H=2560, F=9728 is the reference's real checkpoint),
+    one launch per linear, or fused / fused and grouped."""
     torch, quant = ctx.torch, ctx.quant
-    launches = grouped_stack_launches() if grouped else [[sh] for sh in hybrid_stack_shapes(fused=fused)]
+    launches = (grouped_stack_launches(H=H, F=F) if grouped
+                else [[sh] for sh in hybrid_stack_shapes(H=H, F=F, fused=fused)])
     shapes = [sh for grp in launches for sh in grp]
     layers = [ctx.weights(N, K, 2000 + i) for i, (N, K) in enumerate(shapes)]
     wbytes = sum(N * K for N, K in shapes)
@@ -807,6 +813,7 @@ def main():
               "prefill_fp32_y": lambda ctx: [prefill_bench(ctx, M, xdtype=xd, ydtype=ctx.torch.float32)
                                              for M in (512, 2048) for xd in (ctx.torch.float16, ctx.torch.float32)],
               "stack_grouped": lambda ctx: stack_bench(ctx, grouped=True),
+              "stack_checkpoint_grouped": lambda ctx: stack_bench(ctx, grouped=True, H=2560, F=9728),
               "cpu_baseline": lambda ctx: cpu_baseline(args.cpu_budget)}[args.only]
         print(json.dumps({args.only: fn(ctx)}), flush=True)
         return
@@ -853,6 +860,8 @@ def main():
         extra["stack_fused"] = stack_bench(ctx, fused=True)
         log("36-layer linear stack, fused, independent pairs grouped")
         extra["stack_grouped"] = stack_bench(ctx, grouped=True)
+        log("decode step of the real checkpoint's shapes (hidden 2560, FFN 9728), fused and grouped")
+        extra["stack_checkpoint_grouped"] = stack_bench(ctx, grouped=True, H=2560, F=9728)
         torch.cuda.empty_cache()
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
