@@ -415,7 +415,7 @@ def grouped_stack_launches(H=4096, F=12288, heads=32, d=128):
     return out
 
 
-def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, H=4096, F=12288):
+def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, H=4096, F=12288, xdtype=None):
     """One decode step through every quantized linear of the 36-layer hybrid
     model (hidden H, FFN F; H=2560, F=9728 is the reference's real checkpoint),
     one launch per linear, or fused / fused and grouped."""
@@ -430,7 +430,7 @@ def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, 
         xs = {}
         for N, K in shapes:
             if K not in xs:
-                xs[K] = [ctx.act(M, K, 3000 + K), ctx.act(M, K, 3500 + K)]  # a grouped pair reads two inputs
+                xs[K] = [ctx.act(M, K, 3000 + K, xdtype), ctx.act(M, K, 3500 + K, xdtype)]  # a grouped pair reads two inputs
         ys = [torch.empty((M, N), dtype=torch.float16, device=ctx.dev) for N, K in shapes]
         plan, j = [], 0
         for grp in launches:
@@ -814,6 +814,8 @@ def main():
                                              for M in (512, 2048) for xd in (ctx.torch.float16, ctx.torch.float32)],
               "stack_grouped": lambda ctx: stack_bench(ctx, grouped=True),
               "stack_checkpoint_grouped": lambda ctx: stack_bench(ctx, grouped=True, H=2560, F=9728),
+              "stack_checkpoint_grouped_f32x": lambda ctx: stack_bench(ctx, grouped=True, H=2560, F=9728,
+                                                                       xdtype=ctx.torch.float32),
               "cpu_baseline": lambda ctx: cpu_baseline(args.cpu_budget)}[args.only]
         print(json.dumps({args.only: fn(ctx)}), flush=True)
         return
