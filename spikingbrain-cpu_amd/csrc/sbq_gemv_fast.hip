@@ -21,6 +21,9 @@
 //        reads fragments from LDS on use;
 //   direct  each lane loads its 16-element fragment of row min(r, M-1) per
 //        tile from global memory (L2-resident) next to the weight tile.
+// fp32 x in XL mode (weight-only, M <= 8) is split once, after the copy, into
+// bf16 high and remainder planes in LDS; MFMA columns 0..7 multiply the high
+// planes, columns 8..15 the remainders, and the epilogue adds the pairs.
 // Lanes of rows >= M compute on a duplicate row and never store.
 //
 // Per-wave partial tiles are summed through LDS in wave order 0..KS-1 by wave
@@ -44,6 +47,7 @@ constexpr int kFastMaxWaves = 8;
 constexpr int kFusedChunks = 8;         // QM 2: 16-byte chunks of x per thread (at most)
 constexpr int kFusedMinWaves = 4;       // QM 2: x <= kFusedChunks * 16 * 64 * waves bytes
 constexpr int kFastSplitBytes = 49152;  // fp32 x split into bf16 planes in LDS up to this size
+constexpr int kSplitChunks = 12;        // fp32 x split: 16-byte chunks of x per thread (at most)
 
 __device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
@@ -222,8 +226,12 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   uint8_t* xs = smem + red_bytes<G>(KS) + mm_bytes();
   const int xrow = K * EB;  // bytes of one x row in LDS
   constexpr bool kSplitX = XL && XT == XT_F32 && !W8A8;
-  uint8_t* xhi = xs + xch * (int)blockDim.x * 16;  // kSplitX: bf16 planes [M][K] after the raw copy
+  uint8_t* xhi = xs + xch * (int)blockDim.x * 16;  // kSplitX: bf16 planes [M][K] after the x copy
   uint8_t* xlo = xhi + M * K * 2;
+  // kSplitX (M <= 8): MFMA column r < 8 multiplies the high plane of row r,
+  // column r + 8 the remainder plane of the same row; the epilogue adds the
+  // two columns
+  const uint8_t* xpl = (r < 8 ? xhi : xlo) + min(r & 7, M - 1) * K * 2 + g * 16 * 2;
   // end of the x copy and planes: the fused argmax keeps G * 16 keys there
   const int xend = (XL ? xch * (int)blockDim.x * 16 : 0) + (kSplitX ? M * K * 4 : 0);
 
@@ -315,23 +323,37 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       if (lane == 0) mmx[ks] = make_float2(mn, mx);
     }
     if constexpr (XL) wait_vm<D * G>();  // this wave's x copies are in LDS; weights stay in flight
-    lds_barrier();
+    if constexpr (!kSplitX) lds_barrier();  // (kSplitX: each thread first reads back only its own copies)
     if constexpr (kSplitX) {
-      // fp32 x: split once into bf16 high / remainder planes (the per-tile
-      // split would cost ~48 VALU per lane per tile)
-      const int nel = M * K;
-      for (int e = tid * 4; e < nel; e += (int)blockDim.x * 4) {
-        const f32x4 v = *(const f32x4*)(xs + e * 4);
-        bf16x4 h, l;
+      // fp32 x: split once into bf16 high / remainder planes (hi + lo holds 16
+      // significant bits of each activation, at fp32's exponent range).  Each
+      // thread splits the chunks it copied itself (c = tid + i * T), reading
+      // them back four at a time with the reads issued together.
+      const f32x4* raw = (const f32x4*)xs;
+      const int T = blockDim.x, xnch = M * (K / 4), last = xch * T - 1;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          __bf16 hh, ll;
-          split_bf16(v[j], hh, ll);
-          h[j] = hh;
-          l[j] = ll;
+      for (int b = 0; b < kSplitChunks; b += 4) {
+        if (b * T < xnch) {  // uniform
+          f32x4 v[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = raw[min(tid + (b + j) * T, last)];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int c = tid + (b + j) * T;
+            if (c < xnch) {
+              bf16x4 h, l;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                __bf16 hh, ll;
+                split_bf16(v[j][e], hh, ll);
+                h[e] = hh;
+                l[e] = ll;
+              }
+              *(bf16x4*)(xhi + c * 8) = h;  // element 4c of the [M][K] plane
+              *(bf16x4*)(xlo + c * 8) = l;
+            }
+          }
         }
-        *(bf16x4*)(xhi + e * 2) = h;
-        *(bf16x4*)(xlo + e * 2) = l;
       }
       lds_barrier();
     }
@@ -352,18 +374,14 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   const uint8_t* xl = xs + mr * xrow + g * 16 * EB;
   auto step = [&](int p, int kt) {  // kt: tile index within this wave's range
     if constexpr (kSplitX) {
-      const int e = mr * K + (kbeg + kt) * 64 + g * 16;
-      const bf16x8 h0 = *(const bf16x8*)(xhi + e * 2), h1 = *(const bf16x8*)(xhi + e * 2 + 16);
-      const bf16x8 l0 = *(const bf16x8*)(xlo + e * 2), l1 = *(const bf16x8*)(xlo + e * 2 + 16);
+      const uint8_t* e = xpl + (kbeg + kt) * 64 * 2;
+      const bf16x8 v0 = *(const bf16x8*)e, v1 = *(const bf16x8*)(e + 16);
 #pragma unroll
       for (int j = 0; j < G; ++j) {
         bf16x8 w0, w1;
         u8x16_to_bf16(w[p][j], w0, w1);
-        // same order as tile_mma<XT_F32>: remainder first, then the high part
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, l0, acc[j], 0, 0, 0);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, l1, acc[j], 0, 0, 0);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, h0, acc[j], 0, 0, 0);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, h1, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, v0, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, v1, acc[j], 0, 0, 0);
       }
       return;
     }
@@ -413,10 +431,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   const bool am = a.flags & kGemvArgmax;
   const int nt = nt0 + ks;
   const int n = nt * 16 + 4 * g;
-  const bool live = ks < G && r < M && nt < a.Nt && n < a.N;
-  if (!live && !am) return;
-  unsigned long long key = 0;
-  if (live) {
+  const auto tile_sum = [&]() {
     Acc s;
     if (KS > 1) {
       s = red[ks * 64 + lane];
@@ -424,6 +439,21 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
     } else {
       s = acc[0];  // one wave implies one row tile (the host keeps KS >= G)
     }
+    return s;
+  };
+  Acc s{};
+  if constexpr (kSplitX) {
+    if (ks < G) {  // whole waves: column r + 8 (remainder plane) into column r
+      s = tile_sum();
+#pragma unroll
+      for (int v = 0; v < 4; ++v) s[v] += __shfl_down(s[v], 8, 64);
+    }
+  }
+  const bool live = ks < G && r < M && nt < a.Nt && n < a.N;
+  if (!live && !am) return;
+  unsigned long long key = 0;
+  if (live) {
+    if constexpr (!kSplitX) s = tile_sum();
     const int nvalid = min(4, a.N - n);
     f32x4 o;
     if constexpr (PT) {
@@ -683,13 +713,15 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   if (w8a8 && ks * 64 < a.nparts) return -1;  // one min/max partial per thread
   const int eb = xt == XT_F32 ? 4 : 2;
   const int64_t xbytes = (int64_t)a.M * a.K * eb;
-  const bool split = c.XL && xt == XT_F32 && !w8a8;  // fp32 x: raw copy + bf16 planes
+  const bool split = c.XL && xt == XT_F32 && !w8a8;  // fp32 x: raw copy + fp16 planes
   if (c.XL && xbytes > (split ? kFastSplitBytes : kFastXLdsBytes)) return -1;
+  if (split && a.M > 8) return -1;  // the two planes of a row share the 16 MFMA columns
   if (c.D * c.G > 32) return -1;
   const int T = ks * 64;
   const int xch = c.XL ? (int)((xbytes / 16 + T - 1) / T) : 0;
+  if (split && xch > kSplitChunks) return -1;  // the chunks of x each thread splits
   size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
-  if (split) lds += (size_t)a.M * a.K * 4;  // bf16 high / remainder planes
+  if (split) lds += (size_t)xbytes;  // bf16 high / remainder planes
   if (a.flags & kGemvArgmax) lds += (size_t)c.G * 16 * 8;  // the fused argmax's keys per row tile
   const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
   if (qm == 2 && (xbytes > (int64_t)kFusedChunks * 16 * T || ks < kFusedMinWaves)) return -1;
@@ -786,26 +818,37 @@ int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st) {
 // 8-tile steps over one row tile for long K or narrow N, two waves per row tile
 // once M > 8 (the activation fragments then dominate the registers).  bf16
 // activations follow the fp16 rules; fp32 activations are copied to LDS and
-// split once into bf16 high / remainder planes when x fits, and otherwise take
+// split once into row-scaled fp16 high / remainder planes when x fits, and otherwise take
 // direct steps with two row tiles per wave on wide layers (M = 4, N = 6144 and
 // 24576: 21-28% faster than one row tile).
 bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks) {
   if (M < 1 || M > 16 || K % 64 != 0 || !xvec) return false;
   const int64_t Kc = K / 64, Nt = (N + 15) / 16;
   if (xt == XT_F32) {
-    // x in LDS (weight-only: split once into bf16 planes) when it fits 24 KiB,
-    // or 48 KiB for one row (M = 1, K = 12288: 16% faster than direct steps;
-    // the raw copy and the planes then hold 96 KiB of LDS, one workgroup per
-    // CU); one row of a wide layer takes 4-tile steps over two row tiles per
-    // wave (half the copies and splits: QKV and gate+up 2-6% faster) with 8
-    // waves per workgroup.  Else direct steps: 8 tiles over
-    // one row tile for long K, 4 tiles over two row tiles for wide layers, 4
-    // tiles over one row tile otherwise.
+    // x in LDS (weight-only, M <= 8: split once into bf16 planes) when it
+    // fits 24 KiB, or 48 KiB for one row (M = 1, K = 12288: 16% faster than
+    // direct steps; the raw copy and the planes then hold 96 KiB of LDS, one
+    // workgroup per CU).  One row of a wide layer takes 4-tile steps over two
+    // row tiles per wave with 8 waves per workgroup (half the copies and
+    // splits: QKV and gate+up at K = 4096 2-6% faster) unless that grid needs
+    // fewer rounds of the 256 CUs than one row tile per workgroup
+    // (measured on MI355X at M = 1: N = 19456 and 18820 at K = 2560, 14.0 ->
+    // 12.0 us; N = 5120, K = 4096 keeps two tiles, 7.9 -> 7.2 us against one).
+    // Long K over fewer than 256 row tiles takes 8 waves (N = 2560, K = 9728:
+    // 9.5 -> 9.1 us).  Else direct steps: 8 tiles over one row tile for long
+    // K, 4 tiles over two row tiles for wide layers, 4 tiles over one row
+    // tile otherwise; K <= 256 one wave of 4-tile steps (K = 128: 3.0 ->
+    // 2.65 us).
     const int64_t xb = M * K * 4;
-    const bool xl = xb <= 24576 || (!w8a8 && M == 1 && xb <= kFastSplitBytes);
-    const bool wide1 = xl && !w8a8 && M == 1 && Kc < 128 && Nt >= 384;
+    const bool xl = (w8a8 || M <= 8) && (xb <= 24576 || (!w8a8 && M == 1 && xb <= kFastSplitBytes));
+    const auto rounds = [](int64_t wgs) { return (wgs + 255) / 256; };
+    const bool wide1 = xl && !w8a8 && M == 1 && Kc < 128 && Nt > 256 && rounds(Nt) >= 2 * rounds((Nt + 1) / 2);
     *id = wide1 ? 6 : (xl ? 0 : (Kc >= 128 ? 3 : (Nt >= 384 ? 4 : 2)));
-    *ks = wide1 ? 8 : 4;
+    *ks = wide1 || (xl && !w8a8 && Kc >= 128 && Nt < 256) ? 8 : 4;
+    if (!w8a8 && Kc <= 4) {
+      *id = 2;
+      *ks = 1;
+    }
   } else if (M <= 8) {
     // two row tiles per workgroup for wide layers; weight-only also from 257
     // row tiles, where one tile per workgroup needs a second round of the 256

@@ -279,6 +279,37 @@ FAST_CASES = [
 ]
 
 
+FAST_F32_CASES = [
+    # fp32 activations at decode shapes: x in LDS as bf16 high / remainder
+    # planes (M <= 8, x <= 24 KiB, or 48 KiB for one row), M = 2..8 filling
+    # the planes' MFMA columns partly or wholly, and direct steps beyond
+    (1, 6152, 4096), (1, 2560, 9728), (1, 19456, 2560), (2, 24, 64), (5, 1000, 1024), (8, 4096, 128),
+    (8, 130, 704), (3, 6160, 4096), (8, 2560, 2560), (12, 1000, 512), (16, 4096, 128),
+]
+
+
+@pytest.mark.parametrize("M,N,K", FAST_F32_CASES)
+def test_w8_fast_path_f32_planes(dev, M, N, K):
+    """fp32 x runs as high + remainder parts (x in LDS: row-scaled fp16, 22
+    significant bits; direct steps: bf16, 16 bits): every row, at magnitudes
+    from 1e-20 to 1e20, within 2e-5 of the float64 product of the oracle's
+    quantized weights, on activations no 2-byte type holds exactly.  Dropping
+    the remainder part would leave about 1e-3."""
+    announce(f"w8 fast f32 planes M={M} N={N} K={K}")
+    w = make_weights(N, K, 5200 + N + K)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(N + 1))
+    x = make_x(M, K, 6200 + M + K) * (1.0 + 1e-3 * torch.rand(M, K, generator=torch.Generator().manual_seed(M)))
+    x = x * torch.pow(10.0, torch.linspace(-20.0, 20.0, M, dtype=torch.float64)).float()[:, None]  # rows 1e-20 .. 1e20
+    for m in range(M):  # one element per row 1000x the rest: a row scale that missed it would overflow fp16
+        x[m, (K - 1 - 131 * m) % K] *= 1000.0
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref = (x.double().numpy() @ q.astype(np.float64).T) * s.astype(np.float64) + b.double().numpy()
+    lin = quant.Int8Linear(w, b)
+    y = quant.linear_w8(x.to(dev), lin.packed, lin.scale, lin.bias, N).cpu().numpy().astype(np.float64)
+    row_err = np.linalg.norm(y - ref, axis=1) / np.linalg.norm(ref, axis=1)
+    assert row_err.max() <= 2e-5, (float(row_err.max()), int(row_err.argmax()))
+
+
 @pytest.mark.parametrize("xd", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("M,N,K", FAST_CASES)
 def test_w8_fast_path_bias_strided(dev, M, N, K, xd):
