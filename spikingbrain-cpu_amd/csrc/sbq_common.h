@@ -70,12 +70,15 @@ __device__ __forceinline__ void u8x16_to_f16(u32x4 w, f16x8& s0, f16x8& s1) {
 }
 
 // 4 offset-binary bytes -> 4 bf16 values q (|q| <= 128 has <= 8 significant
-// bits, so every conversion below is exact).
+// bits, so every conversion below is exact).  One xor turns the four bytes
+// into q as signed bytes; each then converts with one sign-extending
+// sub-dword convert (no separate subtract of the offset).
 __device__ __forceinline__ void u8x4_to_bf16(uint32_t w, __bf16* out) {
-  out[0] = (__bf16)((float)(w & 0xffu) - 128.0f);
-  out[1] = (__bf16)((float)((w >> 8) & 0xffu) - 128.0f);
-  out[2] = (__bf16)((float)((w >> 16) & 0xffu) - 128.0f);
-  out[3] = (__bf16)((float)(w >> 24) - 128.0f);
+  const uint32_t s = w ^ 0x80808080u;
+  out[0] = (__bf16)(float)(int8_t)s;
+  out[1] = (__bf16)(float)(int8_t)(s >> 8);
+  out[2] = (__bf16)(float)(int8_t)(s >> 16);
+  out[3] = (__bf16)(float)(int8_t)(s >> 24);
 }
 
 __device__ __forceinline__ void u8x16_to_bf16(u32x4 w, bf16x8& s0, bf16x8& s1) {
