@@ -864,6 +864,8 @@ def main():
         extra["stack_grouped"] = stack_bench(ctx, grouped=True)
         log("decode step of the real checkpoint's shapes (hidden 2560, FFN 9728), fused and grouped")
         extra["stack_checkpoint_grouped"] = stack_bench(ctx, grouped=True, H=2560, F=9728)
+        log("the same step with fp32 activations, the reference model's own dtype")
+        extra["stack_checkpoint_grouped_f32x"] = stack_bench(ctx, grouped=True, H=2560, F=9728, xdtype=torch.float32)
         torch.cuda.empty_cache()
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
