@@ -415,15 +415,17 @@ def grouped_stack_launches(H=4096, F=12288, heads=32, d=128):
     return out
 
 
-def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, H=4096, F=12288, xdtype=None):
+def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, H=4096, F=12288, xdtype=None,
+                w8a8=False):
     """One decode step through every quantized linear of the 36-layer hybrid
     model (hidden H, FFN F; H=2560, F=9728 is the reference's real checkpoint),
-    one launch per linear, or fused / fused and grouped."""
+    one launch per linear, or fused / fused and grouped; w8a8: int8-dyn
+    linears (DynamicInt8Linear), one launch each (no grouped form)."""
     torch, quant = ctx.torch, ctx.quant
     launches = (grouped_stack_launches(H=H, F=F) if grouped
                 else [[sh] for sh in hybrid_stack_shapes(H=H, F=F, fused=fused)])
     shapes = [sh for grp in launches for sh in grp]
-    layers = [ctx.weights(N, K, 2000 + i) for i, (N, K) in enumerate(shapes)]
+    layers = [ctx.weights(N, K, 2000 + i, colsum=w8a8) for i, (N, K) in enumerate(shapes)]
     wbytes = sum(N * K for N, K in shapes)
     res = {"linears": len(shapes), "launches": len(launches), "weight_bytes": wbytes}
     for M in Ms:
@@ -432,6 +434,7 @@ def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, 
             if K not in xs:
                 xs[K] = [ctx.act(M, K, 3000 + K, xdtype), ctx.act(M, K, 3500 + K, xdtype)]  # a grouped pair reads two inputs
         ys = [torch.empty((M, N), dtype=torch.float16, device=ctx.dev) for N, K in shapes]
+        wss = {K: quant.w8a8_workspace(M, K, ctx.dev, None, xs[K][0].dtype) for K in xs} if w8a8 else {}
         plan, j = [], 0
         for grp in launches:
             plan.append((grp, layers[j:j + len(grp)], ys[j:j + len(grp)]))
@@ -439,7 +442,10 @@ def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, 
 
         def step():
             for grp, lays, outs in plan:
-                if len(grp) == 1:
+                if w8a8:
+                    (N, K), (packed, s, cs) = grp[0], lays[0]
+                    quant.linear_w8a8(xs[K][0], packed, s, cs, None, N, workspace=wss[K], out=outs[0])
+                elif len(grp) == 1:
                     (N, K), (packed, s, _) = grp[0], lays[0]
                     quant.linear_w8(xs[K][0], packed, s, None, N, out=outs[0])
                 else:
@@ -451,7 +457,7 @@ def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, 
         ms = ctx.time_graphs([g], steps, warmup)
         nbytes = sum(gemv_bytes(M, N, K) for N, K in shapes)
         res[f"M{M}"] = {"ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3), "GBps": nbytes / (ms * 1e-3) / 1e9}
-        del g, ys
+        del g, ys, wss
     del layers
     return res
 
@@ -816,6 +822,9 @@ def main():
               "stack_checkpoint_grouped": lambda ctx: stack_bench(ctx, grouped=True, H=2560, F=9728),
               "stack_checkpoint_grouped_f32x": lambda ctx: stack_bench(ctx, grouped=True, H=2560, F=9728,
                                                                        xdtype=ctx.torch.float32),
+              "stack_checkpoint_w8a8": lambda ctx: {xd: stack_bench(ctx, fused=True, H=2560, F=9728, w8a8=True,
+                                                                    xdtype=getattr(ctx.torch, xd))
+                                                    for xd in ("float16", "float32")},
               "cpu_baseline": lambda ctx: cpu_baseline(args.cpu_budget)}[args.only]
         print(json.dumps({args.only: fn(ctx)}), flush=True)
         return

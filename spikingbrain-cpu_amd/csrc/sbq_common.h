@@ -224,16 +224,29 @@ __device__ __forceinline__ void store_y4(void* y, int ytype, int64_t idx, f32x4 
 // ---------------------------------------------------------------------------
 // Wave reductions
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+// Minimum / maximum over the wave's 64 lanes by DPP lane moves, with no LDS
+// round trip: within quads, rows of 16 (half mirror, mirror), then row 0 into
+// row 1 and row 2 into row 3 (row_bcast:15), rows 0-1 into rows 2-3
+// (row_bcast:31); lane 63 ends with the result, which every lane then reads.
+// NaN inputs are ignored (fminf / fmaxf).  Called by whole waves.
+template <int CTRL, int ROWS, bool MAX>
+__device__ __forceinline__ float dpp_minmax_step(float v) {
+  const float t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xf,
+                                                             false));
+  return MAX ? fmaxf(v, t) : fminf(v, t);
 }
-__device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
-  return v;
+template <bool MAX>
+__device__ __forceinline__ float wave_minmax(float v) {
+  v = dpp_minmax_step<0xb1, 0xf, MAX>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_minmax_step<0x4e, 0xf, MAX>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_minmax_step<0x141, 0xf, MAX>(v);  // row_half_mirror
+  v = dpp_minmax_step<0x140, 0xf, MAX>(v);  // row_mirror
+  v = dpp_minmax_step<0x142, 0xa, MAX>(v);  // row_bcast:15
+  v = dpp_minmax_step<0x143, 0xc, MAX>(v);  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+__device__ __forceinline__ float wave_max(float v) { return wave_minmax<true>(v); }
+__device__ __forceinline__ float wave_min(float v) { return wave_minmax<false>(v); }
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -45,7 +45,7 @@ namespace {
 constexpr int kFastXLdsBytes = 32768;  // x[M][K] copied to LDS up to this size
 constexpr int kFastMaxWaves = 8;
 constexpr int kFusedChunks = 8;         // QM 2: 16-byte chunks of x per thread (at most)
-constexpr int kFusedMinWaves = 4;       // QM 2: x <= kFusedChunks * 16 * 64 * waves bytes
+constexpr int kFusedMinWaves = 4;       // W8A8 picks: 256 threads (QM 1: one min/max partial each)
 constexpr int kFastSplitBytes = 49152;  // fp32 x split into bf16 planes in LDS up to this size
 constexpr int kSplitChunks = 12;        // fp32 x split: 16-byte chunks of x per thread (at most)
 
@@ -698,7 +698,7 @@ int launch_fast_typed(int id, const GemvArgs& a, int ks, int KW, int xch, size_t
 // Launch of fast-path configuration `id` with `ks` waves per workgroup
 // (returns -1 when the configuration cannot run this shape).  W8A8 with
 // a.nparts == 0 reduces the activation min/max in the kernel (x must fit
-// kFusedChunks 16-byte chunks per thread, >= kFusedMinWaves waves).
+// kFusedChunks 16-byte chunks per thread of the workgroup).
 int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, hipStream_t st) {
   if (id < 0 || id >= kNumFastCfgs || ks < 1 || ks > kFastMaxWaves) return -1;
   const FastCfg c = kFastCfgs[id];
@@ -724,7 +724,7 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   if (split) lds += (size_t)xbytes;  // bf16 high / remainder planes
   if (a.flags & kGemvArgmax) lds += (size_t)c.G * 16 * 8;  // the fused argmax's keys per row tile
   const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
-  if (qm == 2 && (xbytes > (int64_t)kFusedChunks * 16 * T || ks < kFusedMinWaves)) return -1;
+  if (qm == 2 && xbytes > (int64_t)kFusedChunks * 16 * T) return -1;  // every thread holds its chunks of x
 #define SBQ_FAST_QM(XT_)                                                  \
   switch (qm) {                                                           \
     case 0:                                                               \
