@@ -233,7 +233,10 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   // two columns
   const uint8_t* xpl = (r < 8 ? xhi : xlo) + min(r & 7, M - 1) * K * 2 + g * 16 * 2;
   // end of the x copy and planes: the fused argmax keeps G * 16 keys there
-  const int xend = (XL ? xch * (int)blockDim.x * 16 : 0) + (kSplitX ? M * K * 4 : 0);
+  // QM 2: x is quantized once, from the chunks each thread holds for the
+  // min/max, into s8 rows [M][K] at xs (no x copy, no per-tile quantization)
+  constexpr bool kQX = QM == 2;
+  const int xend = kQX ? M * K : (XL ? xch * (int)blockDim.x * 16 : 0) + (kSplitX ? M * K * 4 : 0);
 
   // epilogue operands of row tile `ks` (wave ks < G finishes tile ks)
   const int nte = min(nt0 + min(ks, G - 1), a.Nt - 1);
@@ -270,7 +273,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
 
   // x copy into LDS: xch 16-byte chunks per thread, sources clamped
   const uint8_t* xg = (const uint8_t*)a.x;
-  if constexpr (XL) {
+  if constexpr (XL && !kQX) {
     const int cpr = xrow / 16, nch = M * cpr;
     for (int i = 0; i < xch; ++i) {
       const int c0 = i * blockDim.x + ks * 64;  // first chunk of this wave
@@ -286,11 +289,11 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   for (int j = 0; j < G; ++j) wp[j] = a.packed + ((int64_t)min(nt0 + j, a.Nt - 1) * Kc + kbeg) * 1024 + lane * 16;
   const uint8_t* xp = xg + (int64_t)mr * a.ldx * EB + ((int64_t)kbeg * 64 + g * 16) * EB;
   u32x4 w[D][G];
-  XRaw<XT> xd[XL ? 1 : D];
+  XRaw<XT> xd[XL || kQX ? 1 : D];
 #pragma unroll
   for (int p = 0; p < D; ++p) {
     const int kt = min(p, cnt - 1);
-    if constexpr (!XL) load_frag<XT>(xd[p], xp + kt * 64 * EB);
+    if constexpr (!XL && !kQX) load_frag<XT>(xd[p], xp + kt * 64 * EB);
 #pragma unroll
     for (int j = 0; j < G; ++j) w[p][j] = load_tile_nt(wp[j] + kt * 1024);
   }
@@ -366,6 +369,36 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       }
       qp = choose_act_qparams(mn, mx);
     }
+    if constexpr (kQX) {
+      // the s8 values xq - 128 of this thread's chunks (quant16's arithmetic:
+      // one fma and one pack per value), 16 / EB values per chunk
+      constexpr int NE = 16 / EB;
+      const int cpr = K * EB / 16;
+#pragma unroll
+      for (int i = 0; i < kFusedChunks; ++i) {
+        if (i * (int)blockDim.x >= xm_nch) break;
+        const int c = min(tid + i * (int)blockDim.x, xm_nch - 1);
+        const int m = c / cpr;
+        uint8_t* dst = xs + m * K + (c - m * cpr) * NE;
+        float v[NE];
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+          const uint32_t word = xmm[i][EB == 4 ? j : j / 2];
+          if constexpr (XT == XT_F32) v[j] = __uint_as_float(word);
+          else if constexpr (XT == XT_F16) v[j] = (float)__builtin_bit_cast(f16x2, word)[j & 1];
+          else v[j] = (float)__builtin_bit_cast(bf16x2, word)[j & 1];
+        }
+        uint32_t d[NE / 4];
+#pragma unroll
+        for (int j = 0; j < NE / 4; ++j)
+          d[j] = pack_act_s8x4(__builtin_fmaf(v[4 * j], qp.inv, qp.zpf), __builtin_fmaf(v[4 * j + 1], qp.inv, qp.zpf),
+                               __builtin_fmaf(v[4 * j + 2], qp.inv, qp.zpf),
+                               __builtin_fmaf(v[4 * j + 3], qp.inv, qp.zpf));
+        if constexpr (NE == 4) *(uint32_t*)dst = d[0];
+        else *(u32x2*)dst = (u32x2){d[0], d[1]};
+      }
+      lds_barrier();
+    }
   }
 
   Acc acc[G];
@@ -383,6 +416,12 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, v0, acc[j], 0, 0, 0);
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, v1, acc[j], 0, 0, 0);
       }
+      return;
+    }
+    if constexpr (kQX) {
+      const i32x4 q = *(const i32x4*)(xs + mr * K + (kbeg + kt) * 64 + g * 16);
+#pragma unroll
+      for (int j = 0; j < G; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_to_s8(w[p][j]), q, acc[j], 0, 0, 0);
       return;
     }
     XRaw<XT> f;
@@ -407,7 +446,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
     for (int p = 0; p < D; ++p) {
       step(p, t + p);
       const int kt = min(t + D + p, cnt - 1);
-      if constexpr (!XL) load_frag<XT>(xd[p], xp + kt * 64 * EB);
+      if constexpr (!XL && !kQX) load_frag<XT>(xd[p], xp + kt * 64 * EB);
 #pragma unroll
       for (int j = 0; j < G; ++j) w[p][j] = load_tile_nt(wp[j] + kt * 1024);
       // keep each refill next to the step that freed its registers (otherwise
@@ -718,12 +757,13 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   if (split && a.M > 8) return -1;  // the two planes of a row share the 16 MFMA columns
   if (c.D * c.G > 32) return -1;
   const int T = ks * 64;
-  const int xch = c.XL ? (int)((xbytes / 16 + T - 1) / T) : 0;
+  const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
+  const int xch = c.XL && qm != 2 ? (int)((xbytes / 16 + T - 1) / T) : 0;
   if (split && xch > kSplitChunks) return -1;  // the chunks of x each thread splits
   size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
-  if (split) lds += (size_t)xbytes;  // bf16 high / remainder planes
+  if (split) lds += (size_t)xbytes;               // bf16 high / remainder planes
+  if (qm == 2) lds += (size_t)a.M * a.K;           // the quantized s8 rows
   if (a.flags & kGemvArgmax) lds += (size_t)c.G * 16 * 8;  // the fused argmax's keys per row tile
-  const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
   if (qm == 2 && xbytes > (int64_t)kFusedChunks * 16 * T) return -1;  // every thread holds its chunks of x
 #define SBQ_FAST_QM(XT_)                                                  \
   switch (qm) {                                                           \
@@ -886,7 +926,12 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     // decode 8-24% faster); 8 waves beyond 32 KiB and on the widest layers
     const int64_t xb = M * K * (xt == XT_F32 ? 4 : 2);
     if (xb > 16384 && xb <= 65536 && (xb > 32768 || Nt >= 1024)) *ks = 8;
-    if (*ks < kFusedMinWaves) *ks = kFusedMinWaves;  // 256 threads cover the min/max partials / fused x
+    if (Kc <= 4 && xb <= (int64_t)kFusedChunks * 16 * 64) {  // short K: one wave, as for weight-only
+      *id = 2;
+      *ks = 1;
+    } else if (*ks < kFusedMinWaves) {
+      *ks = kFusedMinWaves;  // 256 threads cover the min/max partials / fused x
+    }
   }
   return true;
 }
