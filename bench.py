@@ -875,6 +875,9 @@ def main():
         extra["stack_checkpoint_grouped"] = stack_bench(ctx, grouped=True, H=2560, F=9728)
         log("the same step with fp32 activations, the reference model's own dtype")
         extra["stack_checkpoint_grouped_f32x"] = stack_bench(ctx, grouped=True, H=2560, F=9728, xdtype=torch.float32)
+        log("the same step in int8-dyn mode (DynamicInt8Linear), fused layers, fp16 and fp32 activations")
+        extra["stack_checkpoint_w8a8"] = {xd: stack_bench(ctx, fused=True, H=2560, F=9728, w8a8=True,
+                                                          xdtype=getattr(torch, xd)) for xd in ("float16", "float32")}
         torch.cuda.empty_cache()
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
