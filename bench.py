@@ -620,7 +620,7 @@ def _short(name):
     return name.split("(")[0] if name.startswith("sbq::") else name[:60]
 
 
-def summarize_trace(d, command):
+def summarize_trace(d, command, title="the default bench run"):
     """Markdown summary of a rocprofv3 --kernel-trace --stats run: kernels by
     total time, split by launch grid, and the dominant kernel's average."""
     import statistics
@@ -632,7 +632,7 @@ def summarize_trace(d, command):
         key = (_short(r["Kernel_Name"]), grid, int(r["Workgroup_Size_X"]))
         agg.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
     total = sum(sum(v) for v in agg.values())
-    out = ["# rocprofv3 kernel trace of the default bench run", "", "Command:", "", "```", command, "```", "",
+    out = [f"# rocprofv3 kernel trace of {title}", "", "Command:", "", "```", command, "```", "",
            f"Dispatches: {sum(len(v) for v in agg.values())}, kernel time {total / 1e3:.1f} ms.", "",
            "| kernel | grid (work-items) | block | calls | avg us | median us | min us | % time |",
            "|---|---|---|---|---|---|---|---|"]
@@ -773,9 +773,12 @@ def main():
                     help="print per-dispatch counter averages from rocprofv3 --pmc directories")
     ap.add_argument("--match", default="gemm_dl_kernel", help="kernel-name filter for --summarize-counters")
     ap.add_argument("--command", default="", help="the profiling command(s), recorded in the summary")
+    ap.add_argument("--title", default="the default bench run", help="what --summarize-trace's run measured")
+    ap.add_argument("--stack-m", type=int, nargs="+", default=[1, 8], metavar="M",
+                    help="decode batch sizes of the --only stack_* measurements")
     args = ap.parse_args()
     if args.summarize_trace:
-        print(summarize_trace(args.summarize_trace, args.command), end="")
+        print(summarize_trace(args.summarize_trace, args.command, args.title), end="")
         return
     if args.summarize_pmc:
         print(summarize_pmc(*args.summarize_pmc, args.command), end="")
@@ -810,19 +813,20 @@ def main():
         gemv_probe(ctx, N, K, M)
         return
     if args.only:
+        sm = tuple(args.stack_m)
         fn = {"lm_head_greedy": lm_head_greedy_bench, "device_state": device_state_bench,
-              "stack_fused": lambda ctx: stack_bench(ctx, fused=True),
+              "stack_fused": lambda ctx: stack_bench(ctx, Ms=sm, fused=True),
               "w8a8_token": lambda ctx: [w8a8_bench(ctx, M, N, token=True) for M in (1, 128, 2048)
                                          for N in (4096, 12288)],
               "mid_m": lambda ctx: [midm_bench(ctx, M, N, fmt) for fmt in ("int8", "int8-dyn") for M in (64, 128, 256)
                                     for N in (4096, 12288)],
               "prefill_fp32_y": lambda ctx: [prefill_bench(ctx, M, xdtype=xd, ydtype=ctx.torch.float32)
                                              for M in (512, 2048) for xd in (ctx.torch.float16, ctx.torch.float32)],
-              "stack_grouped": lambda ctx: stack_bench(ctx, grouped=True),
-              "stack_checkpoint_grouped": lambda ctx: stack_bench(ctx, grouped=True, H=2560, F=9728),
-              "stack_checkpoint_grouped_f32x": lambda ctx: stack_bench(ctx, grouped=True, H=2560, F=9728,
+              "stack_grouped": lambda ctx: stack_bench(ctx, Ms=sm, grouped=True),
+              "stack_checkpoint_grouped": lambda ctx: stack_bench(ctx, Ms=sm, grouped=True, H=2560, F=9728),
+              "stack_checkpoint_grouped_f32x": lambda ctx: stack_bench(ctx, Ms=sm, grouped=True, H=2560, F=9728,
                                                                        xdtype=ctx.torch.float32),
-              "stack_checkpoint_w8a8": lambda ctx: {xd: stack_bench(ctx, fused=True, H=2560, F=9728, w8a8=True,
+              "stack_checkpoint_w8a8": lambda ctx: {xd: stack_bench(ctx, Ms=sm, fused=True, H=2560, F=9728, w8a8=True,
                                                                     xdtype=getattr(ctx.torch, xd))
                                                     for xd in ("float16", "float32")},
               "cpu_baseline": lambda ctx: cpu_baseline(args.cpu_budget)}[args.only]
