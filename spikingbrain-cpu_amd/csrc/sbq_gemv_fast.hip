@@ -874,8 +874,8 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     // fewer rounds of the 256 CUs than one row tile per workgroup
     // (measured on MI355X at M = 1: N = 19456 and 18820 at K = 2560, 14.0 ->
     // 12.0 us; N = 5120, K = 4096 keeps two tiles, 7.9 -> 7.2 us against one).
-    // Long K over fewer than 256 row tiles takes 8 waves (N = 2560, K = 9728:
-    // 9.5 -> 9.1 us).  Else direct steps: 8 tiles over one row tile for long
+    // Long K over at most 256 row tiles takes 8 waves (N = 2560, K = 9728:
+    // 8.9 -> 8.5 us; N = 4096, K = 12288: 11.6 -> 11.35 us).  Else direct steps: 8 tiles over one row tile for long
     // K, 4 tiles over two row tiles for wide layers, 4 tiles over one row
     // tile otherwise; K <= 256 one wave of 4-tile steps (K = 128: 3.0 ->
     // 2.65 us).
@@ -884,7 +884,7 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     const auto rounds = [](int64_t wgs) { return (wgs + 255) / 256; };
     const bool wide1 = xl && !w8a8 && M == 1 && Kc < 128 && Nt > 256 && rounds(Nt) >= 2 * rounds((Nt + 1) / 2);
     *id = wide1 ? 6 : (xl ? 0 : (Kc >= 128 ? 3 : (Nt >= 384 ? 4 : 2)));
-    *ks = wide1 || (xl && !w8a8 && Kc >= 128 && Nt < 256) ? 8 : 4;
+    *ks = wide1 || (xl && !w8a8 && Kc >= 128 && Nt <= 256) ? 8 : 4;
     if (!w8a8 && Kc <= 4) {
       *id = 2;
       *ks = 1;
