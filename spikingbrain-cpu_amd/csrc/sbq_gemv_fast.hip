@@ -43,6 +43,7 @@ namespace sbq {
 namespace {
 
 constexpr int kFastXLdsBytes = 32768;  // x[M][K] copied to LDS up to this size
+constexpr int kFastXLdsWideBytes = 65536;  // ... with 5 row tiles per workgroup (one workgroup per CU)
 constexpr int kFastMaxWaves = 8;
 constexpr int kFusedChunks = 8;         // QM 2: 16-byte chunks of x per thread (at most)
 constexpr int kFusedMinWaves = 4;       // W8A8 picks: 256 threads (QM 1: one min/max partial each)
@@ -701,7 +702,8 @@ namespace {
   X(3, 8, 1, false)         \
   X(4, 4, 2, false)         \
   X(5, 8, 2, false)         \
-  X(6, 4, 2, true)
+  X(6, 4, 2, true)          \
+  X(7, 2, 5, true)
 
 struct FastCfg {
   int id, D, G;
@@ -753,7 +755,7 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   const int eb = xt == XT_F32 ? 4 : 2;
   const int64_t xbytes = (int64_t)a.M * a.K * eb;
   const bool split = c.XL && xt == XT_F32 && !w8a8;  // fp32 x: raw copy + fp16 planes
-  if (c.XL && xbytes > (split ? kFastSplitBytes : kFastXLdsBytes)) return -1;
+  if (c.XL && xbytes > (split ? kFastSplitBytes : (c.G == 5 ? kFastXLdsWideBytes : kFastXLdsBytes))) return -1;
   if (split && a.M > 8) return -1;  // the two planes of a row share the 16 MFMA columns
   if (c.D * c.G > 32) return -1;
   const int T = ks * 64;
@@ -913,6 +915,16 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
         *ks = 1;
       } else if (xl && (wide ? rounds(Nt) < 2 * rounds((Nt + 1) / 2) : Nt < 256)) {
         *id = 0;  // D=8, G=1, x in LDS
+      }
+      // M = 4 .. 8, a wide layer at short K whose grid of five row tiles per
+      // workgroup fills one round of the CUs: x (up to 64 KiB) in LDS, read
+      // once per five row tiles instead of once per one or two (M = 8, N =
+      // 19456 / 18820, K = 2560: 12.5 -> 10.9 / 12.7 -> 10.7 us; M = 4: 11.9
+      // -> 10.5 / 11.8 -> 10.3 us; grids of more than 256 such workgroups, as
+      // N = 24576 at K = 4096, run slower)
+      if (M >= 4 && Kc < 128 && Nt > 1024 && (Nt + 4) / 5 <= 256 && M * K * 2 <= kFastXLdsWideBytes) {
+        *id = 7;  // D=2, G=5, x in LDS
+        *ks = 8;
       }
     }
   } else {

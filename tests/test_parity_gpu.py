@@ -276,6 +276,9 @@ FAST_CASES = [
     # (the checkpoint's grouped 2 x 2560 x 4096 output projections among them)
     (1, 6152, 4096), (3, 6160, 4096), (5, 6144, 4096), (8, 4100, 12288), (16, 6152, 2560), (2, 24, 64),
     (1, 4, 128), (1, 5120, 4096), (4, 4610, 2560), (7, 6100, 4096),
+    # M = 4 .. 8 over more than 1024 row tiles at short K: five row tiles per
+    # workgroup with x in LDS (ragged last workgroup; 1025 row tiles)
+    (8, 19456, 2560), (4, 18820, 2560), (6, 16400, 2560),
 ]
 
 
