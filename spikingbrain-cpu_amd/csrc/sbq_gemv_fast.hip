@@ -49,6 +49,8 @@ constexpr int kFusedChunks = 8;         // QM 2: 16-byte chunks of x per thread 
 constexpr int kFusedMinWaves = 4;       // W8A8 picks: 256 threads (QM 1: one min/max partial each)
 constexpr int kFastSplitBytes = 49152;  // fp32 x split into bf16 planes in LDS up to this size
 constexpr int kSplitChunks = 12;        // fp32 x split: 16-byte chunks of x per thread (at most)
+constexpr int kSplitRegChunks = 10;     // ... held in registers by five-row-tile workgroups
+constexpr int kSplitWideBytes = 81920;  // fp32 x split by five-row-tile workgroups up to this size
 
 __device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
@@ -227,7 +229,10 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   uint8_t* xs = smem + red_bytes<G>(KS) + mm_bytes();
   const int xrow = K * EB;  // bytes of one x row in LDS
   constexpr bool kSplitX = XL && XT == XT_F32 && !W8A8;
-  uint8_t* xhi = xs + xch * (int)blockDim.x * 16;  // kSplitX: bf16 planes [M][K] after the x copy
+  // five row tiles per workgroup (one workgroup per CU, up to 256 VGPRs per
+  // wave): x goes to registers and only the planes take LDS
+  constexpr bool kSplitReg = kSplitX && G == 5;
+  uint8_t* xhi = xs + (kSplitReg ? 0 : xch * (int)blockDim.x * 16);  // kSplitX: bf16 planes [M][K] after the x copy
   uint8_t* xlo = xhi + M * K * 2;
   // kSplitX (M <= 8): MFMA column r < 8 multiplies the high plane of row r,
   // column r + 8 the remainder plane of the same row; the epilogue adds the
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   // QM 2: x is quantized once, from the chunks each thread holds for the
   // min/max, into s8 rows [M][K] at xs (no x copy, no per-tile quantization)
   constexpr bool kQX = QM == 2;
-  const int xend = kQX ? M * K : (XL ? xch * (int)blockDim.x * 16 : 0) + (kSplitX ? M * K * 4 : 0);
+  const int xend = kQX ? M * K : (XL && !kSplitReg ? xch * (int)blockDim.x * 16 : 0) + (kSplitX ? M * K * 4 : 0);
 
   // epilogue operands of row tile `ks` (wave ks < G finishes tile ks)
   const int nte = min(nt0 + min(ks, G - 1), a.Nt - 1);
@@ -274,7 +279,18 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
 
   // x copy into LDS: xch 16-byte chunks per thread, sources clamped
   const uint8_t* xg = (const uint8_t*)a.x;
-  if constexpr (XL && !kQX) {
+  f32x4 xr[kSplitReg ? kSplitRegChunks : 1];
+  if constexpr (kSplitReg) {  // chunks c = tid + i * T of x (row c / (K / 4)), sources clamped
+    const int K4 = K / 4, xnch = M * K4;
+#pragma unroll
+    for (int i = 0; i < kSplitRegChunks; ++i) {
+      if (i * (int)blockDim.x < xnch) {
+        const int c = min(tid + i * (int)blockDim.x, xnch - 1);
+        const int m = c / K4;
+        xr[i] = *(const f32x4*)(xg + ((int64_t)m * a.ldx + (c - m * K4) * 4) * 4);
+      }
+    }
+  } else if constexpr (XL && !kQX) {
     const int cpr = xrow / 16, nch = M * cpr;
     for (int i = 0; i < xch; ++i) {
       const int c0 = i * blockDim.x + ks * 64;  // first chunk of this wave
@@ -335,26 +351,35 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       // them back four at a time with the reads issued together.
       const f32x4* raw = (const f32x4*)xs;
       const int T = blockDim.x, xnch = M * (K / 4), last = xch * T - 1;
+      const auto split_store = [&](const f32x4& v, int c) {
+        bf16x4 h, l;
 #pragma unroll
-      for (int b = 0; b < kSplitChunks; b += 4) {
-        if (b * T < xnch) {  // uniform
-          f32x4 v[4];
+        for (int e = 0; e < 4; ++e) {
+          __bf16 hh, ll;
+          split_bf16(v[e], hh, ll);
+          h[e] = hh;
+          l[e] = ll;
+        }
+        *(bf16x4*)(xhi + c * 8) = h;  // element 4c of the [M][K] plane
+        *(bf16x4*)(xlo + c * 8) = l;
+      };
+      if constexpr (kSplitReg) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) v[j] = raw[min(tid + (b + j) * T, last)];
+        for (int i = 0; i < kSplitRegChunks; ++i) {
+          const int c = tid + i * T;
+          if (i * T < xnch && c < xnch) split_store(xr[i], c);
+        }
+      } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int c = tid + (b + j) * T;
-            if (c < xnch) {
-              bf16x4 h, l;
+        for (int b = 0; b < kSplitChunks; b += 4) {
+          if (b * T < xnch) {  // uniform
+            f32x4 v[4];
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                __bf16 hh, ll;
-                split_bf16(v[j][e], hh, ll);
-                h[e] = hh;
-                l[e] = ll;
-              }
-              *(bf16x4*)(xhi + c * 8) = h;  // element 4c of the [M][K] plane
-              *(bf16x4*)(xlo + c * 8) = l;
+            for (int j = 0; j < 4; ++j) v[j] = raw[min(tid + (b + j) * T, last)];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int c = tid + (b + j) * T;
+              if (c < xnch) split_store(v[j], c);
             }
           }
         }
@@ -755,12 +780,15 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   const int eb = xt == XT_F32 ? 4 : 2;
   const int64_t xbytes = (int64_t)a.M * a.K * eb;
   const bool split = c.XL && xt == XT_F32 && !w8a8;  // fp32 x: raw copy + fp16 planes
-  if (c.XL && xbytes > (split ? kFastSplitBytes : (c.G == 5 ? kFastXLdsWideBytes : kFastXLdsBytes))) return -1;
+  const bool split_reg = split && c.G == 5;  // fp32 x in registers, planes only in LDS
+  if (c.XL && xbytes > (split ? (split_reg ? kSplitWideBytes : kFastSplitBytes)
+                              : (c.G == 5 ? kFastXLdsWideBytes : kFastXLdsBytes))) return -1;
   if (split && a.M > 8) return -1;  // the two planes of a row share the 16 MFMA columns
   if (c.D * c.G > 32) return -1;
   const int T = ks * 64;
   const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
-  const int xch = c.XL && qm != 2 ? (int)((xbytes / 16 + T - 1) / T) : 0;
+  const int xch = c.XL && qm != 2 && !split_reg ? (int)((xbytes / 16 + T - 1) / T) : 0;
+  if (split_reg && (xbytes / 16 + T - 1) / T > kSplitRegChunks) return -1;  // the chunks each thread holds
   if (split && xch > kSplitChunks) return -1;  // the chunks of x each thread splits
   size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
   if (split) lds += (size_t)xbytes;               // bf16 high / remainder planes
@@ -890,6 +918,13 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     if (!w8a8 && Kc <= 4) {
       *id = 2;
       *ks = 1;
+    }
+    // M = 4 .. 8 on a wide short-K layer whose grid of five row tiles per
+    // workgroup fits one round of the CUs: x (up to 80 KiB) loaded into
+    // registers and split into planes in LDS, read once per five row tiles
+    if (!w8a8 && M >= 4 && M <= 8 && Kc < 128 && Nt > 1024 && (Nt + 4) / 5 <= 256 && xb <= kSplitWideBytes) {
+      *id = 7;  // D=2, G=5, x in LDS
+      *ks = 8;
     }
   } else if (M <= 8) {
     // two row tiles per workgroup for wide layers; weight-only also from 257

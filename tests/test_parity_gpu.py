@@ -288,6 +288,7 @@ FAST_F32_CASES = [
     # the planes' MFMA columns partly or wholly, and direct steps beyond
     (1, 6152, 4096), (1, 2560, 9728), (1, 19456, 2560), (2, 24, 64), (5, 1000, 1024), (8, 4096, 128),
     (8, 130, 704), (3, 6160, 4096), (8, 2560, 2560), (12, 1000, 512), (16, 4096, 128), (1, 4096, 12288),
+    (8, 19456, 2560), (5, 16400, 2560),  # five row tiles per workgroup, x split from registers
 ]
 
 
