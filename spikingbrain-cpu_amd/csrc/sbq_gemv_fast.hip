@@ -979,6 +979,12 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     } else if (*ks < kFusedMinWaves) {
       *ks = kFusedMinWaves;  // 256 threads cover the min/max partials / fused x
     }
+    // M = 4 .. 8 on a wide short-K layer: five row tiles per workgroup, as
+    // for weight-only, when x fits the fused min/max (8 chunks per thread)
+    if (M >= 4 && Kc < 128 && Nt > 1024 && (Nt + 4) / 5 <= 256 && xb <= (int64_t)kFusedChunks * 16 * 512) {
+      *id = 7;
+      *ks = 8;
+    }
   }
   return true;
 }

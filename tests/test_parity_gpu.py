@@ -370,7 +370,7 @@ def test_w8_integer_activations_exact(dev):
 W8A8_CASES = [(1, 4096, 4096), (1, 4, 2560), (5, 64, 4096), (16, 13, 96), (33, 512, 256), (64, 100, 1000),
               (65, 64, 4096), (128, 1024, 4096), (300, 130, 200),
               (3, 6152, 4096), (8, 4100, 12288), (16, 6144, 4096), (2, 24, 64), (4, 16400, 4096), (1, 4100, 12288),
-              (1, 4096, 128), (8, 4096, 256), (1, 2560, 9728)]
+              (1, 4096, 128), (8, 4096, 256), (1, 2560, 9728), (8, 19456, 2560), (5, 16400, 2560)]
 
 
 @pytest.mark.parametrize("xd", ["f32", "f16", "bf16"])
