@@ -758,6 +758,10 @@ GROUP_CASES = [
     (1, 4096, (4096, 4096, 4096), "f32"),
     (1, 12288, (4096, 10), "f16"),
     (24, 4096, (4096, 1000), "f16"),
+    # M = 4 .. 8 over more than 1024 row tiles in all at K = 2560: five row
+    # tiles per workgroup with x in LDS (fp32: split from registers), ragged
+    # segments
+    (8, 2560, (9728, 9728), "f16"), (8, 2560, (9728, 9728), "f32"), (4, 2560, (9000, 8000, 700), "bf16"),
 ]
 
 
