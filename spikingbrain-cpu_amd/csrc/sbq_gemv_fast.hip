@@ -886,11 +886,12 @@ int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st) {
 // MI355X over the decode shapes (M = 1, 4, 16; K = 4096, 12288; N = 4096 ..
 // 151936): 4-tile steps over two row tiles per wave for wide K = 4096 layers,
 // 8-tile steps over one row tile for long K or narrow N, two waves per row tile
-// once M > 8 (the activation fragments then dominate the registers).  bf16
+// once M > 8 (the activation fragments then dominate the registers), five row
+// tiles per workgroup with x in LDS at M = 4 .. 8 on wide short-K layers.  bf16
 // activations follow the fp16 rules; fp32 activations are copied to LDS and
-// split once into row-scaled fp16 high / remainder planes when x fits, and otherwise take
-// direct steps with two row tiles per wave on wide layers (M = 4, N = 6144 and
-// 24576: 21-28% faster than one row tile).
+// split once into bf16 high / remainder planes when x fits (M <= 8), and
+// otherwise take direct steps with two row tiles per wave on wide layers (M =
+// 4, N = 6144 and 24576: 21-28% faster than one row tile).
 bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks) {
   if (M < 1 || M > 16 || K % 64 != 0 || !xvec) return false;
   const int64_t Kc = K / 64, Nt = (N + 15) / 16;
