@@ -242,7 +242,11 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   // QM 2: x is quantized once, from the chunks each thread holds for the
   // min/max, into s8 rows [M][K] at xs (no x copy, no per-tile quantization)
   constexpr bool kQX = QM == 2;
-  const int xend = kQX ? M * K : (XL && !kSplitReg ? xch * (int)blockDim.x * 16 : 0) + (kSplitX ? M * K * 4 : 0);
+  // QM 1 with five row tiles per workgroup: the (s_x, zp) of the pre-pass
+  // partials quantize the thread's chunks of x, held in registers, the same way
+  constexpr bool kQX1 = QM == 1 && G == 5;
+  constexpr bool kQXL = kQX || kQX1;  // s8 rows in LDS
+  const int xend = kQXL ? M * K : (XL && !kSplitReg ? xch * (int)blockDim.x * 16 : 0) + (kSplitX ? M * K * 4 : 0);
 
   // epilogue operands of row tile `ks` (wave ks < G finishes tile ks)
   const int nte = min(nt0 + min(ks, G - 1), a.Nt - 1);
@@ -279,6 +283,18 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
 
   // x copy into LDS: xch 16-byte chunks per thread, sources clamped
   const uint8_t* xg = (const uint8_t*)a.x;
+  u32x4 xq1[kQX1 ? kSplitRegChunks : 1];
+  if constexpr (kQX1) {  // chunks c = tid + i * T of x, sources clamped
+    const int cpr = K * EB / 16;
+#pragma unroll
+    for (int i = 0; i < kSplitRegChunks; ++i) {
+      if (i * (int)blockDim.x < xm_nch) {
+        const int c = min(tid + i * (int)blockDim.x, xm_nch - 1);
+        const int m = c / cpr;
+        xq1[i] = *(const u32x4*)(xg + (int64_t)m * a.ldx * EB + (c - m * cpr) * 16);
+      }
+    }
+  }
   f32x4 xr[kSplitReg ? kSplitRegChunks : 1];
   if constexpr (kSplitReg) {  // chunks c = tid + i * T of x (row c / (K / 4)), sources clamped
     const int K4 = K / 4, xnch = M * K4;
@@ -290,7 +306,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
         xr[i] = *(const f32x4*)(xg + ((int64_t)m * a.ldx + (c - m * K4) * 4) * 4);
       }
     }
-  } else if constexpr (XL && !kQX) {
+  } else if constexpr (XL && !kQXL) {
     const int cpr = xrow / 16, nch = M * cpr;
     for (int i = 0; i < xch; ++i) {
       const int c0 = i * blockDim.x + ks * 64;  // first chunk of this wave
@@ -395,21 +411,18 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       }
       qp = choose_act_qparams(mn, mx);
     }
-    if constexpr (kQX) {
+    if constexpr (kQXL) {
       // the s8 values xq - 128 of this thread's chunks (quant16's arithmetic:
       // one fma and one pack per value), 16 / EB values per chunk
       constexpr int NE = 16 / EB;
       const int cpr = K * EB / 16;
-#pragma unroll
-      for (int i = 0; i < kFusedChunks; ++i) {
-        if (i * (int)blockDim.x >= xm_nch) break;
-        const int c = min(tid + i * (int)blockDim.x, xm_nch - 1);
+      const auto quant_store = [&](const u32x4& raw, int c) {
         const int m = c / cpr;
         uint8_t* dst = xs + m * K + (c - m * cpr) * NE;
         float v[NE];
 #pragma unroll
         for (int j = 0; j < NE; ++j) {
-          const uint32_t word = xmm[i][EB == 4 ? j : j / 2];
+          const uint32_t word = raw[EB == 4 ? j : j / 2];
           if constexpr (XT == XT_F32) v[j] = __uint_as_float(word);
           else if constexpr (XT == XT_F16) v[j] = (float)__builtin_bit_cast(f16x2, word)[j & 1];
           else v[j] = (float)__builtin_bit_cast(bf16x2, word)[j & 1];
@@ -422,6 +435,17 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
                                __builtin_fmaf(v[4 * j + 3], qp.inv, qp.zpf));
         if constexpr (NE == 4) *(uint32_t*)dst = d[0];
         else *(u32x2*)dst = (u32x2){d[0], d[1]};
+      };
+      if constexpr (kQX) {
+#pragma unroll
+        for (int i = 0; i < kFusedChunks; ++i) {
+          if (i * (int)blockDim.x >= xm_nch) break;
+          quant_store(xmm[i], min(tid + i * (int)blockDim.x, xm_nch - 1));
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kSplitRegChunks; ++i)
+          if (i * (int)blockDim.x < xm_nch) quant_store(xq1[i], min(tid + i * (int)blockDim.x, xm_nch - 1));
       }
       lds_barrier();
     }
@@ -444,7 +468,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       }
       return;
     }
-    if constexpr (kQX) {
+    if constexpr (kQXL) {
       const i32x4 q = *(const i32x4*)(xs + mr * K + (kbeg + kt) * 64 + g * 16);
 #pragma unroll
       for (int j = 0; j < G; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(tile_to_s8(w[p][j]), q, acc[j], 0, 0, 0);
@@ -781,18 +805,20 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   const int64_t xbytes = (int64_t)a.M * a.K * eb;
   const bool split = c.XL && xt == XT_F32 && !w8a8;  // fp32 x: raw copy + fp16 planes
   const bool split_reg = split && c.G == 5;  // fp32 x in registers, planes only in LDS
-  if (c.XL && xbytes > (split ? (split_reg ? kSplitWideBytes : kFastSplitBytes)
-                              : (c.G == 5 ? kFastXLdsWideBytes : kFastXLdsBytes))) return -1;
+  const bool qx1 = w8a8 && a.nparts > 0 && c.G == 5;  // pre-pass (s_x, zp), x quantized from registers
+  if (c.XL && xbytes > (split_reg || qx1 ? kSplitWideBytes
+                                         : (split ? kFastSplitBytes : (c.G == 5 ? kFastXLdsWideBytes : kFastXLdsBytes))))
+    return -1;
   if (split && a.M > 8) return -1;  // the two planes of a row share the 16 MFMA columns
   if (c.D * c.G > 32) return -1;
   const int T = ks * 64;
   const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
-  const int xch = c.XL && qm != 2 && !split_reg ? (int)((xbytes / 16 + T - 1) / T) : 0;
-  if (split_reg && (xbytes / 16 + T - 1) / T > kSplitRegChunks) return -1;  // the chunks each thread holds
+  const int xch = c.XL && qm != 2 && !split_reg && !qx1 ? (int)((xbytes / 16 + T - 1) / T) : 0;
+  if ((split_reg || qx1) && (xbytes / 16 + T - 1) / T > kSplitRegChunks) return -1;  // the chunks each thread holds
   if (split && xch > kSplitChunks) return -1;  // the chunks of x each thread splits
   size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
   if (split) lds += (size_t)xbytes;               // bf16 high / remainder planes
-  if (qm == 2) lds += (size_t)a.M * a.K;           // the quantized s8 rows
+  if (qm == 2 || qx1) lds += (size_t)a.M * a.K;    // the quantized s8 rows
   if (a.flags & kGemvArgmax) lds += (size_t)c.G * 16 * 8;  // the fused argmax's keys per row tile
   if (qm == 2 && xbytes > (int64_t)kFusedChunks * 16 * T) return -1;  // every thread holds its chunks of x
 #define SBQ_FAST_QM(XT_)                                                  \
@@ -981,8 +1007,9 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
       *ks = kFusedMinWaves;  // 256 threads cover the min/max partials / fused x
     }
     // M = 4 .. 8 on a wide short-K layer: five row tiles per workgroup, as
-    // for weight-only, when x fits the fused min/max (8 chunks per thread)
-    if (M >= 4 && Kc < 128 && Nt > 1024 && (Nt + 4) / 5 <= 256 && xb <= (int64_t)kFusedChunks * 16 * 512) {
+    // for weight-only: x up to 64 KiB with the fused min/max (8 chunks per
+    // thread), up to 80 KiB after the min/max pre-pass (10 chunks per thread)
+    if (M >= 4 && Kc < 128 && Nt > 1024 && (Nt + 4) / 5 <= 256 && xb <= kSplitWideBytes) {
       *id = 7;
       *ks = 8;
     }
