@@ -1357,6 +1357,21 @@ int launch_gemm_w8a8_token(const void* x, int xt, int64_t M, int64_t K, int64_t 
                            int64_t ldy, int32_t* acc_out, int8_t* xq, float* s_t, hipStream_t st, bool yvec) {
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64, Kp = Kc * 64;
   if (Kp > ((int64_t)1 << 21)) return -1;  // 32-bit block offsets of the direct-to-LDS GEMM
+  if (M <= 16 && xvec && K % 64 == 0) {
+    // decode sizes with x of at most 8 chunks of 16 bytes per thread: one
+    // launch, the GEMV quantizing each row itself (the row quantizer's
+    // values, bit for bit); xq and s_t are not written
+    GemvArgs g{};
+    g.x = x; g.ldx = ldx; g.M = (int)M; g.K = (int)K; g.Kc = (int)Kc;
+    g.packed = packed; g.scale = scale; g.bias = bias;
+    g.N = (int)N; g.Nt = (int)Nt; g.y = y; g.yt = yt; g.ldy = ldy; g.acc_out = acc_out;
+    g.flags = kGemvXVec | (yvec ? kGemvYVec : 0) | kGemvPerToken;
+    int id = 0, ks = 0;
+    if (pick_gemv_fast(M, K, N, xt, true, true, &id, &ks)) {
+      const int frc = launch_gemv_fast_cfg(id, ks, g, xt, true, st);
+      if (frc != -1) return frc;
+    }
+  }
   int rc = launch_quantize_rows_sym(x, xt, ldx, xvec, M, K, Kp, xq, s_t, st);
   if (rc) return rc;
   if (M <= 16) {  // decode sizes: the HBM-streaming GEMV on the s8 rows

@@ -212,6 +212,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   }
   constexpr bool W8A8 = QM != 0;
   constexpr bool PT = QM == 3;
+  constexpr bool PTF = QM == 4;  // per-token, x quantized in the kernel
   static_assert(!PT || (XT == XT_S8 && !XL), "per-token: s8 fragments loaded directly");
   typedef typename std::conditional<W8A8, i32x4, f32x4>::type Acc;
   constexpr int EB = x_bytes<XT>();
@@ -245,7 +246,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   // QM 1 with five row tiles per workgroup: the (s_x, zp) of the pre-pass
   // partials quantize the thread's chunks of x, held in registers, the same way
   constexpr bool kQX1 = QM == 1 && G == 5;
-  constexpr bool kQXL = kQX || kQX1;  // s8 rows in LDS
+  constexpr bool kQXL = kQX || kQX1 || PTF;  // s8 rows in LDS
   const int xend = kQXL ? M * K : (XL && !kSplitReg ? xch * (int)blockDim.x * 16 : 0) + (kSplitX ? M * K * 4 : 0);
 
   // epilogue operands of row tile `ks` (wave ks < G finishes tile ks)
@@ -259,7 +260,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       const int nn = min(ne + v, a.N - 1);
       sc[v] = a.scale[nn];
       if (a.bias) bi[v] = a.bias[nn];
-      if constexpr (W8A8 && !PT) cs[v] = a.colsum[nn];
+      if constexpr (W8A8 && !PT && !PTF) cs[v] = a.colsum[nn];
     }
   }
   // W8A8: min/max partials of the activation pre-pass, or (QM 2) up to
@@ -267,10 +268,10 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   // of x are skipped (the condition is uniform over the workgroup), and the
   // clamped duplicates of a partial round are harmless
   float2 part = {0.f, 0.f};
-  u32x4 xmm[QM == 2 ? kFusedChunks : 1];
+  u32x4 xmm[QM == 2 || PTF ? kFusedChunks : 1];
   const int xm_nch = M * (K * EB / 16);  // QM 2: 16-byte chunks of x
   if constexpr (QM == 1) part = a.partials[min(tid, a.nparts - 1)];
-  if constexpr (QM == 2) {
+  if constexpr (QM == 2 || PTF) {
     const int cpr = K * EB / 16;
 #pragma unroll
     for (int i = 0; i < kFusedChunks; ++i) {
@@ -322,16 +323,30 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   for (int j = 0; j < G; ++j) wp[j] = a.packed + ((int64_t)min(nt0 + j, a.Nt - 1) * Kc + kbeg) * 1024 + lane * 16;
   const uint8_t* xp = xg + (int64_t)mr * a.ldx * EB + ((int64_t)kbeg * 64 + g * 16) * EB;
   u32x4 w[D][G];
-  XRaw<XT> xd[XL || kQX ? 1 : D];
+  XRaw<XT> xd[XL || kQXL ? 1 : D];
 #pragma unroll
   for (int p = 0; p < D; ++p) {
     const int kt = min(p, cnt - 1);
-    if constexpr (!XL && !kQX) load_frag<XT>(xd[p], xp + kt * 64 * EB);
+    if constexpr (!XL && !kQXL) load_frag<XT>(xd[p], xp + kt * 64 * EB);
 #pragma unroll
     for (int j = 0; j < G; ++j) w[p][j] = load_tile_nt(wp[j] + kt * 1024);
   }
 
+  // the 16 / EB activations of a 16-byte chunk of x as fp32
+  constexpr int NE = 16 / EB;
+  const auto chunk_vals = [](const u32x4& raw, float* v) {
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+      // copy the dword out first: a bit_cast of a vector-element lvalue
+      // reads element 0 with this compiler
+      const uint32_t word = raw[EB == 4 ? j : j / 2];
+      if constexpr (XT == XT_F32) v[j] = __uint_as_float(word);
+      else if constexpr (XT == XT_F16) v[j] = (float)__builtin_bit_cast(f16x2, word)[j & 1];
+      else v[j] = (float)__builtin_bit_cast(bf16x2, word)[j & 1];
+    }
+  };
   ActQParams qp = {};
+  float tok_s = 0.0f;  // PTF: the scale of row min(r, M - 1)
   if constexpr (XL || (W8A8 && !PT)) {
     if constexpr (QM == 2) {
       float mn = 0.0f, mx = 0.0f;
@@ -354,9 +369,31 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       }
       part = make_float2(mn, mx);
     }
-    if constexpr (W8A8) {
+    if constexpr (W8A8 && !PTF) {
       const float mn = wave_min(part.x), mx = wave_max(part.y);
       if (lane == 0) mmx[ks] = make_float2(mn, mx);
+    }
+    if constexpr (PTF) {
+      // per-row max |x| (the row quantizer's): per-wave maxima [KS][16] in
+      // the partial-tile area, unused until the main loop ends
+      float* rmx = (float*)smem;
+      const int cpr = K * EB / 16;
+      for (int m = 0; m < M; ++m) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kFusedChunks; ++i) {
+          if (i * (int)blockDim.x >= xm_nch) break;
+          const int c = min(tid + i * (int)blockDim.x, xm_nch - 1);
+          if (c >= m * cpr && c < (m + 1) * cpr) {
+            float v[NE];
+            chunk_vals(xmm[i], v);
+#pragma unroll
+            for (int j = 0; j < NE; ++j) mx = fmaxf(mx, __builtin_fabsf(v[j]));
+          }
+        }
+        mx = wave_max(mx);
+        if (lane == 0) rmx[ks * 16 + m] = mx;
+      }
     }
     if constexpr (XL) wait_vm<D * G>();  // this wave's x copies are in LDS; weights stay in flight
     if constexpr (!kSplitX) lds_barrier();  // (kSplitX: each thread first reads back only its own copies)
@@ -402,7 +439,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       }
       lds_barrier();
     }
-    if constexpr (W8A8) {
+    if constexpr (W8A8 && !PTF) {
       float mn = 0.0f, mx = 0.0f;
       for (int i = 0; i < KS; ++i) {
         const float2 v = mmx[i];
@@ -411,32 +448,47 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       }
       qp = choose_act_qparams(mn, mx);
     }
+    if constexpr (PTF) {  // s = max(max |x|, 1e-8) / 127, the IEEE division of the row quantizer
+      const float* rmx = (const float*)smem;
+      const int rr = min(r, M - 1);
+      float mx = rmx[rr];
+      for (int i = 1; i < KS; ++i) mx = fmaxf(mx, rmx[i * 16 + rr]);
+      tok_s = fmaxf(mx, 1e-8f) / 127.0f;
+    }
     if constexpr (kQXL) {
       // the s8 values xq - 128 of this thread's chunks (quant16's arithmetic:
-      // one fma and one pack per value), 16 / EB values per chunk
-      constexpr int NE = 16 / EB;
+      // one fma and one pack per value), 16 / EB values per chunk; per-token:
+      // clamp(rne(x / s), -127, 127), the row quantizer's values
       const int cpr = K * EB / 16;
       const auto quant_store = [&](const u32x4& raw, int c) {
         const int m = c / cpr;
         uint8_t* dst = xs + m * K + (c - m * cpr) * NE;
         float v[NE];
-#pragma unroll
-        for (int j = 0; j < NE; ++j) {
-          const uint32_t word = raw[EB == 4 ? j : j / 2];
-          if constexpr (XT == XT_F32) v[j] = __uint_as_float(word);
-          else if constexpr (XT == XT_F16) v[j] = (float)__builtin_bit_cast(f16x2, word)[j & 1];
-          else v[j] = (float)__builtin_bit_cast(bf16x2, word)[j & 1];
-        }
+        chunk_vals(raw, v);
         uint32_t d[NE / 4];
+        if constexpr (PTF) {
+          const float sr = __shfl(tok_s, m, 64);  // lane m holds row m's scale
 #pragma unroll
-        for (int j = 0; j < NE / 4; ++j)
-          d[j] = pack_act_s8x4(__builtin_fmaf(v[4 * j], qp.inv, qp.zpf), __builtin_fmaf(v[4 * j + 1], qp.inv, qp.zpf),
-                               __builtin_fmaf(v[4 * j + 2], qp.inv, qp.zpf),
-                               __builtin_fmaf(v[4 * j + 3], qp.inv, qp.zpf));
+          for (int j = 0; j < NE / 4; ++j) {
+            d[j] = 0u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float q = __builtin_rintf(v[4 * j + e] / sr);
+              q = fminf(fmaxf(q, -127.0f), 127.0f);
+              d[j] |= ((uint32_t)(int)q & 0xffu) << (8 * e);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < NE / 4; ++j)
+            d[j] = pack_act_s8x4(__builtin_fmaf(v[4 * j], qp.inv, qp.zpf), __builtin_fmaf(v[4 * j + 1], qp.inv, qp.zpf),
+                                 __builtin_fmaf(v[4 * j + 2], qp.inv, qp.zpf),
+                                 __builtin_fmaf(v[4 * j + 3], qp.inv, qp.zpf));
+        }
         if constexpr (NE == 4) *(uint32_t*)dst = d[0];
         else *(u32x2*)dst = (u32x2){d[0], d[1]};
       };
-      if constexpr (kQX) {
+      if constexpr (kQX || PTF) {
 #pragma unroll
         for (int i = 0; i < kFusedChunks; ++i) {
           if (i * (int)blockDim.x >= xm_nch) break;
@@ -496,7 +548,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
     for (int p = 0; p < D; ++p) {
       step(p, t + p);
       const int kt = min(t + D + p, cnt - 1);
-      if constexpr (!XL && !kQX) load_frag<XT>(xd[p], xp + kt * 64 * EB);
+      if constexpr (!XL && !kQXL) load_frag<XT>(xd[p], xp + kt * 64 * EB);
 #pragma unroll
       for (int j = 0; j < G; ++j) w[p][j] = load_tile_nt(wp[j] + kt * 1024);
       // keep each refill next to the step that freed its registers (otherwise
@@ -545,8 +597,8 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
     if constexpr (!kSplitX) s = tile_sum();
     const int nvalid = min(4, a.N - n);
     f32x4 o;
-    if constexpr (PT) {
-      const float st = a.rscale[r];
+    if constexpr (PT || PTF) {
+      const float st = PT ? a.rscale[r] : tok_s;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         if (a.acc_out && v < nvalid) a.acc_out[(int64_t)r * a.N + n + v] = s[v];
@@ -812,22 +864,25 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   if (split && a.M > 8) return -1;  // the two planes of a row share the 16 MFMA columns
   if (c.D * c.G > 32) return -1;
   const int T = ks * 64;
-  const int qm = !w8a8 ? 0 : (a.nparts > 0 ? 1 : 2);
-  const int xch = c.XL && qm != 2 && !split_reg && !qx1 ? (int)((xbytes / 16 + T - 1) / T) : 0;
+  // per-token W8A8 with x quantized in the kernel: QM 4
+  const int qm = !w8a8 ? 0 : ((a.flags & kGemvPerToken) ? 4 : (a.nparts > 0 ? 1 : 2));
+  if (qm == 4 && (a.M > 16 || a.nparts > 0)) return -1;
+  const int xch = c.XL && qm != 2 && qm != 4 && !split_reg && !qx1 ? (int)((xbytes / 16 + T - 1) / T) : 0;
   if ((split_reg || qx1) && (xbytes / 16 + T - 1) / T > kSplitRegChunks) return -1;  // the chunks each thread holds
   if (split && xch > kSplitChunks) return -1;  // the chunks of x each thread splits
   size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
   if (split) lds += (size_t)xbytes;               // bf16 high / remainder planes
-  if (qm == 2 || qx1) lds += (size_t)a.M * a.K;    // the quantized s8 rows
+  if (qm == 2 || qm == 4 || qx1) lds += (size_t)a.M * a.K;  // the quantized s8 rows
   if (a.flags & kGemvArgmax) lds += (size_t)c.G * 16 * 8;  // the fused argmax's keys per row tile
-  if (qm == 2 && xbytes > (int64_t)kFusedChunks * 16 * T) return -1;  // every thread holds its chunks of x
+  if ((qm == 2 || qm == 4) && xbytes > (int64_t)kFusedChunks * 16 * T) return -1;  // every thread holds its chunks of x
 #define SBQ_FAST_QM(XT_)                                                  \
   switch (qm) {                                                           \
     case 0:                                                               \
       return a.nseg > 1 ? launch_fast_typed<XT_, 0, true>(id, a, ks, KW, xch, lds, st) \
                         : launch_fast_typed<XT_, 0>(id, a, ks, KW, xch, lds, st);      \
     case 1: return launch_fast_typed<XT_, 1>(id, a, ks, KW, xch, lds, st); \
-    default: return launch_fast_typed<XT_, 2>(id, a, ks, KW, xch, lds, st); \
+    case 2: return launch_fast_typed<XT_, 2>(id, a, ks, KW, xch, lds, st); \
+    default: return launch_fast_typed<XT_, 4>(id, a, ks, KW, xch, lds, st); \
   }
   switch (xt) {
     case XT_F16: SBQ_FAST_QM(XT_F16)

@@ -59,6 +59,7 @@ constexpr int kArgmaxStateBytes = (kArgmaxSlots + 1) * kArgmaxSlotBytes;
 constexpr int kGemvXVec = 1;     // x rows 16-byte aligned: vector loads
 constexpr int kGemvYVec = 2;     // y rows aligned for 4-element vector stores
 constexpr int kGemvArgmax = 4;   // also pick each row's argmax (fused greedy token)
+constexpr int kGemvPerToken = 8; // W8A8 per-token symmetric, x quantized in the kernel (rows, M <= 16)
 
 // ---------------------------------------------------------------------------
 // Raw activations of one lane: x[m][k0 .. k0+15], m = mt*16 + r,

@@ -454,7 +454,8 @@ def test_w8a8_quantizer_ties(dev, M):
 
 @pytest.mark.parametrize("xd", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 64, 1000), (33, 512, 256), (128, 1024, 4096), (300, 130, 200),
-                                   (2048, 512, 4096)])
+                                   (2048, 512, 4096), (8, 4100, 2560), (16, 1000, 1024), (3, 6160, 4096),
+                                   (1, 19456, 2560), (2, 24, 64)])
 def test_w8a8_token_bitexact(dev, M, N, K, xd):
     """Per-token symmetric W8A8 (opt-in granularity): int32 accumulators and
     fp32 outputs bit-exact against the oracle, on every activation dtype,
@@ -470,6 +471,30 @@ def test_w8a8_token_bitexact(dev, M, N, K, xd):
     np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
     np.testing.assert_array_equal(y.cpu().numpy(), ref)
     np.testing.assert_array_equal(lin(x.to(dev)).cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("xd", ["f32", "f16"])
+def test_w8a8_token_rows_edge_cases(dev, xd):
+    """Per-token decode with each row quantized in the GEMV: a zero row (scale
+    1e-8 / 127), rows of tiny and huge magnitude and a row whose largest value
+    sits in its last column, bit-exact against the oracle with a bias."""
+    announce(f"w8a8 token edge rows x={xd}")
+    M, N, K = 6, 2000, 2560
+    w = make_weights(N, K, 3710)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(3711))
+    x = make_x(M, K, 3712)
+    x[0] = 0.0
+    x[1] *= 1e-30 if xd == "f32" else 1e-3
+    x[2] *= 1e30 if xd == "f32" else 1e3
+    x[4, K - 1] = 50.0
+    x = x.to(DT[xd])
+    q, s = oracle.quantize_per_channel(w.numpy())
+    ref, info = oracle.dyn_linear_token(x.float().numpy(), q, s, bias=b.numpy(), return_intermediates=True)
+    lin = quant.DynamicInt8Linear(w, b.to(dev), granularity="token")
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y = quant.linear_w8a8_token(x.to(dev), lin.packed, lin.scale, lin.bias, N, acc_out=acc)
+    np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
+    np.testing.assert_array_equal(y.cpu().numpy(), ref)
 
 
 def test_w8a8_token_bias_and_default_granularity(dev):
