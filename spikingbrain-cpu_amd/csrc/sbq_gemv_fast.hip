@@ -233,7 +233,11 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   // five row tiles per workgroup (one workgroup per CU, up to 256 VGPRs per
   // wave): x goes to registers and only the planes take LDS
   constexpr bool kSplitReg = kSplitX && G == 5;
-  uint8_t* xhi = xs + (kSplitReg ? 0 : xch * (int)blockDim.x * 16);  // kSplitX: bf16 planes [M][K] after the x copy
+  // otherwise each wave copies and splits only its own K range of x (the
+  // tiles it multiplies), in a region of its own: no workgroup barrier
+  constexpr bool kSplitWave = kSplitX && !kSplitReg;
+  const int sw_cap = (M * KW * 16 + 63) / 64 * 64;  // kSplitWave: 16-byte chunks per wave region
+  uint8_t* xhi = xs + (kSplitReg ? 0 : KS * sw_cap * 16);  // kSplitX: bf16 planes [M][K] after the x copies
   uint8_t* xlo = xhi + M * K * 2;
   // kSplitX (M <= 8): MFMA column r < 8 multiplies the high plane of row r,
   // column r + 8 the remainder plane of the same row; the epilogue adds the
@@ -247,7 +251,9 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
   // partials quantize the thread's chunks of x, held in registers, the same way
   constexpr bool kQX1 = QM == 1 && G == 5;
   constexpr bool kQXL = kQX || kQX1 || PTF;  // s8 rows in LDS
-  const int xend = kQXL ? M * K : (XL && !kSplitReg ? xch * (int)blockDim.x * 16 : 0) + (kSplitX ? M * K * 4 : 0);
+  const int xend = kQXL ? M * K
+                        : (kSplitX ? (kSplitReg ? 0 : KS * sw_cap * 16) + M * K * 4
+                                   : (XL ? xch * (int)blockDim.x * 16 : 0));
 
   // epilogue operands of row tile `ks` (wave ks < G finishes tile ks)
   const int nte = min(nt0 + min(ks, G - 1), a.Nt - 1);
@@ -306,6 +312,16 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
         const int m = c / K4;
         xr[i] = *(const f32x4*)(xg + ((int64_t)m * a.ldx + (c - m * K4) * 4) * 4);
       }
+    }
+  } else if constexpr (kSplitWave) {
+    // this wave's rows x[m][kbeg*64 .. (kbeg+cnt)*64): cnt * 16 chunks per row,
+    // 64 per copy into consecutive slots of the wave's region, sources clamped
+    const int cpw = cnt * 16, swn = M * cpw;
+    uint8_t* xw = xs + ks * sw_cap * 16;
+    for (int i = 0; i * 64 < swn; ++i) {
+      const int j = min(i * 64 + lane, swn - 1);
+      const int m = j / cpw;
+      lds_copy16(xg + ((int64_t)m * a.ldx + (int64_t)kbeg * 64 + (j - m * cpw) * 4) * 4, xw + i * 64 * 16);
     }
   } else if constexpr (XL && !kQXL) {
     const int cpr = xrow / 16, nch = M * cpr;
@@ -422,22 +438,34 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
           const int c = tid + i * T;
           if (i * T < xnch && c < xnch) split_store(xr[i], c);
         }
+        lds_barrier();
       } else {
+        // the lane's own copies (slot j = i * 64 + lane of the wave region),
+        // four at a time; chunk j is row j / (cnt * 16), element
+        // kbeg * 64 + 4 * (j % (cnt * 16)) of it
+        (void)raw;
+        (void)last;
+        const f32x4* rw = (const f32x4*)(xs + ks * sw_cap * 16);
+        const int cpw = cnt * 16, swn = M * cpw;
+        for (int b = 0; b * 64 < swn; b += 4) {
+          f32x4 v[4];
 #pragma unroll
-        for (int b = 0; b < kSplitChunks; b += 4) {
-          if (b * T < xnch) {  // uniform
-            f32x4 v[4];
+          for (int j = 0; j < 4; ++j) v[j] = rw[min((b + j) * 64 + lane, swn - 1)];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = raw[min(tid + (b + j) * T, last)];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int c = tid + (b + j) * T;
-              if (c < xnch) split_store(v[j], c);
+          for (int j = 0; j < 4; ++j) {
+            const int jj = (b + j) * 64 + lane;
+            if (jj < swn) {
+              const int m = jj / cpw;
+              split_store(v[j], (m * K + kbeg * 64) / 4 + (jj - m * cpw));
             }
           }
         }
+        // the wave reads back only planes its own lanes wrote (its K range):
+        // its LDS writes complete, no workgroup barrier
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        asm volatile("" ::: "memory");
       }
-      lds_barrier();
     }
     if constexpr (W8A8 && !PTF) {
       float mn = 0.0f, mx = 0.0f;
@@ -870,7 +898,8 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   const int xch = c.XL && qm != 2 && qm != 4 && !split_reg && !qx1 ? (int)((xbytes / 16 + T - 1) / T) : 0;
   if ((split_reg || qx1) && (xbytes / 16 + T - 1) / T > kSplitRegChunks) return -1;  // the chunks each thread holds
   if (split && xch > kSplitChunks) return -1;  // the chunks of x each thread splits
-  size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL ? (size_t)xch * T * 16 : 0);
+  size_t lds = (size_t)ks * c.G * 64 * 16 + mm_bytes() + (c.XL && !split ? (size_t)xch * T * 16 : 0);
+  if (split && !split_reg) lds += (size_t)ks * ((a.M * KW * 16 + 63) / 64 * 64) * 16;  // each wave's x copy
   if (split) lds += (size_t)xbytes;               // bf16 high / remainder planes
   if (qm == 2 || qm == 4 || qx1) lds += (size_t)a.M * a.K;  // the quantized s8 rows
   if (a.flags & kGemvArgmax) lds += (size_t)c.G * 16 * 8;  // the fused argmax's keys per row tile
