@@ -264,6 +264,65 @@ def test_random_prefill_picks_match_oracle(dev, i, M, N, K, xd, has_bias):
     np.testing.assert_array_equal(pick(y8, rows, cols), y_ref)
 
 
+def _random_decode_cases(n, seed):
+    """Seeded decode shapes: M 1..16 (mostly 1 and 4..8), K from the model's
+    (128, 2560, 4096, 9728, 12288), other multiples of 64 and a few ragged
+    ones, N up to 24576 (often wide enough for five row tiles per workgroup),
+    every activation dtype, with and without a bias."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        M = int(rng.choice([1, 1, 1, 2, 3, 4, 5, 6, 7, 8, 8, 12, 16]))
+        r = rng.random()
+        if r < 0.6:
+            K = int(rng.choice([128, 2560, 2560, 4096, 9728, 12288]))
+        elif r < 0.9:
+            K = 64 * int(rng.integers(1, 161))
+        else:
+            K = int(rng.integers(65, 4000))
+        N = int(rng.integers(16385, 24577)) if rng.random() < 0.4 and K < 8192 else int(rng.integers(1, 12289))
+        out.append((i, M, N, K, str(rng.choice(["f16", "bf16", "f32"])), bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i,M,N,K,xd,has_bias", _random_decode_cases(24, 2029))
+def test_random_decode_picks_match_oracle(dev, i, M, N, K, xd, has_bias):
+    """Whatever decode kernel and configuration the library picks (x in LDS or
+    direct fragments, one to five row tiles per workgroup, fused or pre-pass
+    min/max, per-token rows quantized in the GEMV or by the row quantizer):
+    W-only within 2e-5 (fp32 x: high + remainder keep 16 bits) or 1e-5, per-tensor
+    and per-token W8A8 acc and y bit-exact, on sampled output channels."""
+    announce(f"random decode {i}: M={M} N={N} K={K} x={xd} bias={has_bias}")
+    w = gpu_weight(N, K, 1800 + i, dev)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(1900 + i)) if has_bias else None
+    bd = None if b is None else b.to(dev)
+    lin = quant.Int8Linear(w, bd)
+    dyn = quant.DynamicInt8Linear(w, bd)
+    tok = quant.DynamicInt8Linear(w, bd, granularity="token")
+    cols = tile_sample(N, 2000 + i, cap=96)
+    q, s = ref_rows(w, cols)
+    del w
+    x = cpu_x(M, K, 2100 + i, outliers=True).to(DT[xd])
+    xv = x.float().numpy()
+    xg = x.to(dev)
+    rows = np.arange(M)
+    bc = None if b is None else b.numpy()[cols]
+    y = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N)
+    ref = oracle.int8_linear(xv, q, s, bc)
+    assert oracle.rel_l2(pick(y, rows, cols), ref) <= (2e-5 if xd == "f32" else 1e-5)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y8 = quant.linear_w8a8(xg, dyn.packed, dyn.scale, dyn.colsum, dyn.bias, N, acc_out=acc)
+    acc_ref, y_ref = ref_w8a8(xv, rows, q, s, bc)
+    c_ = torch.from_numpy(cols).to(dev)
+    np.testing.assert_array_equal(acc[:, c_].cpu().numpy(), acc_ref)
+    np.testing.assert_array_equal(pick(y8, rows, cols), y_ref)
+    y_t_ref, info = oracle.dyn_linear_token(xv, q, s, bias=bc, return_intermediates=True)
+    y_t = quant.linear_w8a8_token(xg, tok.packed, tok.scale, tok.bias, N, acc_out=acc)
+    np.testing.assert_array_equal(acc[:, c_].cpu().numpy(), info["acc"])
+    np.testing.assert_array_equal(pick(y_t, rows, cols), y_t_ref)
+
+
 # ---------------------------------------------------------------------------
 # the fused hybrid "reads-x" group (N = 18820)
 # ---------------------------------------------------------------------------
