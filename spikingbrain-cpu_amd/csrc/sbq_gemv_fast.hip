@@ -43,7 +43,7 @@ namespace sbq {
 namespace {
 
 constexpr int kFastXLdsBytes = 32768;  // x[M][K] copied to LDS up to this size
-constexpr int kFastXLdsWideBytes = 65536;  // ... with 5 row tiles per workgroup (one workgroup per CU)
+constexpr int kFastXLdsWideBytes = 81920;  // ... with 5 row tiles per workgroup (one workgroup per CU)
 constexpr int kFastMaxWaves = 8;
 constexpr int kFusedChunks = 8;         // QM 2: 16-byte chunks of x per thread (at most)
 constexpr int kFusedMinWaves = 4;       // W8A8 picks: 256 threads (QM 1: one min/max partial each)
@@ -1077,6 +1077,11 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     const bool wide = Kc <= 64 && Nt >= 384;
     *id = wide ? 5 : 3;  // D=8, G=2 | D=8, G=1
     *ks = 2;
+    // five row tiles per workgroup with x in LDS, as at M = 4 .. 8
+    if (!w8a8 && Kc < 128 && Nt > 1024 && (Nt + 4) / 5 <= 256 && M * K * 2 <= kFastXLdsWideBytes) {
+      *id = 7;  // D=2, G=5, x in LDS
+      *ks = 8;
+    }
   }
   if (w8a8) {
     // the activation min/max is reduced in the kernel for x <= 64 KiB (up to

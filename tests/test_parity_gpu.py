@@ -278,7 +278,7 @@ FAST_CASES = [
     (1, 4, 128), (1, 5120, 4096), (4, 4610, 2560), (7, 6100, 4096),
     # M = 4 .. 8 over more than 1024 row tiles at short K: five row tiles per
     # workgroup with x in LDS (ragged last workgroup; 1025 row tiles)
-    (8, 19456, 2560), (4, 18820, 2560), (6, 16400, 2560),
+    (8, 19456, 2560), (4, 18820, 2560), (6, 16400, 2560), (12, 19456, 2560), (16, 18820, 2560),
 ]
 
 
