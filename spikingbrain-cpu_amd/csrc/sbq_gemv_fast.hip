@@ -182,7 +182,9 @@ __device__ __forceinline__ void argmax_epilogue(uint8_t* state, int64_t* idx, un
 // QM: 0 weight-only; 1 W8A8 with the activation min/max partials of the
 // pre-pass; 2 W8A8 that reduces min/max over the whole (small) x itself;
 // 3 per-token symmetric W8A8 on pre-quantized s8 activations (XT_S8) with
-// per-row scales a.rscale.
+// per-row scales a.rscale; 4 per-token symmetric W8A8 that reduces each row's
+// max |x| and quantizes the rows itself.  QM 2 and 4 (and QM 1 with five row
+// tiles) quantize x once per workgroup into s8 rows in LDS.
 // GRP: grouped weight-only launch (a.nseg linears, see GemvArgs); a separate
 // instance, so that the single-linear kernels carry no segment lookup.
 template <int XT, int D, int G, bool XL, int QM, bool GRP = false>
