@@ -414,14 +414,14 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       }
     }
     if constexpr (XL) wait_vm<D * G>();  // this wave's x copies are in LDS; weights stay in flight
-    if constexpr (!kSplitX) lds_barrier();  // (kSplitX: each thread first reads back only its own copies)
+    if constexpr (!kSplitX) lds_barrier();  // (kSplitX: x from registers, or each wave's own copies)
     if constexpr (kSplitX) {
       // fp32 x: split once into bf16 high / remainder planes (hi + lo holds 16
-      // significant bits of each activation, at fp32's exponent range).  Each
-      // thread splits the chunks it copied itself (c = tid + i * T), reading
-      // them back four at a time with the reads issued together.
-      const f32x4* raw = (const f32x4*)xs;
-      const int T = blockDim.x, xnch = M * (K / 4), last = xch * T - 1;
+      // significant bits of each activation, at fp32's exponent range).
+      // Five-row-tile workgroups split the chunks their threads hold in
+      // registers (c = tid + i * T), then wait at a workgroup barrier; the
+      // other configurations split each wave's own K range (below).
+      const int T = blockDim.x, xnch = M * (K / 4);
       const auto split_store = [&](const f32x4& v, int c) {
         bf16x4 h, l;
 #pragma unroll
@@ -445,8 +445,6 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
         // the lane's own copies (slot j = i * 64 + lane of the wave region),
         // four at a time; chunk j is row j / (cnt * 16), element
         // kbeg * 64 + 4 * (j % (cnt * 16)) of it
-        (void)raw;
-        (void)last;
         const f32x4* rw = (const f32x4*)(xs + ks * sw_cap * 16);
         const int cpw = cnt * 16, swn = M * cpw;
         for (int b = 0; b * 64 < swn; b += 4) {
