@@ -398,7 +398,7 @@ def hybrid_stack_shapes(H=4096, F=12288, heads=32, kv_heads=8, d=128, routers=4,
 
 def grouped_stack_launches(H=4096, F=12288, heads=32, d=128):
     """The fused stack's launches with the independent pairs of each hybrid
-    layer grouped (sbq_linear_w8_grouped): lora_q[1] + lora_k[1] (two inputs
+    layer grouped (sbq_linear_w8_grouped / sbq_linear_w8a8_grouped): lora_q[1] + lora_k[1] (two inputs
     of K = 128) and sse_o + swa_o (two attention outputs of K = 4096).  Each
     launch is a list of (N, K); the weight bytes are the fused stack's."""
     pair_lora = [(heads * d, d), (heads * d, d)]
@@ -420,7 +420,7 @@ def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, 
     """One decode step through every quantized linear of the 36-layer hybrid
     model (hidden H, FFN F; H=2560, F=9728 is the reference's real checkpoint),
     one launch per linear, or fused / fused and grouped; w8a8: int8-dyn
-    linears (DynamicInt8Linear), one launch each (no grouped form)."""
+    linears (DynamicInt8Linear), fused, one launch each or grouped."""
     torch, quant = ctx.torch, ctx.quant
     launches = (grouped_stack_launches(H=H, F=F) if grouped
                 else [[sh] for sh in hybrid_stack_shapes(H=H, F=F, fused=fused)])
@@ -442,9 +442,14 @@ def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, 
 
         def step():
             for grp, lays, outs in plan:
-                if w8a8:
+                if w8a8 and len(grp) == 1:
                     (N, K), (packed, s, cs) = grp[0], lays[0]
                     quant.linear_w8a8(xs[K][0], packed, s, cs, None, N, workspace=wss[K], out=outs[0])
+                elif w8a8:
+                    K = grp[0][1]
+                    quant.linear_w8a8_grouped([xs[K][i] for i in range(len(grp))], [p for p, _, _ in lays],
+                                              [s for _, s, _ in lays], [c for _, _, c in lays], [None] * len(grp),
+                                              [N for N, _ in grp], outs=outs, workspace=wss[K])
                 elif len(grp) == 1:
                     (N, K), (packed, s, _) = grp[0], lays[0]
                     quant.linear_w8(xs[K][0], packed, s, None, N, out=outs[0])
@@ -826,9 +831,12 @@ def main():
               "stack_checkpoint_grouped": lambda ctx: stack_bench(ctx, Ms=sm, grouped=True, H=2560, F=9728),
               "stack_checkpoint_grouped_f32x": lambda ctx: stack_bench(ctx, Ms=sm, grouped=True, H=2560, F=9728,
                                                                        xdtype=ctx.torch.float32),
-              "stack_checkpoint_w8a8": lambda ctx: {xd: stack_bench(ctx, Ms=sm, fused=True, H=2560, F=9728, w8a8=True,
+              "stack_checkpoint_w8a8": lambda ctx: {xd: stack_bench(ctx, Ms=sm, grouped=True, H=2560, F=9728, w8a8=True,
                                                                     xdtype=getattr(ctx.torch, xd))
                                                     for xd in ("float16", "float32")},
+              "stack_checkpoint_w8a8_ungrouped": lambda ctx: {
+                  xd: stack_bench(ctx, Ms=sm, fused=True, H=2560, F=9728, w8a8=True, xdtype=getattr(ctx.torch, xd))
+                  for xd in ("float16", "float32")},
               "cpu_baseline": lambda ctx: cpu_baseline(args.cpu_budget)}[args.only]
         print(json.dumps({args.only: fn(ctx)}), flush=True)
         return
@@ -879,8 +887,8 @@ def main():
         extra["stack_checkpoint_grouped"] = stack_bench(ctx, grouped=True, H=2560, F=9728)
         log("the same step with fp32 activations, the reference model's own dtype")
         extra["stack_checkpoint_grouped_f32x"] = stack_bench(ctx, grouped=True, H=2560, F=9728, xdtype=torch.float32)
-        log("the same step in int8-dyn mode (DynamicInt8Linear), fused layers, fp16 and fp32 activations")
-        extra["stack_checkpoint_w8a8"] = {xd: stack_bench(ctx, fused=True, H=2560, F=9728, w8a8=True,
+        log("the same step in int8-dyn mode (DynamicInt8Linear), fused and grouped, fp16 and fp32 activations")
+        extra["stack_checkpoint_w8a8"] = {xd: stack_bench(ctx, grouped=True, H=2560, F=9728, w8a8=True,
                                                           xdtype=getattr(torch, xd)) for xd in ("float16", "float32")}
         torch.cuda.empty_cache()
 

@@ -208,6 +208,25 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
                     void* y, int y_dtype, int64_t ldy, int32_t* acc_out,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* `count` (1..SBQ_MAX_GROUP) independent int8-dyn linears of one M, K and
+ * dtypes: y_i = sbq_linear_w8a8(x_i, packed_i, scale_i, colsum_i, bias_i,
+ * N_i) for each i, every x_i quantized with its own (s_x, zp).  Arguments as
+ * in sbq_linear_w8_grouped, plus host arrays of the column sums (required)
+ * and one workspace of >= sbq_w8a8_workspace_bytes(M, K) bytes.  For decode
+ * shapes whose x fits the fused GEMV (each workgroup reduces its linear's
+ * min/max itself) the linears run as one launch; otherwise one by one as
+ * sbq_linear_w8a8, sharing the workspace in stream order.  Bit-exact with
+ * separate calls (integer accumulation).  No counterpart in the reference:
+ * it is for callers holding several independent int8-dyn projections of one
+ * step (model.py: the two lora up-projections, the SSE and SWA output
+ * projections of a hybrid layer). */
+int sbq_linear_w8a8_grouped(int count, const void* const* x, const int64_t* ldx, int x_dtype,
+                            int64_t M, int64_t K, const uint8_t* const* packed,
+                            const float* const* scale, const int32_t* const* colsum,
+                            const float* const* bias, const int64_t* N, void* const* y,
+                            const int64_t* ldy, int y_dtype, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* Largest quantized-activation scratch of sbq_linear_w8a8_noalloc:
  * M * ceil(K/64)*64 bytes must not exceed it (e.g. M = 2048 at K = 4096,
  * M = 512 at K = 12288). */

@@ -305,6 +305,51 @@ int sbq_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
                          ws_split_bytes(workspace, workspace_bytes, M, K), (hipStream_t)stream);
 }
 
+int sbq_linear_w8a8_grouped(int count, const void* const* x, const int64_t* ldx, int x_dtype, int64_t M, int64_t K,
+                            const uint8_t* const* packed, const float* const* scale, const int32_t* const* colsum,
+                            const float* const* bias, const int64_t* N, void* const* y, const int64_t* ldy,
+                            int y_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  if (count < 1 || count > SBQ_MAX_GROUP || !x || !ldx || !packed || !scale || !colsum || !N || !y || !ldy)
+    return SBQ_ERR_ARG;
+  bool xv = true, yv = true;
+  for (int i = 0; i < count; ++i) {
+    const int rc = check_linear(x[i], x_dtype, M, K, ldx[i], packed[i], scale[i], N[i], y[i], y_dtype, ldy[i]);
+    if (rc) return rc;
+    if (M > 0) {
+      if (!colsum[i]) return SBQ_ERR_ARG;
+      xv = xv && x_vec_ok(x[i], x_dtype, ldx[i]);
+      yv = yv && y_vec_ok(y[i], y_dtype, ldy[i], N[i]);
+    }
+  }
+  if (M == 0) return SBQ_OK;
+  if (!workspace || (int64_t)workspace_bytes < sbq_w8a8_workspace_bytes(M, K)) return SBQ_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  if (count > 1 && sbq::gemv_supports(M, K, true, x_dtype)) {
+    sbq::GemvSeg segs[SBQ_MAX_GROUP] = {};
+    for (int i = 0; i < count; ++i) {
+      segs[i].x = x[i];
+      segs[i].packed = packed[i];
+      segs[i].scale = scale[i];
+      segs[i].bias = bias ? bias[i] : nullptr;
+      segs[i].colsum = colsum[i];
+      segs[i].y = y[i];
+      segs[i].ldx = ldx[i];
+      segs[i].ldy = ldy[i];
+      segs[i].N = (int)N[i];
+      segs[i].Nt = (int)((N[i] + 15) / 16);
+    }
+    const int rc = sbq::launch_gemv_w8_grouped(segs, count, x_dtype, M, K, xv, y_dtype, yv, st, true);
+    if (rc != -1) return rc;
+  }
+  // one by one (stream order lets the calls share the workspace)
+  for (int i = 0; i < count; ++i) {
+    const int rc = sbq_linear_w8a8(x[i], x_dtype, M, K, ldx[i], packed[i], scale[i], colsum[i], bias ? bias[i] : nullptr,
+                                   N[i], y[i], y_dtype, ldy[i], nullptr, workspace, workspace_bytes, stream);
+    if (rc) return rc;
+  }
+  return SBQ_OK;
+}
+
 int sbq_linear_w8a8_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
                             const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y,
                             int y_dtype, int64_t ldy, int32_t* acc_out, void* stream) {

@@ -547,23 +547,24 @@ int launch_gemv_w8_mt(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, 
   return launch_gemv_mt(a, xt, st);
 }
 
-// Independent weight-only linears of one M, K and dtypes in one fast-path
-// launch (picked as one linear of their summed rows).  -1: the fast path does
-// not apply; the caller runs them one by one.
+// Independent linears of one M, K and dtypes in one fast-path launch (picked
+// as one linear of their summed rows): weight-only, or int8-dyn (w8a8: each
+// segment's colsum set) with the activation min/max reduced in the kernel.
+// -1: the fast path does not apply; the caller runs them one by one.
 int launch_gemv_w8_grouped(const GemvSeg* segs, int n, int xt, int64_t M, int64_t K, bool xvec, int yt, bool yvec,
-                           hipStream_t st) {
+                           hipStream_t st, bool w8a8) {
   if (n < 2 || n > kGemvMaxSeg) return -1;
   int64_t nt = 0;
   for (int i = 0; i < n; ++i) nt += segs[i].Nt;
   int fid, fks;
-  if (!pick_gemv_fast(M, K, nt * 16, xt, false, xvec, &fid, &fks)) return -1;
+  if (!pick_gemv_fast(M, K, nt * 16, xt, w8a8, xvec, &fid, &fks)) return -1;
   GemvArgs a{};
   a.M = (int)M; a.K = (int)K; a.Kc = (int)(K / 64);
   a.yt = yt;
   a.flags = (xvec ? kGemvXVec : 0) | (yvec ? kGemvYVec : 0);
   a.nseg = n;
   for (int i = 0; i < n; ++i) a.seg[i] = segs[i];
-  return launch_gemv_fast_grouped(fid, fks, a, xt, st);
+  return launch_gemv_fast_grouped(fid, fks, a, xt, w8a8, st);
 }
 
 int launch_gemv_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,

@@ -185,11 +185,12 @@ __device__ __forceinline__ void argmax_epilogue(uint8_t* state, int64_t* idx, un
 // per-row scales a.rscale; 4 per-token symmetric W8A8 that reduces each row's
 // max |x| and quantizes the rows itself.  QM 2 and 4 (and QM 1 with five row
 // tiles) quantize x once per workgroup into s8 rows in LDS.
-// GRP: grouped weight-only launch (a.nseg linears, see GemvArgs); a separate
+// GRP: grouped launch (a.nseg linears, see GemvArgs), weight-only or QM 2
+// (each workgroup reduces the min/max of its own linear's x); a separate
 // instance, so that the single-linear kernels carry no segment lookup.
 template <int XT, int D, int G, bool XL, int QM, bool GRP = false>
 __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs a, int KW, int xch) {
-  static_assert(!GRP || QM == 0, "grouped launches: weight-only");
+  static_assert(!GRP || QM == 0 || QM == 2, "grouped launches: weight-only or fused int8-dyn");
   int bid = blockIdx.x;
   if constexpr (GRP) {
     {  // this workgroup's linear (uniform); fields read at constant indexes
@@ -202,6 +203,7 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
           a.packed = a.seg[i].packed;
           a.scale = a.seg[i].scale;
           a.bias = a.seg[i].bias;
+          if constexpr (QM == 2) a.colsum = a.seg[i].colsum;
           a.y = a.seg[i].y;
           a.ldx = a.seg[i].ldx;
           a.ldy = a.seg[i].ldy;
@@ -910,7 +912,9 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
       return a.nseg > 1 ? launch_fast_typed<XT_, 0, true>(id, a, ks, KW, xch, lds, st) \
                         : launch_fast_typed<XT_, 0>(id, a, ks, KW, xch, lds, st);      \
     case 1: return launch_fast_typed<XT_, 1>(id, a, ks, KW, xch, lds, st); \
-    case 2: return launch_fast_typed<XT_, 2>(id, a, ks, KW, xch, lds, st); \
+    case 2:                                                               \
+      return a.nseg > 1 ? launch_fast_typed<XT_, 2, true>(id, a, ks, KW, xch, lds, st) \
+                        : launch_fast_typed<XT_, 2>(id, a, ks, KW, xch, lds, st);      \
     default: return launch_fast_typed<XT_, 4>(id, a, ks, KW, xch, lds, st); \
   }
   switch (xt) {
@@ -922,12 +926,13 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   return -2;
 }
 
-// Grouped weight-only launch of configuration `id`: a.seg[0 .. a.nseg) hold
-// the linears (x, weights, scales, bias, y, strides, N, Nt); every linear
+// Grouped launch of configuration `id`: a.seg[0 .. a.nseg) hold the linears
+// (x, weights, scales, bias, column sums, y, strides, N, Nt); every linear
 // gets ceil(Nt / G) workgroups of the grid, in segment order.  M, K, the
-// dtypes and the flags are shared.  Returns -1 when the configuration cannot
-// run the shape.
-int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, hipStream_t st) {
+// dtypes and the flags are shared.  w8a8: int8-dyn with the min/max of each
+// linear's x reduced in the kernel (QM 2; x within its fused capacity).
+// Returns -1 when the configuration cannot run the shape.
+int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, bool w8a8, hipStream_t st) {
   if (id < 0 || id >= kNumFastCfgs || a.nseg < 2 || a.nseg > kGemvMaxSeg) return -1;
   const int G = kFastCfgs[id].G;
   int64_t wg = 0;
@@ -942,7 +947,9 @@ int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, hipStream_t st)
   a.N = a.Nt * 16;
   a.x = a.seg[0].x;
   a.ldx = a.seg[0].ldx;
-  return launch_gemv_fast_cfg(id, ks, a, xt, false, st);
+  a.nparts = 0;
+  a.flags &= ~(kGemvArgmax | kGemvPerToken);
+  return launch_gemv_fast_cfg(id, ks, a, xt, w8a8, st);
 }
 
 // Decode over several 16-row tiles of x (gemv_mt_kernel): weight-only on fp16

@@ -16,6 +16,7 @@ struct GemvSeg {
   const uint8_t* packed;
   const float* scale;
   const float* bias;
+  const int32_t* colsum;  // int8-dyn: the weight column sums
   void* y;
   int64_t ldx, ldy;
   int N, Nt, wg0, pad;
@@ -45,7 +46,8 @@ struct GemvArgs {
   // it) and the int64 token per row
   uint8_t* am_state;
   int64_t* idx;
-  // grouped launch (weight-only fast path): nseg > 1 independent linears of
+  // grouped launch (fast path, weight-only or int8-dyn with the activation
+  // min/max reduced in the kernel): nseg > 1 independent linears of
   // the same M, K and dtypes; workgroup b belongs to the last segment s with
   // seg[s].wg0 <= b and takes its operands (the fields above describe none)
   int nseg;

@@ -43,13 +43,14 @@ int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st);
 int launch_gemv_w8_mt(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                       const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
                       bool yvec);
-// Grouped weight-only launch: a.seg / a.nseg hold 2..kGemvMaxSeg linears.
-int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, hipStream_t st);
-// n independent weight-only linears sharing M, K and dtypes in one launch
-// (x / weight / scale / bias / y / strides / N / Nt per segment); -1 when the
-// fast path does not apply.
+// Grouped launch: a.seg / a.nseg hold 2..kGemvMaxSeg linears (w8a8: int8-dyn
+// with the activation min/max reduced in the kernel).
+int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, bool w8a8, hipStream_t st);
+// n independent linears sharing M, K and dtypes in one launch (x / weight /
+// scale / bias / colsum / y / strides / N / Nt per segment), weight-only or
+// int8-dyn (w8a8); -1 when the fast path does not apply.
 int launch_gemv_w8_grouped(const GemvSeg* segs, int n, int xt, int64_t M, int64_t K, bool xvec, int yt, bool yvec,
-                           hipStream_t st);
+                           hipStream_t st, bool w8a8 = false);
 
 // Fused greedy token of the decode GEMV (fp32 y, M <= 16): the argmax state
 // (kArgmaxStateBytes, zero before a launch, zero again after it) and the

@@ -14,7 +14,7 @@ SBQ_OK = 0
 SBQ_F32, SBQ_F16, SBQ_BF16 = 0, 1, 2
 SBQ_NOALLOC_XQ_BYTES = 8 << 20  # include/sbq.h
 SBQ_ARGMAX_WS_BYTES = 16640  # include/sbq.h
-SBQ_MAX_GROUP = 4  # linears per sbq_linear_w8_grouped call (include/sbq.h)
+SBQ_MAX_GROUP = 4  # linears per sbq_linear_w8_grouped / sbq_linear_w8a8_grouped call (include/sbq.h)
 
 # Every entry point declared in include/sbq.h, with its ctypes signature.
 _P = ctypes.c_void_p
@@ -37,6 +37,7 @@ SIGNATURES = {
     "sbq_gemm_config": (_I, [_L, _L, _L, _I, _I, _P]),
     "sbq_act_qparams": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _S, _P]),
     "sbq_linear_w8a8": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _L, _P, _I, _L, _P, _P, _S, _P]),
+    "sbq_linear_w8a8_grouped": (_I, [_I, _P, _P, _I, _L, _L, _P, _P, _P, _P, _P, _P, _P, _I, _P, _S, _P]),
     "sbq_linear_w8a8_token": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _L, _P, _I, _L, _P, _P, _S, _P]),
     "sbq_linear_w8a8_noalloc": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _L, _P, _I, _L, _P, _P]),
     "sbq_argmax_rows": (_I, [_P, _L, _L, _L, _P, _P]),

@@ -217,9 +217,27 @@ def linear_w8_grouped(xs, packeds, scales, biases, Ns, out_dtype: torch.dtype = 
     summed rows (the per-launch ramp and tail paid once); other shapes run one
     by one.  Results can differ from separate calls in the fp32 summation
     order.  More than MAX_GROUP linears are split into groups."""
+    return _run_grouped("linear_w8_grouped", xs, packeds, scales, None, biases, Ns, out_dtype, outs, None)
+
+
+def linear_w8a8_grouped(xs, packeds, scales, colsums, biases, Ns, out_dtype: torch.dtype = torch.float32, outs=None,
+                        workspace: torch.Tensor | None = None):
+    """Independent int8-dyn linears of one step in one launch:
+    ys[i] = linear_w8a8(xs[i], packeds[i], scales[i], colsums[i], biases[i],
+    Ns[i]), each x quantized with its own (s_x, zp).
+
+    Shapes as in linear_w8_grouped.  Decode shapes whose x fits the fused
+    GEMV run as one launch; others run one by one, sharing `workspace`
+    (default: allocated for [M, K]).  Bit-exact with separate calls."""
+    return _run_grouped("linear_w8a8_grouped", xs, packeds, scales, colsums, biases, Ns, out_dtype, outs, workspace)
+
+
+def _run_grouped(name, xs, packeds, scales, colsums, biases, Ns, out_dtype, outs, workspace):
+    w8a8 = colsums is not None
     n = len(xs)
-    if not (len(packeds) == len(scales) == len(biases) == len(Ns) == n) or (outs is not None and len(outs) != n):
-        raise ValueError("linear_w8_grouped: the argument lists differ in length")
+    if not (len(packeds) == len(scales) == len(biases) == len(Ns) == n) or (outs is not None and len(outs) != n) \
+            or (w8a8 and len(colsums) != n):
+        raise ValueError(f"{name}: the argument lists differ in length")
     if n == 0:
         return []
     xs = [_as_activation(x) for x in xs]
@@ -227,54 +245,76 @@ def linear_w8_grouped(xs, packeds, scales, biases, Ns, out_dtype: torch.dtype = 
     dev, xdt = xs[0].device, xs[0].dtype
     for x in xs:
         if tuple(x.shape) != (M, K) or x.device != dev or x.dtype != xdt:
-            raise ValueError("linear_w8_grouped: every x must have the shape, dtype and device of xs[0]")
+            raise ValueError(f"{name}: every x must have the shape, dtype and device of xs[0]")
     ys = list(outs) if outs is not None else [torch.empty((M, N), dtype=out_dtype, device=dev) for N in Ns]
     ydt = ys[0].dtype
+    ws = None
+    if w8a8:
+        ws = workspace if workspace is not None else w8a8_workspace(M, K, dev)
     for i in range(n):
         if ys[i].dtype != ydt:
-            raise ValueError("linear_w8_grouped: every output must have one dtype")
-        _check_operands("linear_w8_grouped", xs[i], packeds[i], Ns[i], ys[i],
-                        (("scale", scales[i], torch.float32), ("bias", biases[i], torch.float32)))
+            raise ValueError(f"{name}: every output must have one dtype")
+        ops = (("scale", scales[i], torch.float32), ("bias", biases[i], torch.float32))
+        if w8a8:
+            ops += (("colsum", colsums[i], torch.int32),)
+        _check_operands(name, xs[i], packeds[i], Ns[i], ys[i], ops, ws)
     L = _lib.load()
     for g0 in range(0, n, MAX_GROUP):
         idx = range(g0, min(n, g0 + MAX_GROUP))
         c = len(idx)
         arr = lambda ctype, vals: (ctype * c)(*vals)  # noqa: E731
-        with torch.cuda.device(dev):
-            _lib.check(L.sbq_linear_w8_grouped(
-                c, arr(ctypes.c_void_p, [xs[i].data_ptr() for i in idx]), arr(ctypes.c_int64, [_ldx(xs[i]) for i in idx]),
+        head = (c, arr(ctypes.c_void_p, [xs[i].data_ptr() for i in idx]), arr(ctypes.c_int64, [_ldx(xs[i]) for i in idx]),
                 _code(xdt), M, K, arr(ctypes.c_void_p, [packeds[i].data_ptr() for i in idx]),
-                arr(ctypes.c_void_p, [scales[i].data_ptr() for i in idx]),
-                arr(ctypes.c_void_p, [0 if biases[i] is None else biases[i].data_ptr() for i in idx]),
+                arr(ctypes.c_void_p, [scales[i].data_ptr() for i in idx]))
+        tail = (arr(ctypes.c_void_p, [0 if biases[i] is None else biases[i].data_ptr() for i in idx]),
                 arr(ctypes.c_int64, [Ns[i] for i in idx]), arr(ctypes.c_void_p, [ys[i].data_ptr() for i in idx]),
-                arr(ctypes.c_int64, [ys[i].stride(0) for i in idx]), _code(ydt), _stream(dev)),
-                "sbq_linear_w8_grouped")
+                arr(ctypes.c_int64, [ys[i].stride(0) for i in idx]), _code(ydt))
+        with torch.cuda.device(dev):
+            if w8a8:
+                rc = L.sbq_linear_w8a8_grouped(*head, arr(ctypes.c_void_p, [colsums[i].data_ptr() for i in idx]),
+                                               *tail, _ptr(ws), _nbytes(ws), _stream(dev))
+            else:
+                rc = L.sbq_linear_w8_grouped(*head, *tail, _stream(dev))
+            _lib.check(rc, "sbq_" + name)
     return ys
 
 
 def grouped_forward(pairs):
-    """Outputs of several Int8Linear layers on their own inputs [(layer, x),
-    ...] as one grouped launch per MAX_GROUP layers: the drop-in for a model
-    step that holds independent projections (model.py: lora_q[1] / lora_k[1],
-    sse_o / swa_o of a hybrid layer).  Each output equals layer(x) to fp32
-    summation order.  Layers of other kinds, or inputs of differing shape,
-    run through their own forward."""
+    """Outputs of several Int8Linear layers, or several per-tensor
+    DynamicInt8Linear layers, on their own inputs [(layer, x), ...] as one
+    grouped launch per MAX_GROUP layers: the drop-in for a model step that
+    holds independent projections (model.py: lora_q[1] / lora_k[1], sse_o /
+    swa_o of a hybrid layer).  Each output equals layer(x) (Int8Linear: to
+    fp32 summation order; DynamicInt8Linear: bit for bit).  Mixed or other
+    kinds of layers, or inputs of differing shape, run through their own
+    forward."""
     layers = [m for m, _ in pairs]
     xs = [x for _, x in pairs]
-    if not pairs or not all(isinstance(m, Int8Linear) and m.qweight.is_cuda for m in layers):
+    if not pairs:
+        return []
+    if all(isinstance(m, Int8Linear) and m.qweight.is_cuda for m in layers):
+        dyn = False
+    elif all(isinstance(m, DynamicInt8Linear) and m.packed.is_cuda
+             and getattr(m, "granularity", "tensor") == "tensor" for m in layers):
+        dyn = True
+    else:
         return [m(x) for m, x in pairs]
-    shape0, dev = xs[0].shape, layers[0].qweight.device
-    if any(x.shape != shape0 or x.dtype != xs[0].dtype or x.device != dev or m.qweight.device != dev
-           or m.out_dtype != layers[0].out_dtype for m, x in pairs):
+    shape0, dev = xs[0].shape, layers[0].packed.device if dyn else layers[0].qweight.device
+    if any(x.shape != shape0 or x.dtype != xs[0].dtype or x.device != dev or m.out_dtype != layers[0].out_dtype
+           or (m.packed.device if dyn else m.qweight.device) != dev for m, x in pairs):
         return [m(x) for m, x in pairs]
     for m, x in pairs:
         _check_in_features(x, m.in_features)
-        m._refresh()
+        if not dyn:
+            m._refresh()
     x2s = [x.reshape(-1, shape0[-1]) for x in xs]
-    ys = linear_w8_grouped(x2s, [m.packed for m in layers],
-                           [m.scale if m.scale.dtype == torch.float32 else m.scale.float() for m in layers],
-                           [None if m.bias is None else m.bias.float() for m in layers],
-                           [m.out_features for m in layers], layers[0].out_dtype)
+    args = ([m.packed for m in layers], [m.scale if m.scale.dtype == torch.float32 else m.scale.float() for m in layers])
+    rest = ([None if m.bias is None else m.bias.float() for m in layers], [m.out_features for m in layers],
+            layers[0].out_dtype)
+    if dyn:
+        ys = linear_w8a8_grouped(x2s, *args, [m.colsum for m in layers], *rest)
+    else:
+        ys = linear_w8_grouped(x2s, *args, *rest)
     return [y.reshape(*shape0[:-1], -1) for y in ys]
 
 

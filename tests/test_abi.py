@@ -115,6 +115,23 @@ def test_argument_validation_without_gpu(lib):
     assert grouped(2, 1, 64, 64, 16, 16, xdt=7) == -2
     assert grouped(2, 1, 64, 64, 16, 16, packed=4097) == -3
     assert grouped(2, 0, 64, 64, 16, 16) == 0
+
+    # grouped int8-dyn linears: checked as sbq_linear_w8a8 checks one, and
+    # the column sums and the workspace are required
+    def grouped8(count, M, K, ldx, N, ldy, colsum=4096, ws=4096, ws_bytes=1 << 20):
+        n = max(count, 1)
+        return lib.sbq_linear_w8a8_grouped(count, arr(P, [4096] * n), arr(ctypes.c_int64, [ldx] * n), 0, M, K,
+                                           arr(P, [4096] * n), arr(P, [4096] * n), arr(P, [colsum] * n), None,
+                                           arr(ctypes.c_int64, [N] * n), arr(P, [4096] * n),
+                                           arr(ctypes.c_int64, [ldy] * n), 0, ws, ws_bytes, None)
+
+    assert grouped8(0, 1, 64, 64, 16, 16) == -1
+    assert grouped8(_lib.SBQ_MAX_GROUP + 1, 1, 64, 64, 16, 16) == -1
+    assert grouped8(2, 1, 64, 32, 16, 16) == -1       # ldx < K
+    assert grouped8(2, 1, 64, 64, 16, 16, colsum=None) == -1
+    assert grouped8(2, 1, 64, 64, 16, 16, ws=None) == -4
+    assert grouped8(2, 1, 64, 64, 16, 16, ws_bytes=16) == -4
+    assert grouped8(2, 0, 64, 64, 16, 16) == 0
     # row / column counts beyond 2^31 - 1 are rejected before any launch
     big = 1 << 31
     assert lib.sbq_linear_w8(dummy, 0, big, 64, 64, dummy, dummy, None, 16, dummy, 0, 16, None, 0, None) == -1

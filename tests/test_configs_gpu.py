@@ -866,12 +866,16 @@ def test_grouped_linears_graph_replays(dev):
     announce("grouped linears graph replays")
     K, Ns = 4096, (4096, 4096)
     lins = [quant.Int8Linear(gpu_weight(N, K, 940 + i, dev), None) for i, N in enumerate(Ns)]
+    dyns = [quant.DynamicInt8Linear(gpu_weight(N, K, 960 + i, dev), None) for i, N in enumerate(Ns)]
     xg = [cpu_x(1, K, 950 + i).half().to(dev) for i in range(len(Ns))]
-    outs = [torch.empty((1, N), dtype=torch.float16, device=dev) for N in Ns]
+    outs = [torch.empty((1, N), dtype=torch.float16, device=dev) for N in Ns * 2]
+    ws8 = quant.w8a8_workspace(1, K, dev)
 
-    def run():
+    def run():  # weight-only and int8-dyn groups
         quant.linear_w8_grouped(xg, [lin.packed for lin in lins], [lin.scale for lin in lins], [None, None],
-                                list(Ns), outs=outs)
+                                list(Ns), outs=outs[:2])
+        quant.linear_w8a8_grouped(xg, [d.packed for d in dyns], [d.scale for d in dyns], [d.colsum for d in dyns],
+                                  [None, None], list(Ns), outs=outs[2:], workspace=ws8)
 
     run()
     torch.cuda.synchronize()
@@ -891,6 +895,54 @@ def test_grouped_linears_graph_replays(dev):
         torch.cuda.synchronize()
         for o, e in zip(outs, eager):
             assert torch.equal(o, e)
+
+
+GROUP_W8A8_CASES = [
+    # (M, K, Ns, x dtype): int8-dyn pairs of the hybrid layer (one fused
+    # launch, each workgroup reducing its own linear's min/max), mixed and
+    # ragged widths, and shapes that run one by one: x beyond the fused
+    # capacity (M = 8 at K = 2560 in fp32) and M > 16
+    (1, 128, (4096, 4096), "f16"),
+    (1, 4096, (2560, 2560), "f32"),
+    (4, 4096, (1000, 64, 4096, 4), "bf16"),
+    (16, 4096, (2048, 6144), "f16"),
+    (1, 12288, (4096, 10), "f32"),
+    (8, 2560, (9728, 9728), "f16"),
+    (8, 2560, (4096, 4096), "f32"),
+    (24, 4096, (4096, 1000), "f16"),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,Ns,xd", GROUP_W8A8_CASES)
+def test_grouped_w8a8_linears(dev, M, K, Ns, xd):
+    """Each output of a grouped int8-dyn call equals its linear run alone bit
+    for bit (every x quantized with its own parameters), and the oracle's
+    outputs bit-exactly on sampled channels; grouped_forward on
+    DynamicInt8Linear layers returns what each layer's forward returns."""
+    announce(f"grouped w8a8 linears M={M} K={K} Ns={Ns} x={xd}")
+    ws = [gpu_weight(N, K, 2400 + i, dev) for i, N in enumerate(Ns)]
+    bs = [torch.randn(N, generator=torch.Generator().manual_seed(2420 + i)) if i % 2 else None
+          for i, N in enumerate(Ns)]
+    dyns = [quant.DynamicInt8Linear(w, None if b is None else b.to(dev)) for w, b in zip(ws, bs)]
+    xs = [(cpu_x(M, K, 2410 + i, outliers=True) * (1 + i)).to(DT[xd]) for i in range(len(Ns))]
+    xg = [x.to(dev) for x in xs]
+    for yd in (torch.float32, torch.float16):
+        got = quant.linear_w8a8_grouped(xg, [d.packed for d in dyns], [d.scale for d in dyns],
+                                        [d.colsum for d in dyns], [d.bias for d in dyns], list(Ns), yd)
+        for i, (d, N) in enumerate(zip(dyns, Ns)):
+            sep = quant.linear_w8a8(xg[i], d.packed, d.scale, d.colsum, d.bias, N, yd)
+            assert got[i].shape == (M, N) and got[i].dtype == yd
+            assert torch.equal(got[i], sep), (i, yd)
+            if yd == torch.float32:
+                cols = tile_sample(N, 2430 + i, cap=96)
+                q, s = ref_rows(ws[i], cols)
+                b = None if bs[i] is None else bs[i].numpy()[cols]
+                _, y_ref = ref_w8a8(xs[i].float().numpy(), np.arange(M), q, s, b)
+                np.testing.assert_array_equal(pick(got[i], np.arange(M), cols), y_ref)
+    outs = quant.grouped_forward(list(zip(dyns, xg)))
+    for d, x, o in zip(dyns, xg, outs):
+        assert torch.equal(o, d(x))
 
 
 # ---------------------------------------------------------------------------
