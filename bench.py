@@ -18,7 +18,8 @@ one decode step through all 539 linears of a random-init 36-layer hybrid
 model (hidden 4096, FFN 12288, vocab 151936) at M=1 and M=8, unfused and with
 the layers that read the same input fused (223 launches, same weight bytes),
 and fused and grouped (171 launches) at this model's and at the real
-checkpoint's sizes (hidden 2560, FFN 9728).
+checkpoint's sizes (hidden 2560, FFN 9728), the latter also with fp32
+activations and in int8-dyn mode.
 
 ``roofline`` covers the dominant kernel (the gate+up GEMV launch): its average
 duration is measured with HIP events around a graph of back-to-back launches
