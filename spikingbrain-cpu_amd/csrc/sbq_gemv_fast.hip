@@ -1047,8 +1047,10 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
   } else if (M <= 8) {
     // two row tiles per workgroup for wide layers; weight-only also from 257
     // row tiles, where one tile per workgroup needs a second round of the 256
-    // CUs (M = 1, N = 5120, K = 4096: 7.06 -> 5.87 us)
-    const bool wide = Kc < 128 && (Nt >= 384 || (!w8a8 && Nt > 256));
+    // CUs (M = 1, N = 5120, K = 4096: 7.06 -> 5.87 us), and so does W8A8 on
+    // more than 32 KiB of x, which every workgroup of the fused min/max reads
+    // whole: half the workgroups halve those reads
+    const bool wide = Kc < 128 && (Nt >= 384 || (Nt > 256 && (!w8a8 || M * K * 2 > 32768)));
     *id = wide ? 4 : 3;  // D=4, G=2 | D=8, G=1
     *ks = 4;
     if (!w8a8) {

@@ -909,6 +909,7 @@ GROUP_W8A8_CASES = [
     (1, 12288, (4096, 10), "f32"),
     (8, 2560, (9728, 9728), "f16"),
     (8, 2560, (4096, 4096), "f32"),
+    (8, 4096, (2560, 2560), "f16"),
     (24, 4096, (4096, 1000), "f16"),
 ]
 
