@@ -46,6 +46,7 @@ constexpr int kFastXLdsBytes = 32768;  // x[M][K] copied to LDS up to this size
 constexpr int kFastXLdsWideBytes = 81920;  // ... with 5 row tiles per workgroup (one workgroup per CU)
 constexpr int kFastMaxWaves = 8;
 constexpr int kFusedChunks = 8;         // QM 2: 16-byte chunks of x per thread (at most)
+constexpr int kFusedChunksWide = 10;    // ... fp32 x with five row tiles per workgroup (one 512-thread workgroup per CU)
 constexpr int kFusedMinWaves = 4;       // W8A8 picks: 256 threads (QM 1: one min/max partial each)
 constexpr int kFastSplitBytes = 49152;  // fp32 x split into bf16 planes in LDS up to this size
 constexpr int kSplitChunks = 12;        // fp32 x split: 16-byte chunks of x per thread (at most)
@@ -274,18 +275,22 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
     }
   }
   // W8A8: min/max partials of the activation pre-pass, or (QM 2) up to
-  // kFusedChunks 16-byte chunks of x per thread: chunk rounds past the end
-  // of x are skipped (the condition is uniform over the workgroup), and the
-  // clamped duplicates of a partial round are harmless
+  // FC 16-byte chunks of x per thread: chunk rounds past the end of x are
+  // skipped (the condition is uniform over the workgroup), and the clamped
+  // duplicates of a partial round are harmless
+  constexpr int FC = G == 5 && XT == XT_F32 ? kFusedChunksWide : kFusedChunks;
   float2 part = {0.f, 0.f};
-  u32x4 xmm[QM == 2 || PTF ? kFusedChunks : 1];
+  u32x4 xmm[QM == 2 || PTF ? FC : 1];
   const int xm_nch = M * (K * EB / 16);  // QM 2: 16-byte chunks of x
   if constexpr (QM == 1) part = a.partials[min(tid, a.nparts - 1)];
   if constexpr (QM == 2 || PTF) {
     const int cpr = K * EB / 16;
 #pragma unroll
-    for (int i = 0; i < kFusedChunks; ++i) {
-      if (i * (int)blockDim.x >= xm_nch) break;
+    for (int i = 0; i < FC; ++i) {
+      if (i * (int)blockDim.x >= xm_nch) {
+        if constexpr (FC > kFusedChunks) continue;  // a break moves xmm to scratch
+        else break;
+      }
       const int c = min(tid + i * (int)blockDim.x, xm_nch - 1);
       const int m = c / cpr;
       xmm[i] = *(const u32x4*)((const uint8_t*)a.x + (int64_t)m * a.ldx * EB + (c - m * cpr) * 16);
@@ -371,8 +376,11 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
     if constexpr (QM == 2) {
       float mn = 0.0f, mx = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kFusedChunks; ++i) {
-        if (i * (int)blockDim.x >= xm_nch) break;
+      for (int i = 0; i < FC; ++i) {
+        if (i * (int)blockDim.x >= xm_nch) {
+        if constexpr (FC > kFusedChunks) continue;  // a break moves xmm to scratch
+        else break;
+      }
         constexpr int NE = 16 / EB;
 #pragma unroll
         for (int j = 0; j < NE; ++j) {
@@ -401,8 +409,11 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       for (int m = 0; m < M; ++m) {
         float mx = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kFusedChunks; ++i) {
-          if (i * (int)blockDim.x >= xm_nch) break;
+        for (int i = 0; i < FC; ++i) {
+          if (i * (int)blockDim.x >= xm_nch) {
+        if constexpr (FC > kFusedChunks) continue;  // a break moves xmm to scratch
+        else break;
+      }
           const int c = min(tid + i * (int)blockDim.x, xm_nch - 1);
           if (c >= m * cpr && c < (m + 1) * cpr) {
             float v[NE];
@@ -520,8 +531,11 @@ __global__ __launch_bounds__(kFastMaxWaves * 64) void gemv_fast_kernel(GemvArgs 
       };
       if constexpr (kQX || PTF) {
 #pragma unroll
-        for (int i = 0; i < kFusedChunks; ++i) {
-          if (i * (int)blockDim.x >= xm_nch) break;
+        for (int i = 0; i < FC; ++i) {
+          if (i * (int)blockDim.x >= xm_nch) {
+        if constexpr (FC > kFusedChunks) continue;  // a break moves xmm to scratch
+        else break;
+      }
           quant_store(xmm[i], min(tid + i * (int)blockDim.x, xm_nch - 1));
         }
       } else {
@@ -870,7 +884,8 @@ int launch_fast_typed(int id, const GemvArgs& a, int ks, int KW, int xch, size_t
 // Launch of fast-path configuration `id` with `ks` waves per workgroup
 // (returns -1 when the configuration cannot run this shape).  W8A8 with
 // a.nparts == 0 reduces the activation min/max in the kernel (x must fit
-// kFusedChunks 16-byte chunks per thread of the workgroup).
+// kFusedChunks 16-byte chunks per thread of the workgroup, kFusedChunksWide for
+// fp32 x with five row tiles).
 int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, hipStream_t st) {
   if (id < 0 || id >= kNumFastCfgs || ks < 1 || ks > kFastMaxWaves) return -1;
   const FastCfg c = kFastCfgs[id];
@@ -905,7 +920,8 @@ int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, h
   if (split) lds += (size_t)xbytes;               // bf16 high / remainder planes
   if (qm == 2 || qm == 4 || qx1) lds += (size_t)a.M * a.K;  // the quantized s8 rows
   if (a.flags & kGemvArgmax) lds += (size_t)c.G * 16 * 8;  // the fused argmax's keys per row tile
-  if ((qm == 2 || qm == 4) && xbytes > (int64_t)kFusedChunks * 16 * T) return -1;  // every thread holds its chunks of x
+  if ((qm == 2 || qm == 4) && xbytes > (int64_t)(c.G == 5 && xt == XT_F32 ? kFusedChunksWide : kFusedChunks) * 16 * T)
+    return -1;  // every thread holds its chunks of x
 #define SBQ_FAST_QM(XT_)                                                  \
   switch (qm) {                                                           \
     case 0:                                                               \
@@ -1106,7 +1122,9 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     }
     // M = 4 .. 8 on a wide short-K layer: five row tiles per workgroup, as
     // for weight-only: x up to 64 KiB with the fused min/max (8 chunks per
-    // thread), up to 80 KiB after the min/max pre-pass (10 chunks per thread)
+    // thread; fp32 x up to 80 KiB, 10 chunks, so that M = 8 at K = 2560
+    // takes no pre-pass launch: checkpoint int8-dyn step 3036 -> 3240 tok/s),
+    // up to 80 KiB after the min/max pre-pass
     if (M >= 4 && Kc < 128 && Nt > 1024 && (Nt + 4) / 5 <= 256 && xb <= kSplitWideBytes) {
       *id = 7;
       *ks = 8;

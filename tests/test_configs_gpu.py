@@ -910,6 +910,7 @@ GROUP_W8A8_CASES = [
     (8, 2560, (9728, 9728), "f16"),
     (8, 2560, (4096, 4096), "f32"),
     (8, 4096, (2560, 2560), "f16"),
+    (8, 2560, (9728, 9728), "f32"), (6, 2560, (9000, 9000), "bf16"),
     (24, 4096, (4096, 1000), "f16"),
 ]
 
