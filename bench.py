@@ -290,6 +290,63 @@ def device_state_bench(ctx, fmt="int8", H=2048, F=5632, blocks=4, V=32000, heads
     return res
 
 
+def device_state_hybrid_bench(ctx, fmt="int8", steps=32, weights=None):
+    """Greedy decoding with the hybrid decoder of tests/hybrid_decoder.py
+    (our own model of the hybrid layer's launch pattern at the real
+    checkpoint's sizes: hidden 2560, FFN 9728, 32 heads of 128, 8 kv heads,
+    vocab 151936; layers hybrid, softmax, hybrid; random weights) over the
+    device-resident state of sbq.state, in three placements: the state on the
+    CPU (every projection copies x up and y back, the token by argmax on the
+    CPU), the state on the GPU with eager launches, and one HIP graph replay
+    per token.  Reports per-token time and tokens/s; the non-projection math
+    (recurrences, attention, norms) is plain torch."""
+    torch = ctx.torch
+    sys.path.insert(0, str(ROOT / "tests"))
+    from hybrid_decoder import Dims, HybridDecoder, SbqLinears, layer_shapes, make_weights
+
+    dm = Dims()
+    w, emb = weights if weights is not None else make_weights(dm)
+    lin = SbqLinears(fmt, w, emb, dm, ctx.dev)
+    wbytes = sum(N * K for i in range(len(dm.hybrid)) for N, K in layer_shapes(dm, i).values()) + dm.V * dm.H
+    res = {"fmt": fmt, "H": dm.H, "F": dm.F, "layers": "hybrid, softmax, hybrid", "vocab": dm.V, "steps": steps,
+           "linears_per_token": len(w) + 1, "weight_bytes_per_token": wbytes}
+
+    def per_token(run, n):
+        run(2)  # warm
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        run(n)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n
+
+    with torch.no_grad():
+        cpu = HybridDecoder(lin, emb, dm, "cpu")
+        cpu.reset(1)
+        res["cpu_state_ms_per_token"] = per_token(lambda n: [cpu.step() for _ in range(n)], min(steps, 8)) * 1e3
+        del cpu
+        gpu = HybridDecoder(lin, emb, dm, ctx.dev)
+        gpu.reset(1)
+        res["device_eager_ms_per_token"] = per_token(lambda n: [gpu.step() for _ in range(n)], steps) * 1e3
+        gpu.reset(1)
+        g = ctx.graph(gpu.step)
+        gpu.reset(1)
+        res["device_graph_ms_per_token"] = per_token(lambda n: [g.replay() for _ in range(n)], steps) * 1e3
+    for k in ("cpu_state", "device_eager", "device_graph"):
+        res[k + "_tokens_per_s"] = 1e3 / res[k + "_ms_per_token"]
+    res["device_graph_weight_GBps"] = wbytes / (res["device_graph_ms_per_token"] * 1e-3) / 1e9
+    del g, gpu, lin
+    return res
+
+
+def device_state_hybrid_both(ctx):
+    """device_state_hybrid_bench for int8 and int8-dyn on one set of weights."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from hybrid_decoder import Dims, make_weights
+
+    wts = make_weights(Dims())
+    return {f: device_state_hybrid_bench(ctx, f, weights=wts) for f in ("int8", "int8-dyn")}
+
+
 # ---------------------------------------------------------------------------
 # prefill GEMM and int8-dyn
 # ---------------------------------------------------------------------------
@@ -416,6 +473,41 @@ def grouped_stack_launches(H=4096, F=12288, heads=32, d=128):
     return out
 
 
+def stack_step(quant, launches, layers, xs, ys, wss, w8a8):
+    """The decode step of a stack as one function of launches: `launches` as
+    grouped_stack_launches / hybrid_stack_shapes give them, `layers` the
+    (packed, scale, colsum) of every linear in launch order, xs[K] two
+    [M, K] inputs per K (a grouped pair reads both; single launches read the
+    first), ys the output of every linear, wss[K] the int8-dyn workspaces.
+    The bench times it and the GPU tests check every output it writes
+    against the oracle."""
+    plan, j = [], 0
+    for grp in launches:
+        plan.append((grp, layers[j:j + len(grp)], ys[j:j + len(grp)]))
+        j += len(grp)
+
+    def step():
+        for grp, lays, outs in plan:
+            if w8a8 and len(grp) == 1:
+                (N, K), (packed, s, cs) = grp[0], lays[0]
+                quant.linear_w8a8(xs[K][0], packed, s, cs, None, N, workspace=wss[K], out=outs[0])
+            elif w8a8:
+                K = grp[0][1]
+                quant.linear_w8a8_grouped([xs[K][i] for i in range(len(grp))], [p for p, _, _ in lays],
+                                          [s for _, s, _ in lays], [c for _, _, c in lays], [None] * len(grp),
+                                          [N for N, _ in grp], outs=outs, workspace=wss[K])
+            elif len(grp) == 1:
+                (N, K), (packed, s, _) = grp[0], lays[0]
+                quant.linear_w8(xs[K][0], packed, s, None, N, out=outs[0])
+            else:
+                K = grp[0][1]
+                quant.linear_w8_grouped([xs[K][i] for i in range(len(grp))], [p for p, _, _ in lays],
+                                        [s for _, s, _ in lays], [None] * len(grp), [N for N, _ in grp],
+                                        outs=outs)
+
+    return step
+
+
 def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, H=4096, F=12288, xdtype=None,
                 w8a8=False):
     """One decode step through every quantized linear of the 36-layer hybrid
@@ -436,29 +528,7 @@ def stack_bench(ctx, Ms=(1, 8), steps=10, warmup=3, fused=False, grouped=False, 
                 xs[K] = [ctx.act(M, K, 3000 + K, xdtype), ctx.act(M, K, 3500 + K, xdtype)]  # a grouped pair reads two inputs
         ys = [torch.empty((M, N), dtype=torch.float16, device=ctx.dev) for N, K in shapes]
         wss = {K: quant.w8a8_workspace(M, K, ctx.dev, None, xs[K][0].dtype) for K in xs} if w8a8 else {}
-        plan, j = [], 0
-        for grp in launches:
-            plan.append((grp, layers[j:j + len(grp)], ys[j:j + len(grp)]))
-            j += len(grp)
-
-        def step():
-            for grp, lays, outs in plan:
-                if w8a8 and len(grp) == 1:
-                    (N, K), (packed, s, cs) = grp[0], lays[0]
-                    quant.linear_w8a8(xs[K][0], packed, s, cs, None, N, workspace=wss[K], out=outs[0])
-                elif w8a8:
-                    K = grp[0][1]
-                    quant.linear_w8a8_grouped([xs[K][i] for i in range(len(grp))], [p for p, _, _ in lays],
-                                              [s for _, s, _ in lays], [c for _, _, c in lays], [None] * len(grp),
-                                              [N for N, _ in grp], outs=outs, workspace=wss[K])
-                elif len(grp) == 1:
-                    (N, K), (packed, s, _) = grp[0], lays[0]
-                    quant.linear_w8(xs[K][0], packed, s, None, N, out=outs[0])
-                else:
-                    quant.linear_w8_grouped([xs[K][i] for i, (N, K) in enumerate(grp)], [p for p, _, _ in lays],
-                                            [s for _, s, _ in lays], [None] * len(grp), [N for N, _ in grp],
-                                            outs=outs)
-
+        step = stack_step(quant, launches, layers, xs, ys, wss, w8a8)
         g = ctx.graph(step)
         ms = ctx.time_graphs([g], steps, warmup)
         nbytes = sum(gemv_bytes(M, N, K) for N, K in shapes)
@@ -821,6 +891,7 @@ def main():
     if args.only:
         sm = tuple(args.stack_m)
         fn = {"lm_head_greedy": lm_head_greedy_bench, "device_state": device_state_bench,
+              "device_state_hybrid": device_state_hybrid_both,
               "stack_fused": lambda ctx: stack_bench(ctx, Ms=sm, fused=True),
               "w8a8_token": lambda ctx: [w8a8_bench(ctx, M, N, token=True) for M in (1, 128, 2048)
                                          for N in (4096, 12288)],
@@ -874,6 +945,8 @@ def main():
         extra["lm_head_greedy"] = lm_head_greedy_bench(ctx)
         log("device-resident decode (toy decoder)")
         extra["device_state"] = device_state_bench(ctx)
+        log("device-resident decode, hybrid layer pattern at the checkpoint's sizes")
+        extra["device_state_hybrid"] = device_state_hybrid_both(ctx)
         log("int8-dyn")
         extra["w8a8"] = [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)]
         log("int8-dyn, per-token symmetric activations (opt-in)")
@@ -896,6 +969,12 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
 
     pre2048 = next((p for p in extra.get("prefill", []) if p["M"] == 2048), None)
+
+    def gemv_4096(key):  # the single 4096x4096 GEMV at M=1 (the metric's quoted shape)
+        r = extra.get(key)
+        return None if r is None else {"us": round(r["ms_per_step"] * 1e3, 3), "GBps": round(r["GBps"], 1),
+                                       "hbm_frac": round(r["hbm_frac"], 4)}
+
     line = {
         "metric": METRIC,
         "value": round(head["GBps"], 2),
@@ -916,6 +995,8 @@ def main():
             "hbm_frac": round(head["hbm_frac"], 4),
             "prefill_M2048_TFLOPs": None if pre2048 is None else round(pre2048["TFLOPs"], 1),
             "prefill_M2048_mfma_frac": None if pre2048 is None else round(pre2048["mfma_frac"], 4),
+            "gemv_4096x4096_M1_f16x": gemv_4096("gemv_4096_f16x"),
+            "gemv_4096x4096_M1_f32x": gemv_4096("gemv_4096_f32x"),
         },
         "roofline": {
             "bound": "hbm",

@@ -89,28 +89,34 @@ inline int64_t ws_split_bytes(void* workspace, size_t workspace_bytes, int64_t M
 // activation min/max partials, (s_x, zp), then the quantized activations.
 // Host code never passes the array's name to a kernel (on the host it is a
 // stand-in, not a device address): the device address comes from
-// hipGetSymbolAddress, looked up once per device with that device current.
+// hipGetSymbolAddress with that device current, kept per device once a
+// lookup has succeeded.
 // ---------------------------------------------------------------------------
 constexpr int64_t kNoAllocHead = kWsPartialBytes + kWsQpBytes;
 static_assert(kNoAllocHead % 256 == 0, "xq starts 256-byte aligned");
 __device__ __align__(256) uint8_t scratch[kNoAllocHead + SBQ_NOALLOC_XQ_BYTES];
 
 constexpr int kMaxDevices = 64;
-std::once_flag g_scratch_once[kMaxDevices];
-void* g_scratch_ptr[kMaxDevices];
-int g_scratch_rc[kMaxDevices];
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];  // null until a lookup on that device succeeded
 
-// Device address of this GPU's scratch array (the current device's).
+// Device address of this GPU's scratch array (the current device's).  Only
+// a successful lookup is kept: a failed one (for instance a first call made
+// while the stream is being captured, where the runtime may refuse the
+// query) returns SBQ_ERR_LAUNCH and the next call looks again.
 int scratch_ptr(void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SBQ_ERR_DEVICE;
-  std::call_once(g_scratch_once[dev], [dev] {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();  // clear the sticky error state of the failed query
+      return SBQ_ERR_LAUNCH;
+    }
     g_scratch_ptr[dev] = p;
-    g_scratch_rc[dev] = (e == hipSuccess && p != nullptr) ? SBQ_OK : SBQ_ERR_LAUNCH;
-  });
-  if (g_scratch_rc[dev] != SBQ_OK) return g_scratch_rc[dev];
+  }
   *out = g_scratch_ptr[dev];
   return SBQ_OK;
 }

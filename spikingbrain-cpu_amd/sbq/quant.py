@@ -827,13 +827,16 @@ class FusedLinear(_Fp32Buffers, nn.Module):
     same x, exact int32 sums), int8 outputs agree to fp32 summation order.
 
     forward(x) returns one tensor per part (contiguous, like the parts').
-    part(i) is a drop-in module for part i: the parts share the result of one
-    launch for the same input tensor.  The shared result is reused while x is
-    the same tensor object at the same address with the same version counter.
-    Inference tensors (torch.inference_mode, as model.py:427 runs the model)
-    carry no version counter: for them an in-place edit of x between two
-    parts' calls is not detected.  Scales and bias stay fp32 under .half() /
-    .to(dtype)."""
+    part(i) is a drop-in module for part i: the parts of one call sequence
+    share the result of one launch.  The first part called on an input
+    launches; the other parts called on the same tensor object (same address,
+    same version counter) take their outputs from that launch, and once every
+    part has taken its output the shared result is dropped, so a part called
+    again (the next step, or the same part twice) launches anew.  Inference
+    tensors (torch.inference_mode, as model.py:427 runs the model) carry no
+    version counter: for them an in-place edit of x between two parts' calls
+    of one sequence is not detected.  Scales and bias stay fp32 under
+    .half() / .to(dtype)."""
 
     _fp32_buffers = ("scale", "bias")
 
@@ -868,6 +871,7 @@ class FusedLinear(_Fp32Buffers, nn.Module):
         self._memo_ref = None
         self._memo_key = None
         self._memo_out = None
+        self._memo_taken = set()
 
     def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, ...]:
         _check_in_features(x, self.in_features)
@@ -885,14 +889,23 @@ class FusedLinear(_Fp32Buffers, nn.Module):
         outs = torch.split(y, self.sizes, dim=-1)
         return tuple(o.contiguous().reshape(*shape[:-1], -1) for o in outs)
 
-    def _shared(self, x: torch.Tensor) -> tuple[torch.Tensor, ...]:
+    def _shared(self, x: torch.Tensor, i: int) -> torch.Tensor:
+        """Part i's output for x from the launch of the current call
+        sequence, launching when there is none for x or part i already took
+        its output from it."""
         ref = self._memo_ref() if self._memo_ref is not None else None
         # inference tensors raise on ._version: their key is the address only
         key = (x.data_ptr(), -1 if x.is_inference() else x._version)
-        if ref is not x or key != self._memo_key:
+        if ref is not x or key != self._memo_key or i in self._memo_taken:
             out = self.forward(x)
             self._memo_ref, self._memo_key, self._memo_out = weakref.ref(x), key, out
-        return self._memo_out
+            self._memo_taken = set()
+        out = self._memo_out[i]
+        self._memo_taken.add(i)
+        if len(self._memo_taken) == len(self.sizes):  # every part has its output: the sequence is over
+            self._memo_ref = self._memo_key = self._memo_out = None
+            self._memo_taken = set()
+        return out
 
     def part(self, i: int) -> nn.Module:
         return _FusedPart(self, i)
@@ -909,7 +922,7 @@ class _FusedPart(nn.Module):
         self.out_features = fused.sizes[i]
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self._fused[0]._shared(x)[self.index]
+        return self._fused[0]._shared(x, self.index)
 
 
 def fuse_linears(parts: list[nn.Module]) -> FusedLinear:

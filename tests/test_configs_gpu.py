@@ -360,6 +360,32 @@ def test_fused_hybrid_group_vs_oracle(dev, fmt, M):
             np.testing.assert_array_equal(po.cpu().numpy(), o.cpu().numpy())
 
 
+@pytest.mark.gpu
+def test_fused_parts_share_one_launch_per_call_sequence(dev):
+    """FusedLinear.part(i) drop-ins under torch.inference_mode() (inference
+    tensors carry no version counter): the parts of one call sequence share
+    one launch; once every part has taken its output, the next call launches
+    again, so an in-place edit of x between two sequences is seen; a part
+    called twice in one sequence launches anew as well."""
+    announce("fused parts: one launch per call sequence")
+    K = 512
+    mods = [quant.make_linear("int8", gpu_weight(n, K, 70 + i, dev)) for i, n in enumerate((64, 32))]
+    fused = quant.fuse_linears(mods)
+    p0, p1 = fused.part(0), fused.part(1)
+    with torch.inference_mode():
+        x = cpu_x(1, K, 71).to(dev)
+        a0, a1 = p0(x), p1(x)
+        for a, m in ((a0, mods[0]), (a1, mods[1])):
+            assert oracle.rel_l2(a.cpu().numpy(), m(x).cpu().numpy()) <= 1e-6
+        x.mul_(2.0)  # in place: doubles every product and sum exactly
+        b0, b1 = p0(x), p1(x)
+        assert torch.equal(b0, 2 * a0) and torch.equal(b1, 2 * a1)
+        c0 = p0(x)
+        x.mul_(0.5)
+        c0_again = p0(x)  # part 0 already took its output from the launch before the edit
+        assert torch.equal(c0, b0) and torch.equal(c0_again, a0)
+
+
 # ---------------------------------------------------------------------------
 # one decode step through the 539 quantized linears of the 36-layer model
 # ---------------------------------------------------------------------------
@@ -430,6 +456,99 @@ def test_decode_step_539_linears(dev, fmt):
                 _, y_ref = ref_w8a8(x, np.arange(M), q, s)
                 np.testing.assert_array_equal(got, y_ref, err_msg=f"{name} M={M}")
     del mods
+
+
+def _check_f16_out(got16, ref32, xd, fmt, what):
+    """fp16 outputs (what the stack step writes) against the oracle's fp32
+    result: int8-dyn bit-exact after the one rounding to fp16; weight-only
+    for fp16 inputs (which the kernels use exactly) within one fp16 ulp of the
+    rounded oracle plus W8_TOL_EXACT_X of the row's largest output (the fp32
+    summation order moves an output by about that much in absolute terms,
+    which is several ulps of an output near zero); rel-L2 <= 1e-3 for fp32
+    inputs (bf16 high + remainder planes)."""
+    ref16 = ref32.astype(np.float16)
+    if fmt == "int8-dyn":
+        np.testing.assert_array_equal(got16.view(np.uint16), ref16.view(np.uint16), err_msg=what)
+    elif xd == torch.float16:
+        bar = np.spacing(np.abs(ref16)).astype(np.float32) + W8_TOL_EXACT_X * np.abs(ref32).max(axis=1, keepdims=True)
+        assert np.all(np.abs(got16.astype(np.float32) - ref16.astype(np.float32)) <= bar), what
+    else:
+        assert oracle.rel_l2(got16, ref32) <= W8_TOL, what
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("model", ["bench36", "checkpoint"])
+def test_grouped_stack_step_vs_oracle(dev, model):
+    """The fused and grouped decode step the bench's stack figures come from
+    (bench.grouped_stack_launches, run by bench.stack_step exactly as the
+    bench runs it: 171 launches for 539 linears) at the 36-layer benchmark
+    model's sizes (hidden 4096, FFN 12288) and at the real checkpoint's
+    (hidden 2560, FFN 9728), at M = 1 and 8, fp16 and fp32 activations, both
+    formats, eager and replayed from a HIP graph: every linear's fp16 output
+    against the oracle on up to 48 sampled output channels (one per sampled
+    16-row tile, all M rows); int8-dyn bit-exact (the activation parameters
+    of each whole input), weight-only within the weight-only bars."""
+    import bench
+
+    H, F = (4096, 12288) if model == "bench36" else (2560, 9728)
+    launches = bench.grouped_stack_launches(H=H, F=F)
+    shapes = [sh for grp in launches for sh in grp]
+    assert len(shapes) == 223 and len(launches) == 171
+    announce(f"grouped stack step {model}: building {len(shapes)} linears")
+    layers, refs = [], []
+    for i, (N, K) in enumerate(shapes):
+        w = gpu_weight(N, K, 3000 + i, dev)
+        q, s = quant.quantize_per_channel_gpu(w)
+        packed, cs = quant.repack(q, with_colsum=True)
+        cols = tile_sample(N, i, cap=48)
+        layers.append((packed, s, cs))
+        refs.append((cols, *ref_rows(w, cols)))
+        del w, q
+    # the input each linear reads: single launches xs[K][0], member j of a
+    # grouped launch xs[K][j]
+    which = [j if len(grp) > 1 else 0 for grp in launches for j in range(len(grp))]
+    torch.cuda.synchronize()
+    for fmt in ("int8", "int8-dyn"):
+        for M in (1, 8):
+            for xd in (torch.float16, torch.float32):
+                announce(f"grouped stack step {model} fmt={fmt} M={M} x={xd}")
+                xs = {K: [cpu_x(M, K, 60 + K % 97).to(xd).to(dev), cpu_x(M, K, 61 + K % 89).to(xd).to(dev)]
+                      for K in {k for _, k in shapes}}
+                ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for N, _ in shapes]
+                w8a8 = fmt == "int8-dyn"
+                wss = {K: quant.w8a8_workspace(M, K, dev, None, xd) for K in xs} if w8a8 else {}
+                step = bench.stack_step(quant, launches, layers, xs, ys, wss, w8a8)
+                for mode in ("eager", "graph"):
+                    for y in ys:
+                        y.fill_(float("nan"))
+                    if mode == "eager":
+                        step()
+                    else:
+                        s = torch.cuda.Stream()
+                        s.wait_stream(torch.cuda.current_stream())
+                        with torch.cuda.stream(s):
+                            step()
+                        torch.cuda.current_stream().wait_stream(s)
+                        g = torch.cuda.CUDAGraph()
+                        with torch.cuda.graph(g):
+                            step()
+                        for y in ys:
+                            y.fill_(float("nan"))
+                        g.replay()
+                    torch.cuda.synchronize()
+                    xh = {K: [v.float().cpu().numpy() for v in pair] for K, pair in xs.items()}
+                    for i, ((N, K), (cols, q, s), y) in enumerate(zip(shapes, refs, ys)):
+                        x = xh[K][which[i]]
+                        got = y[:, torch.from_numpy(cols).to(dev)].cpu().numpy()
+                        if w8a8:
+                            _, ref = ref_w8a8(x, np.arange(M), q, s)
+                        else:
+                            ref = oracle.int8_linear(x, q, s)
+                        _check_f16_out(got, ref, xd, fmt, f"{model} {fmt} M={M} {xd} {mode} linear {i} ({N}x{K})")
+                    if mode == "graph":
+                        del g
+                del ys, wss, xs
+    del layers
 
 
 # ---------------------------------------------------------------------------
@@ -900,8 +1019,11 @@ def test_grouped_linears_graph_replays(dev):
 GROUP_W8A8_CASES = [
     # (M, K, Ns, x dtype): int8-dyn pairs of the hybrid layer (one fused
     # launch, each workgroup reducing its own linear's min/max), mixed and
-    # ragged widths, and shapes that run one by one: x beyond the fused
-    # capacity (M = 8 at K = 2560 in fp32) and M > 16
+    # ragged widths, and shapes that run one by one.  M = 8 at K = 2560 in
+    # fp32 (80 KiB of x) runs as one fused five-row-tile launch (10 chunks per
+    # thread) when the pair has enough row tiles, (9728, 9728); with
+    # (4096, 4096) it exceeds the fused capacity of the other configurations
+    # and runs one by one, as M > 16 does
     (1, 128, (4096, 4096), "f16"),
     (1, 4096, (2560, 2560), "f32"),
     (4, 4096, (1000, 64, 4096, 4), "bf16"),

@@ -824,6 +824,75 @@ def test_from_quantized_and_safetensors_roundtrip(dev, tmp_path):
         quant.load_quantized(path, "float8")
 
 
+# (N, K, weight dtype, bias): ragged N and K (neither a multiple of the 16 x 64
+# tile), a tile-aligned layer, and bf16 weights as loader.py:40,49 hands them
+# to make_linear
+SAVED_LAYERS = [(77, 200, "f32", True), (130, 4100, "bf16", False), (64, 256, "f32", False),
+                (1000, 2560, "bf16", True)]
+
+
+def test_saved_file_matches_oracle_quantization(dev, tmp_path):
+    """The on-disk pre-quantized format against the oracle, not against this
+    build's own layers: every <name>.qweight / <name>.scale in a
+    save_quantized file equals the oracle's quantize_per_channel of the source
+    weight (quant.py:25-29, the buffers of quant.py:36-37) bit for bit, for
+    Int8Linear and for DynamicInt8Linear (saved from its packed tiles through
+    unpack); <name>.bias is the fp32 bias.  The layers load_quantized builds
+    from the file then match the oracle: int8 within the weight-only bar
+    (rel-L2 1e-3; 2e-6 for fp16-valued inputs, which the kernels use exactly),
+    int8-dyn int32 accumulators and outputs bit-exact."""
+    from safetensors import safe_open
+
+    announce("saved pre-quantized file vs oracle")
+    srcs, mods = {}, {}
+    for i, (N, K, wd, has_b) in enumerate(SAVED_LAYERS):
+        w = make_weights(N, K, 150 + i).to(DT[wd])
+        b = torch.randn(N, generator=torch.Generator().manual_seed(160 + i)) if has_b else None
+        for kind, cls in (("w8", quant.Int8Linear), ("dyn", quant.DynamicInt8Linear)):
+            name = f"layer{i}.{kind}"
+            srcs[name] = (w, b)
+            mods[name] = cls(w.to(dev), None if b is None else b.to(dev))
+    path = str(tmp_path / "prequant.safetensors")
+    quant.save_quantized(mods, path)
+    with safe_open(path, framework="pt") as f:
+        keys = set(f.keys())
+        for name, (w, b) in srcs.items():
+            q_ref, s_ref = oracle.quantize_per_channel(w.float().numpy())
+            q = f.get_tensor(name + ".qweight")
+            s = f.get_tensor(name + ".scale")
+            assert q.dtype == torch.int8 and s.dtype == torch.float32, name
+            np.testing.assert_array_equal(q.numpy(), q_ref, err_msg=name)
+            np.testing.assert_array_equal(s.numpy().view(np.uint32), s_ref.view(np.uint32), err_msg=name)
+            if b is None:
+                assert name + ".bias" not in keys, name
+            else:
+                np.testing.assert_array_equal(f.get_tensor(name + ".bias").numpy(), b.float().numpy(), err_msg=name)
+    loaded = {"int8": quant.load_quantized(path, "int8"), "int8-dyn": quant.load_quantized(path, "int8-dyn")}
+    for i, (N, K, wd, has_b) in enumerate(SAVED_LAYERS):
+        for name in (f"layer{i}.w8", f"layer{i}.dyn"):
+            w, b = srcs[name]
+            q_ref, s_ref = oracle.quantize_per_channel(w.float().numpy())
+            bn = None if b is None else b.float().numpy()
+            for M, xd in ((1, torch.float32), (5, torch.float16), (40, torch.float32), (300, torch.float16)):
+                x = make_x(M, K, 170 + M, outliers=True).to(xd)
+                xv = x.float().numpy()
+                lin8 = loaded["int8"][name]
+                assert isinstance(lin8, quant.Int8Linear)
+                np.testing.assert_array_equal(lin8.qweight.cpu().numpy(), q_ref)
+                y = lin8(x.to(dev)).cpu().numpy()
+                tol = W8_TOL if xd == torch.float32 else 2e-6
+                assert oracle.rel_l2(y, oracle.int8_linear(xv, q_ref, s_ref, bn)) <= tol, (name, M)
+                dyn = loaded["int8-dyn"][name]
+                assert isinstance(dyn, quant.DynamicInt8Linear)
+                acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+                xg = x.to(dev)
+                yd = quant.linear_w8a8(xg, dyn.packed, dyn.scale, dyn.colsum, dyn.bias, N, acc_out=acc)
+                y_ref, info = oracle.dyn_linear(xv, q_ref, s_ref, bn, return_intermediates=True)
+                np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"], err_msg=f"{name} M={M}")
+                np.testing.assert_array_equal(yd.cpu().numpy(), y_ref, err_msg=f"{name} M={M}")
+                np.testing.assert_array_equal(dyn(xg).cpu().numpy(), y_ref, err_msg=f"{name} M={M} forward")
+
+
 # ---------------------------------------------------------------------------
 # HIP graph capture: every entry point replays correctly with eager work between
 # ---------------------------------------------------------------------------

@@ -92,3 +92,53 @@ def test_noalloc_rejects_inputs_beyond_the_scratch(dev):
         quant.linear_w8a8_noalloc(x, lin.packed, lin.scale, lin.colsum, None, N, out=y)
     torch.cuda.synchronize()
     assert bool((y == 7.0).all())
+
+
+def test_noalloc_graph_replays(dev):
+    """No-allocation calls captured in a HIP graph: one eager call per case
+    first (it looks the scratch up), then the calls captured back to back and
+    the graph replayed three times with new activations written between
+    replays; every replay's int32 accumulators and outputs equal
+    sbq_linear_w8a8 (the workspace entry point) on the same inputs bit for
+    bit."""
+    cases = [(1, 1024, 4096, torch.float32), (8, 1024, 4096, torch.float16), (200, 768, 4096, torch.float16),
+             (40, 512, 4096, torch.bfloat16)]
+    layers, xs, ys, accs = [], [], [], []
+    for i, (M, N, K, dt) in enumerate(cases):
+        announce(f"noalloc graph warm-up M={M} N={N} K={K} x={dt}")
+        layers.append(_layer(N, K, 30 + i, dev))
+        xs.append(_x(M, K, dt, 60 + i, dev))
+        ys.append(torch.empty((M, N), device=dev))
+        accs.append(torch.empty((M, N), dtype=torch.int32, device=dev))
+        quant.linear_w8a8_noalloc(xs[i], layers[i].packed, layers[i].scale, layers[i].colsum, layers[i].bias, N,
+                                  out=ys[i], acc_out=accs[i])
+    torch.cuda.synchronize()
+
+    def body():
+        for (M, N, K, dt), lin, x, y, acc in zip(cases, layers, xs, ys, accs):
+            quant.linear_w8a8_noalloc(x, lin.packed, lin.scale, lin.colsum, lin.bias, N, out=y, acc_out=acc)
+
+    announce("noalloc graph capture")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        body()
+    for rep in range(3):
+        announce(f"noalloc graph replay {rep}")
+        for i, (M, N, K, dt) in enumerate(cases):
+            xs[i].copy_(_x(M, K, dt, 100 * rep + i, dev))
+            ys[i].fill_(float("nan"))
+            accs[i].fill_(-1)
+        g.replay()
+        torch.cuda.synchronize()
+        for (M, N, K, dt), lin, x, y, acc in zip(cases, layers, xs, ys, accs):
+            acc_ref = torch.empty((M, N), dtype=torch.int32, device=dev)
+            y_ref = quant.linear_w8a8(x, lin.packed, lin.scale, lin.colsum, lin.bias, N, acc_out=acc_ref)
+            np.testing.assert_array_equal(acc.cpu().numpy(), acc_ref.cpu().numpy(), err_msg=f"acc rep {rep} M={M}")
+            np.testing.assert_array_equal(y.cpu().numpy(), y_ref.cpu().numpy(), err_msg=f"y rep {rep} M={M}")
+    del g
