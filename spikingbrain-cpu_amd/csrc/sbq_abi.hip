@@ -59,14 +59,27 @@ inline float* ws_stok(void* workspace, int64_t M, int64_t K) {
 
 // The int8-dyn path of one call as the entry points below run it: scratch
 // from a caller's workspace or from the no-allocation array.
+// Whether the int8-dyn GEMM of an [M, N, K] call can run its planned
+// configuration with `split_bytes` of split-K area (its mid-sized-M plan is
+// then the alternative to the row-tile GEMV).
+bool w8a8_gemm_alt(int64_t M, int64_t N, int64_t K, int64_t split_bytes) {
+  const sbq::DlPlan p = sbq::plan_gemm_dl(true, sbq::XT_F16, M, (N + 15) / 16, (K + 63) / 64, true);
+  return p.splits == 1 || split_bytes >= sbq::split_area_bytes(p);
+}
+
+// Whether an int8-dyn call runs the row-tile GEMV after the pre-passes.
+bool w8a8_runs_mt(int64_t M, int64_t N, int64_t K, int64_t split_bytes) {
+  return M > 16 && sbq::gemv_mt_applies(M, ((K + 63) / 64) * 64, N, sbq::XT_S8, w8a8_gemm_alt(M, N, K, split_bytes));
+}
+
 int linear_w8a8_run(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
                     const float* scale, const int32_t* colsum, const float* bias, int64_t N, void* y, int y_dtype,
                     int64_t ldy, int32_t* acc_out, float2* parts, float* qp, int8_t* xq, uint8_t* split,
                     int64_t split_bytes, hipStream_t st) {
   const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
-  // 16 < M <= 64 with small enough x: the pre-passes, then the row-tile GEMV on
-  // the s8 rows (inside launch_gemm_w8a8) instead of the general GEMV
-  const bool mt = M > 16 && sbq::gemv_mt_applies(M, ((K + 63) / 64) * 64, N, sbq::XT_S8);
+  // 16 < M <= 64 where the row-tile GEMV applies: the pre-passes, then that
+  // GEMV on the s8 rows (inside launch_gemm_w8a8) instead of the general GEMV
+  const bool mt = w8a8_runs_mt(M, N, K, split ? split_bytes : 0);
   if (!mt && sbq::gemv_supports(M, K, true, x_dtype))
     return sbq::launch_gemv_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, y_dtype, ldy, acc_out,
                                  parts, st, yv);
@@ -191,7 +204,10 @@ int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
   const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, y_dtype, ldy, N);
   hipStream_t st = (hipStream_t)stream;
   if (M > 16 && M <= 64) {  // several 16-row tiles of x against streamed weights
-    const int rc = sbq::launch_gemv_w8_mt(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
+    // the tiled GEMM's mid-sized-M plan needs the full workspace (row sums, split area)
+    const bool alt = workspace && (int64_t)workspace_bytes >= sbq_linear_workspace_bytes(M, N, K, x_dtype, 0);
+    const int rc =
+        sbq::launch_gemv_w8_mt(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv, alt);
     if (rc != -1) return rc;
   }
   if (sbq::gemv_supports(M, K, false, x_dtype)) return sbq::launch_gemv_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, y_dtype, ldy, st, yv);
@@ -253,12 +269,27 @@ int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K) {
   return 256 + kWsPartialBytes + kWsQpBytes + ((xq + 255) & ~(int64_t)255) + ((M * 4 + 255) & ~(int64_t)255);
 }
 
+// Whether a call of this shape reaches the tiled GEMM (the entry points'
+// dispatch for 16-byte aligned rows and the full workspace): otherwise a
+// decode GEMV (M <= 16, the general GEMV up to 32 tokens) or the row-tile
+// GEMV (16 < M <= 64 on narrow layers) runs it.
+bool runs_tiled_gemm(int64_t M, int64_t N, int64_t K, int x_dtype, bool w8a8) {
+  const sbq::DlPlan p = sbq::plan_gemm_dl(w8a8, sbq::XT_F16, M, (N + 15) / 16, (K + 63) / 64, true);
+  if (w8a8) {
+    if (w8a8_runs_mt(M, N, K, sbq::split_area_bytes(p))) return false;
+    return !sbq::gemv_supports(M, K, true, x_dtype);
+  }
+  if (M > 16 && M <= 64 && (x_dtype == SBQ_F16 || x_dtype == SBQ_BF16) && sbq::gemv_mt_applies(M, K, N, x_dtype, true))
+    return false;
+  return !sbq::gemv_supports(M, K, false, x_dtype);
+}
+
 int64_t sbq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8) {
   if (M < 0 || N < 1 || K < 1 || M > kIntMax || N > kIntMax || K > kIntMax || !valid_dtype(x_dtype)) return 0;
   if (w8a8 != 0 && w8a8 != 1) return 0;
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
   const int64_t base = w8a8 ? sbq_w8a8_workspace_bytes(M, K) : sbq_w8_workspace_bytes(M, K, x_dtype);
-  if (sbq::gemv_supports(M, K, w8a8 != 0, x_dtype)) return base;
+  if (M == 0 || !runs_tiled_gemm(M, N, K, x_dtype, w8a8 != 0)) return base;
   // the GEMM's operands are s8 (W8A8) or fp16 (weight-only, fp32 / bf16 staged as fp16 planes)
   return base + sbq::split_area_bytes(sbq::plan_gemm_dl(w8a8 != 0, 1, M, Nt, Kc, true));
 }
@@ -270,7 +301,7 @@ int sbq_gemm_config(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8, int*
   // with that workspace every activation dtype reaches the GEMM as fp16 (W-only:
   // fp32 / bf16 staged as fp16 planes, row sums precomputed) or s8 (W8A8)
   const sbq::DlPlan p = sbq::plan_gemm_dl(w8a8 != 0, sbq::XT_F16, M, (N + 15) / 16, (K + 63) / 64, true);
-  if (splits) *splits = p.splits;
+  if (splits) *splits = runs_tiled_gemm(M, N, K, x_dtype, w8a8 != 0) ? p.splits : 0;
   return p.id;
 }
 

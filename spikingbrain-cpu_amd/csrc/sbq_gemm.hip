@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "sbq_common.h"
+#include "sbq_dma.h"
 #include "sbq_gemv_ops.h"
 #include "sbq_index.h"
 #include "sbq_launch.h"
@@ -35,8 +36,6 @@ namespace sbq {
 // 16 bytes; chunk c of row r lives at slot c ^ (r & 7) so that the 16 rows a
 // quarter-wave reads for one fragment spread over all banks.
 __device__ __forceinline__ int xs_off(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
-// LDS activation tile for s8 operands: 64 bytes per row = 4 chunks.
-__device__ __forceinline__ int xq_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
 
 template <int XT>
 struct GemmOp;
@@ -256,27 +255,11 @@ __global__ __launch_bounds__(WN* WM * 64) void gemm_w8_kernel(const void* __rest
 // never stored.
 // ---------------------------------------------------------------------------
 
-// Raw buffer over [base, base + bytes): loads outside it return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
 
-// 16 bytes per lane from buffer offset voff + soff straight into LDS at
-// lds + 16 * lane (lds wave-uniform).
-__device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff, void* lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
-}
 
-// Cache policy of buffer accesses that other XCDs read or wrote (sc1: coherent
-// at device scope without an L2 write-back or invalidate).
-constexpr int kCoherent = 16;
+// Most workgroups K is split over (the split-K plan's largest split).
+constexpr int kMaxSplits = 4;
 
-// s_waitcnt vmcnt(n) (n < 64) leaving the other counters unconstrained.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
 
 // Wait until only the `younger` most recent stages (LPS DMA instructions each)
 // of this wave are still in flight.
@@ -292,16 +275,6 @@ __device__ __forceinline__ void wait_stages(int younger) {
   wait_vmcnt<0>();
 }
 
-// Workgroup barrier without the release/acquire fence of __syncthreads():
-// the fence would wait for every outstanding load, including the LDS DMA of
-// the stages still in flight.  Each wave waits for its own DMA of the stage it
-// is about to read (wait_vmcnt) before arriving here; the asm clobbers keep
-// the compiler from moving LDS accesses across the barrier.
-__device__ __forceinline__ void barrier_nofence() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 __device__ __forceinline__ int xsw_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
@@ -383,9 +356,14 @@ constexpr int dl_min_waves() {
 // one-tile stage.
 // SK: K split over gridDim.z workgroups with the partial-tile fixup (only the
 // configurations the split plan uses are built with it: the fixup's registers
-// would otherwise spill in the large-tile configurations).
+// would otherwise spill in the large-tile configurations).  Its grids are
+// small, so the occupancy hint asks for at most 2 waves per SIMD (256 VGPRs):
+// the fixup holds every other split's partial tile in registers at once.
 template <bool I8, int XT, int BN, int BM, int WN, int WM, int NS, int KG, bool RSP = false, int KT = 1, bool SK = false>
-__global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>())) void gemm_dl_kernel(const GemmArgs a) {
+__global__ __launch_bounds__(KG* WN* WM * 64, (SK ? (dl_min_waves<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>() < 2
+                                                          ? dl_min_waves<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>()
+                                                          : 2)
+                                                    : dl_min_waves<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT>())) void gemm_dl_kernel(const GemmArgs a) {
   typedef GemmOp<XT> Op;
   typedef typename Op::V V;
   typedef typename std::conditional<I8, i32x4, f32x4>::type Acc;
@@ -687,28 +665,37 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (dl_min_waves<I8, XT, BN, BM, WN, 
     // every split of the tile has counted: leave the counter at zero (the
     // pre-pass zeroes it too, for a workspace that holds anything)
     if (w == 0 && lane == 0) __hip_atomic_store(a.tcount + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The other splits' partials, all in flight at once (one memory round
+    // trip; loading them split by split cost one round trip each: 4.6 us on
+    // the last split of a 4-way M = 128 tile), then summed in split order
+    // 0 .. S-1 with this split's own partial at z, so the sum has the same
+    // bits whichever split arrives last.
+    static_assert(kMaxSplits == 4, "the partial slots below");
+    u32x4 v[kMaxSplits][FN][FM];
+#pragma unroll
+    for (int zz = 0; zz < kMaxSplits; ++zz) {
+#pragma unroll
+      for (int t = 0; t < FN; ++t)
+#pragma unroll
+        for (int b = 0; b < FM; ++b)
+          v[zz][t][b] = zz < S && zz != z  // uniform
+                            ? __builtin_amdgcn_raw_buffer_load_b128(prs, zz * kTile + mine + (t * FM + b) * 1024, 0,
+                                                                    kCoherent)
+                            : (u32x4){0u, 0u, 0u, 0u};
+    }
     Acc sum[FN][FM];
 #pragma unroll
     for (int t = 0; t < FN; ++t)
 #pragma unroll
       for (int b = 0; b < FM; ++b) sum[t][b] = Acc{0, 0, 0, 0};
-    for (int zz = 0; zz < S; ++zz) {
-      if (zz == z) {
+#pragma unroll
+    for (int zz = 0; zz < kMaxSplits; ++zz) {
+      if (zz < S) {  // uniform
+        const bool own = zz == z;
 #pragma unroll
         for (int t = 0; t < FN; ++t)
 #pragma unroll
-          for (int b = 0; b < FM; ++b) sum[t][b] += acc[t][b];
-      } else {
-        u32x4 v[FN][FM];
-#pragma unroll
-        for (int t = 0; t < FN; ++t)
-#pragma unroll
-          for (int b = 0; b < FM; ++b)
-            v[t][b] = __builtin_amdgcn_raw_buffer_load_b128(prs, zz * kTile + mine + (t * FM + b) * 1024, 0, kCoherent);
-#pragma unroll
-        for (int t = 0; t < FN; ++t)
-#pragma unroll
-          for (int b = 0; b < FM; ++b) sum[t][b] += __builtin_bit_cast(Acc, v[t][b]);
+          for (int b = 0; b < FM; ++b) sum[t][b] += own ? acc[t][b] : __builtin_bit_cast(Acc, v[zz][t][b]);
       }
     }
 #pragma unroll
@@ -875,6 +862,7 @@ int launch_dl(const GemmArgs& a, hipStream_t st) {
   } else {
     if (a.Kc % KT) return -1;
     if (SK != (a.part != nullptr)) return -1;  // split arguments only for the split instances
+    if (SK && (a.splits < 2 || a.splits > kMaxSplits)) return -1;
     const dim3 grid((unsigned)((a.Nt + BN / 16 - 1) / (BN / 16)), (unsigned)((a.M + BM - 1) / BM),
                     (unsigned)(SK ? a.splits : 1));
     hipLaunchKernelGGL((gemm_dl_kernel<I8, XT, BN, BM, WN, WM, NS, KG, RSP, KT, SK>), grid, dim3(KG * WN * WM * 64),
@@ -985,7 +973,17 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restric
   X(16, 192, 64, 4, 1, 2, 1)  \
   X(17, 192, 64, 4, 1, 2, 4)  \
   X(18, 192, 128, 4, 1, 2, 1) \
-  X(19, 192, 128, 4, 1, 3, 1)
+  X(19, 192, 128, 4, 1, 3, 1) \
+  X(22, 64, 64, 4, 1, 3, 1)
+
+// The mid-sized-M configurations (64 weight rows, one 16-row tile per wave,
+// every token of the block in each wave): (id, BM, NS).  They are built with
+// precomputed row sums (fp16 W-only), two K tiles per stage (W8A8) and the
+// split-K fixup as well.  Measured and not kept: 64 x 128 blocks (3 and 5
+// stages) and 64 x 64 blocks with 5 and 8 stages (deeper rings were no faster:
+// the ring's depth is not what bounds these shapes).
+#define SBQ_MID_CONFIGS(X) \
+  X(22, 64, 3)
 
 template <bool I8, int XT>
 int launch_dl_id(int id, const GemmArgs& a, hipStream_t st) {
@@ -1011,6 +1009,10 @@ int launch_dl_rsp(int id, const GemmArgs& a, hipStream_t st) {
     case 16: return launch_dl<false, XT_F16, 192, 64, 4, 1, 2, 1, true>(a, st);
     case 17: return launch_dl<false, XT_F16, 192, 64, 4, 1, 2, 4, true>(a, st);
     case 18: return launch_dl<false, XT_F16, 192, 128, 4, 1, 2, 1, true>(a, st);
+#define SBQ_MID_RSP(ID, BM, NS) \
+    case ID: return launch_dl<false, XT_F16, 64, BM, 4, 1, NS, 1, true>(a, st);
+    SBQ_MID_CONFIGS(SBQ_MID_RSP)
+#undef SBQ_MID_RSP
   }
   if (a.rscale) return -1;  // staged activations need the row scale: only the configurations above apply it
   GemmArgs b = a;
@@ -1031,24 +1033,50 @@ int launch_dl_i8(int id, const GemmArgs& a, hipStream_t st) {
       return kt2 ? launch_dl<true, XT_F16, 128, 64, 2, 2, 2, 1, false, 2>(a, st) : launch_dl_id<true, XT_F16>(3, a, st);
     case 20:
       return kt2 ? launch_dl<true, XT_F16, 192, 64, 4, 1, 2, 1, false, 2>(a, st) : launch_dl_id<true, XT_F16>(16, a, st);
+#define SBQ_MID_I8(ID, BM, NS) \
+    case ID:                     \
+      return kt2 ? launch_dl<true, XT_F16, 64, BM, 4, 1, NS, 1, false, 2>(a, st) : launch_dl_id<true, XT_F16>(ID, a, st);
+    SBQ_MID_CONFIGS(SBQ_MID_I8)
+#undef SBQ_MID_I8
   }
   return launch_dl_id<true, XT_F16>(id, a, st);
 }
 
-// The split-K instances (128 x 64 blocks; the plan's ids 15 and 3).
-int launch_dl_split(bool i8, const GemmArgs& a, hipStream_t st) {
+// The split-K instances: 128 x 64 blocks (ids 15 and 3, used by the tuning
+// harness) and the mid-sized-M configurations.
+int launch_dl_split(int id, bool i8, const GemmArgs& a, hipStream_t st) {
+  const bool kt2 = a.Kc % 2 == 0;
   if (i8) {
-    return a.Kc % 2 == 0 ? launch_dl<true, XT_F16, 128, 64, 2, 2, 2, 1, false, 2, true>(a, st)
-                         : launch_dl<true, XT_F16, 128, 64, 2, 2, 2, 1, false, 1, true>(a, st);
+    switch (id) {
+      case 3:
+      case 15:
+        return kt2 ? launch_dl<true, XT_F16, 128, 64, 2, 2, 2, 1, false, 2, true>(a, st)
+                   : launch_dl<true, XT_F16, 128, 64, 2, 2, 2, 1, false, 1, true>(a, st);
+#define SBQ_MID_SPLIT_I8(ID, BM, NS)                                                \
+      case ID:                                                                      \
+        return kt2 ? launch_dl<true, XT_F16, 64, BM, 4, 1, NS, 1, false, 2, true>(a, st) \
+                   : launch_dl<true, XT_F16, 64, BM, 4, 1, NS, 1, false, 1, true>(a, st);
+      SBQ_MID_CONFIGS(SBQ_MID_SPLIT_I8)
+#undef SBQ_MID_SPLIT_I8
+    }
+    return -1;
   }
   if (!a.rsum) return -1;  // fp16 W-only splits need the precomputed row sums
-  return launch_dl<false, XT_F16, 128, 64, 2, 2, 2, 1, true, 1, true>(a, st);
+  switch (id) {
+    case 3:
+    case 15: return launch_dl<false, XT_F16, 128, 64, 2, 2, 2, 1, true, 1, true>(a, st);
+#define SBQ_MID_SPLIT(ID, BM, NS) \
+    case ID: return launch_dl<false, XT_F16, 64, BM, 4, 1, NS, 1, true, 1, true>(a, st);
+    SBQ_MID_CONFIGS(SBQ_MID_SPLIT)
+#undef SBQ_MID_SPLIT
+  }
+  return -1;
 }
 
 // Launch of direct-to-LDS configuration `id` (tuning entry; -1: no such id).
 // Arguments with a split-K area (a.part) run the split instances.
 int launch_gemm_dl_cfg(int id, bool i8, int xt, const GemmArgs& a, hipStream_t st) {
-  if (a.part) return (id == 15 || id == 3) && (i8 || xt == XT_F16) ? launch_dl_split(i8, a, st) : -1;
+  if (a.part) return i8 || xt == XT_F16 ? launch_dl_split(id, i8, a, st) : -1;
   if (i8) return launch_dl_i8(id, a, st);
   // 192 x 64 blocks with K split over 4 wave groups leave no LDS for the
   // in-loop row sums: without precomputed sums the 128 x 64 split runs
@@ -1173,29 +1201,37 @@ int pick_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc) {
   return 8;
 }
 
-// Split-K plan.  Grids of fewer than 192 blocks of 128 x 64 leave CUs idle
-// (the 128-token W8A8 GEMM at N = 4096 ran 128 workgroups on 256 CUs and read
-// every weight tile twice): those shapes run 128 x 64 blocks with K split over
-// 4 workgroups (2 when K holds fewer than 32 stage steps), each keeping at
-// least 8 stage steps.  Measured on MI355X at N = 4096..12288, K = 4096
-// (whole calls, pre-passes included): 4 splits beat 2 and 8, and save 2.0 to
-// 2.7 us at M <= 64 and 0.6 to 1.3 us at M = 128; at M = 200 and 256 the
-// fixup costs more than the idle CUs did (W-only +1 us), so only M <= 128
-// splits.  Only for operands that need no in-loop row sums: W8A8, and fp16
-// W-only with precomputed row sums (the staged fp32 / bf16 activations
+// Mid-sized M (M <= 128): 64 x 64 blocks (configuration 22: one 16-row weight
+// tile per wave, every token of the block in each wave, a 3-stage ring), with
+// K split over S workgroups when the grid of B blocks leaves CUs idle:
+// S = min(4, budget / B), budget 288 blocks for W8A8 and 768 for fp16 W-only
+// (whose blocks carry twice the activation bytes per K tile and gain from more
+// workgroups), each split keeping at least 4 stage steps.  Grids of more than
+// 512 blocks keep the picker's configuration.  Measured on MI355X (the GEMM
+// alone, weights rotating beyond the Infinity Cache, against the previous
+// plan: 128 x 64 blocks split when fewer than 192 of them): W8A8 M = 128,
+// N = 4096: 14.4 -> 11.8 us; N = 12288: 23.9 -> 21.0 us; N = 2560, K = 9728:
+// 22.0 -> 16.2 us; fp16 W-only M = 128, N = 4096: 17.4 -> 13.2 us; N = 12288:
+// 30.4 -> 25.6 us.  Only for operands that need no in-loop row sums: W8A8, and
+// fp16 W-only with precomputed row sums (the staged fp32 / bf16 activations
 // included).
+constexpr int kMidId = 22;
+
 DlPlan plan_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc, bool rsp) {
   DlPlan p{pick_gemm_dl(i8, xt, M, Nt, Kc), 1, 0, 0};
   if (!i8 && !(xt == XT_F16 && rsp)) return p;
-  const int64_t tiles = ((Nt + 7) / 8) * ((M + 63) / 64);
-  if (tiles >= 192 || M > 128) return p;
-  const int64_t steps = i8 && Kc % 2 == 0 ? Kc / 2 : Kc;  // stage steps of the 128 x 64 configuration
-  const int S = steps >= 32 ? 4 : (steps >= 16 ? 2 : 1);
+  if (M > 128) return p;
+  const int64_t tiles = ((Nt + 3) / 4) * ((M + 63) / 64);
+  if (tiles > 512) return p;
+  p.id = kMidId;
+  const int64_t steps = i8 && Kc % 2 == 0 ? Kc / 2 : Kc;  // stage steps of the configuration
+  int64_t S = (i8 ? 288 : 768) / tiles;
+  S = S < 1 ? 1 : (S > kMaxSplits ? kMaxSplits : S);
+  while (S > 1 && steps / S < 4) --S;
   if (S == 1) return p;
-  p.id = i8 ? 15 : 3;
-  p.splits = S;
+  p.splits = (int)S;
   p.tiles = tiles;
-  p.part_bytes = tiles * S * 128 * 64 * 4;  // one fp32 / int32 partial tile per split
+  p.part_bytes = tiles * S * 64 * 64 * 4;  // one fp32 / int32 partial tile per split
   return p;
 }
 
@@ -1334,13 +1370,16 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
 #undef SBQ_QUANT_LAUNCH1
   int rc = check_launch();
   if (rc) return rc;
-  if (M > 16 && gemv_mt_applies(M, Kp, N, XT_S8)) {  // small M: the row-tile GEMV on the s8 rows
+  // small M: the row-tile GEMV on the s8 rows where it beats the tiled GEMM
+  // (the GEMM's plan is available when it needs no split area or has it)
+  const bool alt = plan.splits == 1 || zero != nullptr;
+  if (M > 16 && gemv_mt_applies(M, Kp, N, XT_S8, alt)) {
     GemvArgs g{};
     g.x = xq; g.ldx = Kp; g.M = (int)M; g.K = (int)Kp; g.Kc = (int)Kc;
     g.packed = packed; g.scale = scale; g.bias = bias; g.colsum = colsum;
     g.N = (int)N; g.Nt = (int)Nt; g.y = y; g.yt = yt; g.ldy = ldy; g.acc_out = acc_out; g.qpbuf = qpbuf;
     g.flags = kGemvXVec | (yvec ? kGemvYVec : 0);
-    rc = launch_gemv_mt(g, XT_S8, st);
+    rc = launch_gemv_mt(g, XT_S8, st, alt);
     if (rc != -1) return rc;
   }
   a.x = xq; a.ldx = Kp; a.M = (int)M; a.Kc = (int)Kc;

@@ -538,13 +538,13 @@ int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
 // bf16 x with aligned rows, 64 | K); -1 when that path does not apply.
 int launch_gemv_w8_mt(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                       const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
-                      bool yvec) {
+                      bool yvec, bool gemm_alt) {
   GemvArgs a{};
   a.x = x; a.ldx = ldx; a.M = (int)M; a.K = (int)K; a.Kc = (int)((K + 63) / 64);
   a.packed = packed; a.scale = scale; a.bias = bias;
   a.N = (int)N; a.Nt = (int)((N + 15) / 16); a.y = y; a.yt = yt; a.ldy = ldy;
   a.flags = (xvec ? kGemvXVec : 0) | (yvec ? kGemvYVec : 0);
-  return launch_gemv_mt(a, xt, st);
+  return launch_gemv_mt(a, xt, st, gemm_alt);
 }
 
 // Independent linears of one M, K and dtypes in one fast-path launch (picked

@@ -971,25 +971,30 @@ int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, bool w8a8, hipS
 // Decode over several 16-row tiles of x (gemv_mt_kernel): weight-only on fp16
 // / bf16 x, or int8-dyn on the s8 rows of the quantize pre-pass (xt XT_S8,
 // a.qpbuf and a.colsum set); aligned rows, 16 < M <= 64, 64 | K.  -1: not
-// this path.  Every workgroup reads all of x, and the launch time grows with the x bytes
-// its grid reads from L2 (MI355X: about 0.13-0.16 us per MB beyond a 2-5 us
-// base), so the path is taken up to 120 MB of them, where it beats the
-// general GEMV (M <= 32) and the tiled GEMM: N = 4096, M = 24 / 33 / 48:
-// 10.4 / 20.1 / 20.1 -> 9.4 / 12.0 / 15.1 us; N = 12288, M = 24 / 32:
-// 28.7 / 30.7 -> 18.3 / 21.1 us (M = 48 and 64 there, 151 and 201 MB, run
-// the GEMM: 25.5 and 26.0 us against 28.7 and 36.7).
-bool gemv_mt_applies(int64_t M, int64_t K, int64_t N, int xt) {
+// this path.  Every workgroup reads all of x, and the launch time grows with
+// the x bytes its grid reads from L2 (MI355X: about 0.13-0.16 us per MB
+// beyond a 2-5 us base).  gemm_alt: the tiled GEMM's mid-sized-M plan (64 x 64
+// blocks, K split when the grid is small) is available to the caller; it is
+// faster except on narrow layers with little x to read (measured, the GEMM
+// alone against this kernel: int8-dyn N = 4096, K = 4096, M = 24 / 32 / 48:
+// 7.8 / 8.6 / 10.7 us here against 9.9 / 9.8 / 10.0; N = 9728, K = 2560,
+// M = 32: 13.9 against 10.8; weight-only, whose GEMM also needs its row-sum
+// pre-pass, N = 4096, M = 24 / 32: 9.6 / 11.1 against 11.7 us plus the
+// pre-pass), so with it the path is kept for N <= 4096 while the grid's x
+// reads stay within 36 MB (s8) / 80 MB (fp16, bf16).  Without it, up to
+// 90 MB / 120 MB, where this kernel beats the general GEMV and the unsplit
+// GEMM (N = 4096, M = 24 / 33 / 48: 10.4 / 20.1 / 20.1 -> 9.4 / 12.0 / 15.1 us).
+bool gemv_mt_applies(int64_t M, int64_t K, int64_t N, int xt, bool gemm_alt) {
   if (!(xt == XT_F16 || xt == XT_BF16 || xt == XT_S8) || M <= 16 || M > 64 || K % 64 != 0) return false;
   const int64_t Nt = (N + 15) / 16, Kc = K / 64;
   const int G = Kc < 128 && Nt >= 384 ? 2 : 1;
   const int64_t x_grid_bytes = M * K * (xt == XT_S8 ? 1 : 2) * ((Nt + G - 1) / G);
-  // s8 rows: 90 MB (int8-dyn, N = 12288: M = 48 at 75 MB 29.9 -> 27.1 us, M = 64 at
-  // 100 MB 31.4 against 29.8 for the GEMM)
+  if (gemm_alt) return Nt <= 256 && x_grid_bytes <= ((int64_t)(xt == XT_S8 ? 36 : 80) << 20);
   return x_grid_bytes <= ((int64_t)(xt == XT_S8 ? 90 : 120) << 20);
 }
 
-int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st) {
-  if (a.K != a.Kc * 64 || !(a.flags & kGemvXVec) || !gemv_mt_applies(a.M, a.K, a.N, xt)) return -1;
+int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st, bool gemm_alt) {
+  if (a.K != a.Kc * 64 || !(a.flags & kGemvXVec) || !gemv_mt_applies(a.M, a.K, a.N, xt, gemm_alt)) return -1;
   if (xt == XT_S8 && (!a.qpbuf || !a.colsum)) return -1;
   const int mt = (a.M + 15) / 16;
   const bool wide = a.Kc < 128 && a.Nt >= 384;

@@ -37,12 +37,14 @@ struct GemvSeg;
 bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xvec, int* id, int* ks);
 int launch_gemv_fast_cfg(int id, int ks, const GemvArgs& a, int xt, bool w8a8, hipStream_t st);
 // Decode over several 16-row tiles of x (16 < M <= 64): weight-only on fp16 /
-// bf16 x, or int8-dyn on pre-quantized s8 rows (xt XT_S8).
-bool gemv_mt_applies(int64_t M, int64_t K, int64_t N, int xt);
-int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st);
+// bf16 x, or int8-dyn on pre-quantized s8 rows (xt XT_S8).  gemm_alt: the
+// caller can run the tiled GEMM's mid-sized-M plan instead (then the path is
+// taken on fewer shapes).
+bool gemv_mt_applies(int64_t M, int64_t K, int64_t N, int xt, bool gemm_alt);
+int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st, bool gemm_alt);
 int launch_gemv_w8_mt(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                       const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, hipStream_t st,
-                      bool yvec);
+                      bool yvec, bool gemm_alt);
 // Grouped launch: a.seg / a.nseg hold 2..kGemvMaxSeg linears (w8a8: int8-dyn
 // with the activation min/max reduced in the kernel).
 int launch_gemv_fast_grouped(int id, int ks, GemvArgs a, int xt, bool w8a8, hipStream_t st);

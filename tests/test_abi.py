@@ -173,12 +173,44 @@ def test_gemm_config_picks(lib, w8a8, cases):
             assert splits.value == 1
 
 
+# Mid-sized M (M <= 128): 64 x 64 blocks (configuration 22), K split over
+# min(4, budget / blocks) workgroups (budget 288 for W8A8, 768 for fp16
+# weight-only), each split keeping >= 4 stage steps; (M, N, K, w8a8, splits).
+MID_PLANS = [(128, 4096, 4096, 1, 2), (128, 4096, 4096, 0, 4), (64, 4096, 4096, 1, 4), (100, 2048, 4096, 1, 4),
+             (128, 12288, 4096, 1, 1), (128, 12288, 4096, 0, 2), (128, 2560, 9728, 1, 3), (128, 9728, 2560, 1, 1),
+             (128, 4096, 1024, 1, 2), (120, 1024, 2560, 1, 4), (128, 4096, 4160, 1, 2), (80, 2560, 9728, 0, 4)]
+
+
 def test_gemm_config_split_plans_and_errors(lib):
     splits = ctypes.c_int(-1)
-    assert lib.sbq_gemm_config(128, 4096, 4096, 1, 1, ctypes.byref(splits)) == 15 and splits.value == 4
-    assert lib.sbq_gemm_config(128, 4096, 4096, 1, 0, ctypes.byref(splits)) == 3 and splits.value == 4
-    assert lib.sbq_gemm_config(128, 4096, 1024, 1, 1, None) == 8  # too few K steps to split; splits may be NULL
+    for M, N, K, w8a8, S in MID_PLANS:
+        assert lib.sbq_gemm_config(M, N, K, 1, w8a8, ctypes.byref(splits)) == 22, (M, N, K, w8a8)
+        assert splits.value == S, (M, N, K, w8a8, splits.value)
+    # grids of more than 512 blocks of 64 x 64 keep the picker's configuration
+    assert lib.sbq_gemm_config(128, 24576, 4096, 1, 1, ctypes.byref(splits)) != 22 and splits.value == 1
+    assert lib.sbq_gemm_config(128, 4096, 4096, 1, 1, None) == 22  # splits may be NULL
     assert lib.sbq_gemm_config(0, 4096, 4096, 1, 0, None) == -1
     assert lib.sbq_gemm_config(128, 0, 4096, 1, 0, None) == -1
     assert lib.sbq_gemm_config(128, 4096, 4096, 1, 2, None) == -1
     assert lib.sbq_gemm_config(128, 4096, 4096, 7, 0, None) == -2
+
+
+# Shapes that do not reach the tiled GEMM report 0 splits (and add no split
+# area to the workspace): decode sizes (the decode GEMVs) and 16 < M <= 64 on
+# narrow layers (the row-tile GEMV); (M, N, K, x dtype, w8a8).
+NOT_GEMM = [(1, 4096, 4096, 1, 1), (8, 4096, 4096, 0, 0), (16, 4096, 4096, 1, 0), (32, 4096, 4096, 1, 1),
+            (24, 4096, 4096, 1, 0), (48, 2048, 4096, 2, 0), (33, 1000, 2048, 1, 1)]
+GEMM = [(48, 12288, 4096, 1, 1), (64, 4096, 4096, 1, 1), (64, 4096, 4096, 1, 0), (32, 9728, 2560, 1, 1),
+        (40, 4096, 8192, 1, 0), (40, 4096, 8192, 1, 1)]
+
+
+def test_gemm_config_reports_the_route(lib):
+    splits = ctypes.c_int(-1)
+    for M, N, K, dt, w8a8 in NOT_GEMM:
+        lib.sbq_gemm_config(M, N, K, dt, w8a8, ctypes.byref(splits))
+        assert splits.value == 0, (M, N, K, dt, w8a8)
+        base = lib.sbq_w8a8_workspace_bytes(M, K) if w8a8 else lib.sbq_w8_workspace_bytes(M, K, dt)
+        assert lib.sbq_linear_workspace_bytes(M, N, K, dt, w8a8) == base, (M, N, K, dt, w8a8)
+    for M, N, K, dt, w8a8 in GEMM:
+        lib.sbq_gemm_config(M, N, K, dt, w8a8, ctypes.byref(splits))
+        assert splits.value >= 1, (M, N, K, dt, w8a8)

@@ -809,17 +809,26 @@ def test_device_resident_decode(dev, fmt):
 # ---------------------------------------------------------------------------
 # prefill GEMM with K split over workgroups (grids that would leave CUs idle)
 # ---------------------------------------------------------------------------
-SPLIT_CASES = [  # (M, N, K): 128 x 64 blocks, K split 2 or 4 ways (M <= 128 only)
-    (33, 1000, 2048), (64, 4096, 4096), (100, 2048, 4096), (128, 4096, 4096), (120, 1024, 2560),
-    (128, 6144, 4096), (128, 4096, 4160), (48, 256, 12288),
+SPLIT_CASES = [  # (M, N, K): 64 x 64 blocks (configuration 22), K split 2 - 4 ways (M <= 128 only); every
+    # case reaches the split GEMM in both formats (asserted through sbq_gemm_config): ragged M and N, an odd
+    # number of K tiles (4160), short and long K, 16 < M <= 64 on layers the row-tile GEMV leaves to the GEMM
+    (64, 4096, 4096), (100, 2048, 4096), (128, 4096, 4096), (120, 1024, 2560), (100, 2000, 4096),
+    (128, 4096, 4160), (80, 2560, 9728), (40, 4096, 8192),
 ]
 
 
 def _split_bytes(M, N, K, xd, w8a8):
+    """(full workspace, workspace without the split area), and asserts that
+    the shape runs the tiled GEMM with K split (sbq_gemm_config)."""
+    import ctypes
+
     from sbq import _lib
 
     L = _lib.load()
     code = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[xd]
+    splits = ctypes.c_int(-1)
+    L.sbq_gemm_config(M, N, K, code, 1 if w8a8 else 0, ctypes.byref(splits))
+    assert splits.value >= 2, (M, N, K, xd, w8a8, splits.value)
     base = L.sbq_w8a8_workspace_bytes(M, K) if w8a8 else L.sbq_w8_workspace_bytes(M, K, code)
     return L.sbq_linear_workspace_bytes(M, N, K, code, 1 if w8a8 else 0), base
 
@@ -856,7 +865,7 @@ def test_w8a8_split_k_bitexact(dev, M, N, K):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,N,K", SPLIT_CASES[:6])
+@pytest.mark.parametrize("M,N,K", SPLIT_CASES)
 def test_w8_split_k_matches_oracle(dev, M, N, K):
     """Weight-only with K split over workgroups (fp16 x, and fp32 / bf16 x
     staged as fp16 planes): within the tolerance of the oracle, equal across
@@ -1085,7 +1094,10 @@ MT_CASES = [  # (M, N, K, x dtype): ragged M, narrow / wide (two weight tiles pe
 def test_w8_gemv_row_tiles(dev, M, N, K, xd):
     """fp16 / bf16 x at 16 < M <= 64: within fp32 summation order of the
     oracle for exactly representable inputs (fp32 y), one output rounding for
-    2-byte y, with a bias and with strided x rows."""
+    2-byte y, with a bias and with strided x rows.  Each case runs twice: with
+    the full workspace (the row-tile GEMV only where it beats the tiled GEMM's
+    mid-sized-M plan) and with a workspace without the split area (then the
+    row-tile GEMV takes every case here)."""
     announce(f"w8 gemv row tiles M={M} N={N} K={K} x={xd}")
     w = gpu_weight(N, K, 960, dev)
     b = torch.randn(N, generator=torch.Generator().manual_seed(961))
@@ -1095,11 +1107,12 @@ def test_w8_gemv_row_tiles(dev, M, N, K, xd):
     x = cpu_x(M, K, 963).to(DT[xd])
     ref = oracle.int8_linear(x.float().numpy(), q, s, b.numpy()[cols])
     wide = torch.zeros((M, K + 64), dtype=DT[xd], device=dev)
-    for xg in (x.to(dev), wide[:, :K].copy_(x.to(dev))):  # dense rows; rows 128 bytes apart beyond K
-        y = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N)
-        assert oracle.rel_l2(y.cpu().numpy()[:, cols], ref) <= W8_TOL_EXACT_X
-        yh = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N, torch.float16)
-        np.testing.assert_array_equal(yh.cpu().numpy(), y.half().cpu().numpy())
+    for ws in (None, quant.w8_workspace(M, K, dev, DT[xd])):
+        for xg in (x.to(dev), wide[:, :K].copy_(x.to(dev))):  # dense rows; rows 128 bytes apart beyond K
+            y = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N, workspace=ws)
+            assert oracle.rel_l2(y.cpu().numpy()[:, cols], ref) <= W8_TOL_EXACT_X
+            yh = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N, torch.float16, workspace=ws)
+            np.testing.assert_array_equal(yh.cpu().numpy(), y.half().cpu().numpy())
 
 
 MT8_CASES = [  # (M, N, K): int8-dyn on the s8 rows of the quantize pre-pass, within the path's x-read cap
@@ -1110,8 +1123,10 @@ MT8_CASES = [  # (M, N, K): int8-dyn on the s8 rows of the quantize pre-pass, wi
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K", MT8_CASES)
 def test_w8a8_gemv_row_tiles(dev, M, N, K):
-    """int8-dyn at 16 < M <= 64 through the row-tile GEMV: int32 accumulators
-    and outputs bit-exact against the oracle, with and without a bias."""
+    """int8-dyn at 16 < M <= 64: int32 accumulators and outputs bit-exact
+    against the oracle, with and without a bias, with the full workspace (the
+    row-tile GEMV only where it beats the tiled GEMM's plan) and with one
+    without the split area (the row-tile GEMV for every case here)."""
     announce(f"w8a8 gemv row tiles M={M} N={N} K={K}")
     w = gpu_weight(N, K, 970, dev)
     b = torch.randn(N, generator=torch.Generator().manual_seed(971))
@@ -1119,10 +1134,11 @@ def test_w8a8_gemv_row_tiles(dev, M, N, K):
     cols = tile_sample(N, 972)
     q, s = ref_rows(w, cols)
     x = cpu_x(M, K, 973, outliers=True)
-    for bias in (None, b):
+    for bias, ws in ((None, None), (b, None), (None, quant.w8a8_workspace(M, K, dev)),
+                     (b, quant.w8a8_workspace(M, K, dev))):
         lin = quant.DynamicInt8Linear(w, None if bias is None else bias.to(dev))
         acc = torch.empty((M, N), dtype=torch.int32, device=dev)
-        y = quant.linear_w8a8(x.to(dev), lin.packed, lin.scale, lin.colsum, lin.bias, N, acc_out=acc)
+        y = quant.linear_w8a8(x.to(dev), lin.packed, lin.scale, lin.colsum, lin.bias, N, acc_out=acc, workspace=ws)
         acc_ref, y_ref = ref_w8a8(x.numpy(), rows, q, s, None if bias is None else bias.numpy()[cols])
         r_, c_ = torch.from_numpy(rows).to(dev), torch.from_numpy(cols).to(dev)
         np.testing.assert_array_equal(acc[r_][:, c_].cpu().numpy(), acc_ref)
