@@ -105,20 +105,25 @@ int sbq_unpack_w8(const uint8_t* packed, int64_t N, int64_t K, int8_t* q, int64_
 /* y[m,n] = (sum_k x[m,k] * q[n,k]) * scale[n] (+ bias[n])
  * x: device [M, K] (row stride ldx), dtype F32, F16 or BF16.
  *    F16/BF16 inputs are used exactly (BF16 staged for the prefill GEMM: exact
- *    down to 2^28 below each row's maximum).  F32 inputs are split into two
- *    parts: fp16 hi + lo of the row scaled by a power of two on the staged
- *    prefill path (22 significant bits), bf16 hi + remainder elsewhere
- *    (relative representation error <= 2^-16).
+ *    down to 2^28 below each row's maximum).  F32 inputs: on the decode paths
+ *    (M <= 16, and the general GEMV up to 32 tokens) split into bf16 hi +
+ *    remainder (relative representation error <= 2^-16); on the staged prefill
+ *    path one fp16 plane of the row scaled by a power of two (11 significant
+ *    bits: about 3e-4 relative L2 on the outputs).
  * packed: from sbq_repack_w8.  scale: device fp32 [N].  bias: device fp32 [N]
  * or NULL.  y: device [M, N] (row stride ldy), dtype F32, F16 or BF16.
- * Accumulation is fp32.  M <= 32 runs the HBM-streaming MFMA GEMV; larger M
- * runs the LDS-tiled MFMA GEMM.
+ * Accumulation is fp32.  Routes (16-byte aligned rows, 64 | K): M <= 16 the
+ * HBM-streaming MFMA GEMV; 16 < M <= 64 the row-tile GEMV on narrow layers
+ * (N <= 4096 with little x to read, or wherever the workspace below is
+ * missing), else the LDS-tiled MFMA GEMM; other shapes up to 32 tokens the
+ * general GEMV.
  * workspace: optional (NULL, 0 is valid).  With >= sbq_w8_workspace_bytes(M,
- * K, x_dtype) bytes the prefill GEMM (M > 32, K % 64 == 0, aligned rows) runs
- * its fastest path: F16 x with per-row sums from a pre-pass; BF16 / F32 x
- * staged as power-of-two scaled fp16 planes (BF16: exact; F32: hi + lo, 22
- * significant bits) for the same fp16 MFMA kernel.  Without it, F16 / BF16 run
- * a slower tiled GEMM and F32 the register-staged bf16 hi + lo GEMM. */
+ * K, x_dtype) bytes the prefill GEMM (K % 64 == 0, aligned rows) runs its
+ * fastest path: F16 x with per-row sums from a pre-pass; BF16 / F32 x staged
+ * as a power-of-two scaled fp16 plane for the same fp16 MFMA kernel; with
+ * sbq_linear_workspace_bytes it also splits K over workgroups on small grids.
+ * Without it, F16 / BF16 run a slower tiled GEMM and F32 the register-staged
+ * bf16 hi + lo GEMM. */
 int sbq_linear_w8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   const uint8_t* packed, const float* scale, const float* bias, int64_t N,
                   void* y, int y_dtype, int64_t ldy,
@@ -146,8 +151,8 @@ int sbq_linear_w8_grouped(int count, const void* const* x, const int64_t* ldx, i
                           void* const* y, const int64_t* ldy, int y_dtype, void* stream);
 
 /* Workspace bytes that let sbq_linear_w8 run its fastest prefill path for an
- * [M, K] input of x_dtype: 2 * M floats (F16), plus M * K * 2 bytes (BF16) or
- * M * K * 4 bytes (F32) of staged activations, plus alignment slack.  0 for a
+ * [M, K] input of x_dtype: 2 * M floats, plus M * K * 2 bytes of staged
+ * activations for BF16 and F32 x, plus alignment slack.  0 for a
  * bad argument.  No counterpart in the reference (its CPU matmul needs no
  * scratch). */
 int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K, int x_dtype);
@@ -155,8 +160,9 @@ int64_t sbq_w8_workspace_bytes(int64_t M, int64_t K, int x_dtype);
 /* Workspace bytes that let sbq_linear_w8 (w8a8 = 0) or sbq_linear_w8a8
  * (w8a8 = 1) run their fastest path for y [M, N] = x [M, K] * W^T with x of
  * x_dtype: the sizes of sbq_w8_workspace_bytes / sbq_w8a8_workspace_bytes
- * plus, for prefill shapes whose grid would leave CUs idle, the tile counters
- * and fp32 / int32 partial tiles of a GEMM that splits K over workgroups (its
+ * plus, for shapes that reach the tiled GEMM with a grid that would leave CUs
+ * idle, the tile counters and fp32 / int32 partial tiles of a GEMM that
+ * splits K over workgroups (its
  * last split per tile adds the partials in a fixed order, so results do not
  * depend on timing).  Those entry points split K only when given this much;
  * with the smaller sizes they run the same shapes unsplit.  0 for a bad
@@ -168,8 +174,9 @@ int64_t sbq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype,
  * x_dtype, as sbq_linear_w8 (w8a8 = 0) and sbq_linear_w8a8 (w8a8 = 1) run it
  * when given sbq_linear_workspace_bytes of workspace: returns the block
  * configuration id (>= 0) and stores in *splits (if not NULL) the number of
- * workgroups K is split over.  It describes the calls that reach that GEMM;
- * small M runs the decode GEMV paths instead.  Host-only: needs no GPU.
+ * workgroups K is split over, or 0 when calls of this shape (16-byte aligned
+ * rows, that workspace) never reach the GEMM: the decode GEMVs and the
+ * row-tile GEMV run them.  Host-only: needs no GPU.
  * SBQ_ERR_ARG / SBQ_ERR_DTYPE for a bad argument.  No counterpart in the
  * reference (diagnostics and tests of the configuration choice). */
 int sbq_gemm_config(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8, int* splits);
@@ -178,7 +185,7 @@ int sbq_gemm_config(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8, int*
 
 /* Workspace bytes sbq_linear_w8a8 / sbq_act_qparams need for an [M, K] input:
  * 2.5 KiB of activation statistics plus M * ceil(K/64)*64 bytes for the
- * quantized activations of the tiled (M > 32) path, M floats of per-token
+ * quantized activations of the paths with a quantize pre-pass (M > 16), M floats of per-token
  * scales (sbq_linear_w8a8_token), plus alignment slack. */
 int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K);
 

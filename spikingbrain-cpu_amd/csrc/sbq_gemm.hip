@@ -13,8 +13,8 @@
 //           (q + 128) * 2^-24 (one v_perm per pair) and the epilogue removes
 //           128 * rowsum(x); bf16 activations meet exact bf16 weights.  Both
 //           run v_mfma_f32_16x16x32_{f16,bf16}.  With a workspace, fp32 and
-//           bf16 activations are first staged as row-scaled fp16 planes (fp32:
-//           hi + lo) for the fp16 kernel; without one, fp32 runs as bf16
+//           bf16 activations are first staged as a row-scaled fp16 plane (fp32:
+//           11 significant bits) for the fp16 kernel; without one, fp32 runs as bf16
 //           hi + lo planes in the register-staged kernel.  Epilogue:
 //           * scale[n] (+ bias[n]).
 //   W8A8:   the activations are quantized to s8 (xq - 128) once, by a
@@ -1259,7 +1259,7 @@ constexpr int kBN = 128, kBM = 128, kWN = 2, kWM = 2;
 
 W8Ws w8_ws_layout(int64_t M, int64_t K, int xt) {
   auto r256 = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
-  const int np = xt == XT_F32 ? 2 : (xt == XT_BF16 ? 1 : 0);
+  const int np = xt == XT_F32 || xt == XT_BF16 ? 1 : 0;  // one staged fp16 plane
   W8Ws l;
   l.rowsum = 0;
   l.rscale = r256(M * 4);
@@ -1303,8 +1303,8 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
         const int rc = launch_rowsum_f16(x, ldx, M, K, rowsum, st, zero, ncount);
         if (rc) return rc;
       } else {
-        // fp32 / bf16: scaled fp16 planes [hi | lo] per row, then the fp16 GEMM
-        const int np = xt == XT_F32 ? 2 : 1;
+        // fp32 / bf16: one scaled fp16 plane per row, then the fp16 GEMM
+        const int np = 1;
         _Float16* planes = (_Float16*)(w + l.planes);
         float* rscale = (float*)(w + l.rscale);
         const int rc = launch_stage_act(x, xt, ldx, M, K, planes, rowsum, rscale, st, zero, ncount);

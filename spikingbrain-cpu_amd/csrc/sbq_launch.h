@@ -90,7 +90,7 @@ DlPlan plan_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc, bool rsp
 int64_t split_area_bytes(const DlPlan& p);
 
 // W-only prefill scratch: [rowsum: M floats][rscale: M floats][fp16 planes: M x NP x K],
-// each part 256-byte aligned; NP = 2 for fp32 x, 1 for bf16, 0 for fp16.
+// each part 256-byte aligned; NP = 1 for fp32 and bf16 x, 0 for fp16.
 struct W8Ws {
   int64_t rowsum, rscale, planes, bytes;
 };

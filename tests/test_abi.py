@@ -55,7 +55,7 @@ def test_packed_bytes(lib):
     assert lib.sbq_w8a8_workspace_bytes(1, 4096) >= 256 * 8
     assert lib.sbq_w8_workspace_bytes(2048, 4096, 1) >= 2 * 2048 * 4 + 255  # fp16: row sums and scales
     assert lib.sbq_w8_workspace_bytes(2048, 4096, 2) >= 2048 * 4096 * 2     # bf16: one staged plane
-    assert lib.sbq_w8_workspace_bytes(2048, 4096, 0) >= 2048 * 4096 * 4     # fp32: two staged planes
+    assert lib.sbq_w8_workspace_bytes(2048, 4096, 0) >= 2048 * 4096 * 2     # fp32: one staged fp16 plane
     assert lib.sbq_w8_workspace_bytes(-1, 4096, 1) == 0
     assert lib.sbq_w8_workspace_bytes(16, 64, 7) == 0
 

@@ -182,10 +182,10 @@ def test_w8_gemm_block_configs(dev, M, N, K):
 @pytest.mark.parametrize("xd", ["f32", "bf16"])
 @pytest.mark.parametrize("M,N,K", [(64, 512, 2560), (200, 130, 4096), (512, 2048, 512), (300, 4096, 4096)])
 def test_w8_staged_prefill_rows(dev, M, N, K, xd):
-    """fp32 / bf16 prefill activations are staged as power-of-two scaled fp16
-    planes (fp32: hi + lo) for the fp16 GEMM when a workspace is given; rows
-    span 1e-30 .. 1e30, and each row must match the oracle on its own.  The
-    paths without a workspace are held to the same bar."""
+    """fp32 / bf16 prefill activations are staged as a power-of-two scaled
+    fp16 plane for the fp16 GEMM when a workspace is given; rows span
+    1e-30 .. 1e30, and each row must match the oracle on its own.  The paths
+    without a workspace are held to the weight-only tolerance."""
     announce(f"w8 staged M={M} N={N} K={K} x={xd}")
     w = make_weights(N, K, 9000 + N + K)
     q, s = oracle.quantize_per_channel(w.numpy())
@@ -198,8 +198,9 @@ def test_w8_staged_prefill_rows(dev, M, N, K, xd):
     for ws in (None, none):
         y = quant.linear_w8(xd_dev, lin.packed, lin.scale, None, N, workspace=ws).cpu().numpy().astype(np.float64)
         row_err = np.linalg.norm(y - ref, axis=1) / np.linalg.norm(ref, axis=1)
-        # staged fp32 keeps 22 significant bits, staged bf16 is exact: both far inside the tolerance
-        bar = (2e-5 if xd == "f32" else 2e-6) if ws is None else W8_TOL
+        # staged bf16 is exact; staged fp32 keeps 11 significant bits: a relative rounding error of at most
+        # 2^-11 per value, about 3e-4 relative L2 on a row's outputs (6e-4 allows for the row's spread)
+        bar = (6e-4 if xd == "f32" else 2e-6) if ws is None else W8_TOL
         assert row_err.max() <= bar, (ws is None, float(row_err.max()), int(row_err.argmax()))
 
 
@@ -755,7 +756,9 @@ def test_fused_w8_matches_parts(dev, M):
     for w, m, o in zip(ws, mods, outs):
         assert o.device.type == "cpu" and o.shape == (1, M, m.out_features)
         q, s = oracle.quantize_per_channel(w.numpy())
-        assert oracle.rel_l2(o.reshape(M, -1).numpy(), oracle.int8_linear(x.reshape(M, K).numpy(), q, s)) <= 1e-5
+        # fp32 x: bf16 high + remainder on the decode paths (M <= 16), one staged fp16 plane (11 bits) in the GEMM
+        bar = 1e-5 if M <= 16 else 6e-4
+        assert oracle.rel_l2(o.reshape(M, -1).numpy(), oracle.int8_linear(x.reshape(M, K).numpy(), q, s)) <= bar
 
 
 def test_fuse_linears_rejects_mixed_parts(dev):
