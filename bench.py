@@ -625,13 +625,16 @@ def summarize_gaps(d, match, command):
     return "\n".join(out) + "\n"
 
 
-def prefill_probe(ctx, M=2048, N=12288, K=4096, launches=100):
-    """The prefill operation alone (row-sum pre-pass + GEMM; int8 weights, fp16
-    x and y), for counter passes; enough back-to-back launches (~17 ms) for
-    the shader clock to settle under the load."""
+def prefill_probe(ctx, M=2048, N=12288, K=4096, launches=100, xdtype=None):
+    """The prefill operation alone (row-sum or staging pre-pass + GEMM; int8
+    weights, fp16 x unless xdtype says otherwise, fp16 y), for counter passes;
+    enough back-to-back launches (~17 ms) for the shader clock to settle under
+    the load."""
     torch, quant = ctx.torch, ctx.quant
     packed, s, _ = ctx.weights(N, K, 900)
     x = ctx.act(M, K, 901)
+    if xdtype is not None:
+        x = x.to(xdtype)
     y = torch.empty((M, N), dtype=torch.float16, device=ctx.dev)
     ws = quant.w8_workspace(M, K, ctx.dev, x.dtype, N)
     torch.cuda.synchronize()
@@ -838,6 +841,8 @@ def main():
                     help="print the traffic JSON from FETCH_SIZE and WRITE_SIZE passes over --traffic-probe")
     ap.add_argument("--prefill-probe", nargs="*", type=int, metavar="M N K",
                     help="only run the weight-only GEMM, M=2048 N=12288 K=4096 unless given (counter passes)")
+    ap.add_argument("--probe-x", default="float16", choices=("float16", "bfloat16", "float32"),
+                    help="activation dtype of --prefill-probe")
     ap.add_argument("--w8a8-probe", nargs="*", type=int, metavar="M N K",
                     help="only run the int8-dyn linear, M=2048 N=12288 K=4096 unless given (counter passes)")
     ap.add_argument("--only", metavar="NAME", help="run one extra measurement and print it (e.g. lm_head_greedy)")
@@ -879,7 +884,7 @@ def main():
         traffic_probe(ctx)
         return
     if args.prefill_probe is not None:
-        prefill_probe(ctx, *(args.prefill_probe or (2048, 12288, 4096)))
+        prefill_probe(ctx, *(args.prefill_probe or (2048, 12288, 4096)), xdtype=getattr(ctx.torch, args.probe_x))
         return
     if args.w8a8_probe is not None:
         w8a8_probe(ctx, *(args.w8a8_probe or (2048, 12288, 4096)))
@@ -893,6 +898,10 @@ def main():
         fn = {"lm_head_greedy": lm_head_greedy_bench, "device_state": device_state_bench,
               "device_state_hybrid": device_state_hybrid_both,
               "stack_fused": lambda ctx: stack_bench(ctx, Ms=sm, fused=True),
+              "w8a8": lambda ctx: [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)],
+              "prefill": lambda ctx: [prefill_bench(ctx, M) for M in (512, 2048, 8192)],
+              "prefill_other_x": lambda ctx: [prefill_bench(ctx, 2048, xdtype=dt)
+                                              for dt in (ctx.torch.bfloat16, ctx.torch.float32)],
               "w8a8_token": lambda ctx: [w8a8_bench(ctx, M, N, token=True) for M in (1, 128, 2048)
                                          for N in (4096, 12288)],
               "mid_m": lambda ctx: [midm_bench(ctx, M, N, fmt) for fmt in ("int8", "int8-dyn") for M in (64, 128, 256)
@@ -931,7 +940,7 @@ def main():
                                                xdtype=torch.float32)
         log("prefill GEMM")
         extra["prefill"] = [prefill_bench(ctx, M) for M in (512, 2048, 8192)]
-        # the reference model's own activations are fp32: staged as fp16 hi + lo planes
+        # the reference model's own activations are fp32: staged as a scaled fp16 plane
         extra["prefill_other_x"] = [prefill_bench(ctx, 2048, xdtype=dt)
                                     for dt in (ctx.torch.bfloat16, ctx.torch.float32)]
         # fp32 outputs (the reference returns fp32), with fp16 and fp32 activations

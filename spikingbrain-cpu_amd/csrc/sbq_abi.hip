@@ -290,7 +290,7 @@ int64_t sbq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype,
   const int64_t Nt = (N + 15) / 16, Kc = (K + 63) / 64;
   const int64_t base = w8a8 ? sbq_w8a8_workspace_bytes(M, K) : sbq_w8_workspace_bytes(M, K, x_dtype);
   if (M == 0 || !runs_tiled_gemm(M, N, K, x_dtype, w8a8 != 0)) return base;
-  // the GEMM's operands are s8 (W8A8) or fp16 (weight-only, fp32 / bf16 staged as fp16 planes)
+  // the GEMM's operands are s8 (W8A8) or fp16 (weight-only, fp32 / bf16 staged as an fp16 plane)
   return base + sbq::split_area_bytes(sbq::plan_gemm_dl(w8a8 != 0, 1, M, Nt, Kc, true));
 }
 
@@ -299,7 +299,7 @@ int sbq_gemm_config(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8, int*
   if (M < 1 || N < 1 || K < 1 || M > kIntMax || N > kIntMax || K > kIntMax || (w8a8 != 0 && w8a8 != 1))
     return SBQ_ERR_ARG;
   // with that workspace every activation dtype reaches the GEMM as fp16 (W-only:
-  // fp32 / bf16 staged as fp16 planes, row sums precomputed) or s8 (W8A8)
+  // fp32 / bf16 staged as an fp16 plane, row sums precomputed) or s8 (W8A8)
   const sbq::DlPlan p = sbq::plan_gemm_dl(w8a8 != 0, sbq::XT_F16, M, (N + 15) / 16, (K + 63) / 64, true);
   if (splits) *splits = runs_tiled_gemm(M, N, K, x_dtype, w8a8 != 0) ? p.splits : 0;
   return p.id;

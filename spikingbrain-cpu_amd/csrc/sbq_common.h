@@ -144,6 +144,24 @@ __device__ __forceinline__ void load8_f32(const void* x, int64_t ldx, int M, int
   }
 }
 
+// 8 consecutive activations at p (16-byte aligned, all in bounds) widened to
+// fp32, with no guard.
+template <int XT>
+__device__ __forceinline__ void load8_f32_vec(const typename XElem<XT>::T* p, float* t) {
+  typedef typename XElem<XT>::T T;
+  if constexpr (XT == XT_F32) {
+    const f32x4 a = *(const f32x4*)p;
+    const f32x4 b = *(const f32x4*)(p + 4);
+    t[0] = a.x; t[1] = a.y; t[2] = a.z; t[3] = a.w;
+    t[4] = b.x; t[5] = b.y; t[6] = b.z; t[7] = b.w;
+  } else {
+    typedef T v8 __attribute__((ext_vector_type(8)));
+    const v8 a = *(const v8*)p;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = XElem<XT>::to_f32(a[j]);
+  }
+}
+
 // fp32 -> (hi, lo) bf16 pair with hi + lo == v to 16 significant bits.
 __device__ __forceinline__ void split_bf16(float v, __bf16& hi, __bf16& lo) {
   hi = (__bf16)v;
@@ -151,7 +169,7 @@ __device__ __forceinline__ void split_bf16(float v, __bf16& hi, __bf16& lo) {
 }
 
 // Exponent e of the power-of-two row scale that puts a row's largest
-// magnitude mx into [2^14, 2^15) before the row is split into fp16 planes
+// magnitude mx into [2^14, 2^15) before the row is rounded to fp16
 // (exact scaling; no fp16 overflow, at most 2^28 of range lost to
 // subnormals below the maximum).  Rows with no finite nonzero maximum keep
 // e = 0.

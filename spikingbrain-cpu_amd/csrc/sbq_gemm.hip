@@ -295,7 +295,6 @@ struct GemmArgs {
   const float* qpbuf;   // I8 only: (s_x, zp as int bits)
   const float* rsum;    // fp16 W-only with RSP: per-row sums of x [M]
   const float* rscale;  // fp16 W-only with RSP, nullable: per-row output scale [M]
-  int kx;               // activation K tiles (0: Kc); 2 * Kc = two planes over the same weights
   int flags;            // bit 1: x rows vector loads; 2: y rows 4-element vector stores;
                         // 4: W8A8 per-token epilogue; 8: y and ldy 16-byte aligned
   // split K (gridDim.z > 1): partial tiles [tile][split] of dl_tile_bytes()
@@ -433,9 +432,8 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (SK ? (dl_min_waves<I8, XT, BN, BM
   }
   const int nt0 = bx * WT, m0 = by * BM;
   const int M = a.M, Kc = a.Kc, Nt = a.Nt;
-  // stages of activation K tiles: x tile kc meets weight tile kc mod Kc (the
-  // host keeps Kc % KT == 0)
-  const int KX = (a.kx > 0 ? a.kx : Kc) / KT;
+  // stage steps of KT K tiles (the host keeps Kc % KT == 0)
+  const int KX = Kc / KT;
   // split K over gridDim.z workgroups: split z takes stage steps [zb, zb + zc)
   // (the host keeps every split non-empty), its KG groups share them out
   const int S = SK ? (int)gridDim.z : 1, z = SK ? (int)blockIdx.z : 0;
@@ -484,10 +482,9 @@ __global__ __launch_bounds__(KG* WN* WM * 64, (SK ? (dl_min_waves<I8, XT, BN, BM
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
       const int kc = ks * KT + j;
-      const int kw = kc >= Kc ? kc - Kc : kc;
       const int sb = __builtin_amdgcn_readfirstlane((kg * NS + st) * STAGE + j * SUB);
 #pragma unroll
-      for (int i2 = 0; i2 < WT / GW; ++i2) lds_dma16_buf(wrs, woff[i2], kw * 1024, lds + sb + wslot + i2 * 1024);
+      for (int i2 = 0; i2 < WT / GW; ++i2) lds_dma16_buf(wrs, woff[i2], kc * 1024, lds + sb + wslot + i2 * 1024);
 #pragma unroll
       for (int i2 = 0; i2 < XR / GW; ++i2)
         lds_dma16_buf(xrs, xoff[i2], kc * (I8 ? 64 : 128), lds + sb + xslot + i2 * 1024);
@@ -955,6 +952,57 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const void* __restric
 }
 
 
+// Dense x (ldx == K, 16-byte aligned) with K % 64 == 0: the rows of x and of
+// xq (Kp == K) are one flat array each, so chunk c of 16 values goes from
+// x + 16c to xq + 16c with no division or padding.  QC chunks per thread, at
+// (block * QC + i) * 256 + thread; loads clamped to the last chunk, stores
+// guarded.
+template <int XT, int QC>
+__global__ __launch_bounds__(256) void quantize_dense_kernel(const void* __restrict__ x, int64_t nch,
+                                                             const float2* __restrict__ partials, int nparts,
+                                                             int8_t* __restrict__ xq, float* __restrict__ qp_out) {
+  typedef typename XElem<XT>::T T;
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  float t[QC][16];
+  int64_t cc[QC];
+#pragma unroll
+  for (int i = 0; i < QC; ++i) {
+    cc[i] = ((int64_t)blockIdx.x * QC + i) * blockDim.x + threadIdx.x;
+    const T* p = (const T*)x + min(cc[i], nch - 1) * 16;
+    if constexpr (XT == XT_F32) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 a = *(const f32x4*)(p + 4 * q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t[i][4 * q + j] = a[j];
+      }
+    } else {
+      const v8 a0 = *(const v8*)p, a1 = *(const v8*)(p + 8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        t[i][j] = XElem<XT>::to_f32(a0[j]);
+        t[i][8 + j] = XElem<XT>::to_f32(a1[j]);
+      }
+    }
+  }
+  __shared__ float red[16];
+  const ActQParams qp = block_qparams_from_partials(partials, nparts, red);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    qp_out[0] = qp.scale;
+    qp_out[1] = __int_as_float(qp.zp);
+  }
+#pragma unroll
+  for (int i = 0; i < QC; ++i) {
+    uint32_t d[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      d[w] = pack_act_s8x4(__builtin_fmaf(t[i][4 * w], qp.inv, qp.zpf), __builtin_fmaf(t[i][4 * w + 1], qp.inv, qp.zpf),
+                           __builtin_fmaf(t[i][4 * w + 2], qp.inv, qp.zpf),
+                           __builtin_fmaf(t[i][4 * w + 3], qp.inv, qp.zpf));
+    if (cc[i] < nch) *(u32x4*)(xq + cc[i] * 16) = (u32x4){d[0], d[1], d[2], d[3]};
+  }
+}
+
 // Direct-to-LDS configurations (BN, BM, WN, WM, NS, KG), indexed by id.
 #define SBQ_DL_CONFIGS(X) \
   X(0, 256, 128, 4, 2, 2, 1) \
@@ -1289,7 +1337,7 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
     a.x = x; a.ldx = ldx; a.M = (int)M; a.Kc = (int)Kc;
     a.packed = packed; a.scale = scale; a.bias = bias;
     a.N = (int)N; a.Nt = (int)Nt; a.y = y; a.yt = yt; a.ldy = ldy; a.flags = flags;
-    const int gxt = staged ? XT_F16 : xt;  // fp32 / bf16 activations are staged as fp16 planes
+    const int gxt = staged ? XT_F16 : xt;  // fp32 / bf16 activations are staged as an fp16 plane
     // split K when the grid is small and the scratch after the layout holds the partials
     const DlPlan plan = plan_gemm_dl(false, gxt, M, Nt, Kc, staged);
     int ncount = 0;
@@ -1304,12 +1352,11 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
         if (rc) return rc;
       } else {
         // fp32 / bf16: one scaled fp16 plane per row, then the fp16 GEMM
-        const int np = 1;
-        _Float16* planes = (_Float16*)(w + l.planes);
+        _Float16* plane = (_Float16*)(w + l.planes);
         float* rscale = (float*)(w + l.rscale);
-        const int rc = launch_stage_act(x, xt, ldx, M, K, planes, rowsum, rscale, st, zero, ncount);
+        const int rc = launch_stage_act(x, xt, ldx, M, K, plane, rowsum, rscale, st, zero, ncount);
         if (rc) return rc;
-        a.x = planes; a.ldx = np * K; a.kx = (int)(np * Kc); a.rscale = rscale;
+        a.x = plane; a.ldx = K; a.rscale = rscale;
         a.flags = flags | 1;
       }
     }
@@ -1347,6 +1394,13 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
   const int qc = chunks >= (int64_t)256 * 4 * 512 ? 4 : (chunks >= (int64_t)256 * 2 * 256 ? 2 : 1);
   const dim3 qgrid((unsigned)((chunks + 256 * qc - 1) / (256 * qc)));
   const bool qvec = xvec && K % 16 == 0;
+  const bool qdense = xvec && ldx == K && K % 64 == 0;  // flat rows in and out
+#define SBQ_QUANT_DENSE1(XT_, QC_)                                                                                  \
+  hipLaunchKernelGGL((quantize_dense_kernel<XT_, QC_>), qgrid, dim3(256), 0, st, x, chunks, partials, nparts, xq, qpbuf);
+#define SBQ_QUANT_DENSE(XT_)                       \
+  if (qc == 4) SBQ_QUANT_DENSE1(XT_, 4)            \
+  else if (qc == 2) SBQ_QUANT_DENSE1(XT_, 2)       \
+  else SBQ_QUANT_DENSE1(XT_, 1)
 #define SBQ_QUANT_LAUNCH1(XT_, VEC_, QC_)                                                                          \
   hipLaunchKernelGGL((quantize_act_kernel<XT_, VEC_, QC_>), qgrid, dim3(256), 0, st, x, ldx, (int)M, (int)K, (int)Kp, \
                      partials, nparts, xq, qpbuf, flags);
@@ -1360,12 +1414,23 @@ int launch_gemm_w8a8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, b
     else if (qc == 2) SBQ_QUANT_LAUNCH1(XT_, false, 2) \
     else SBQ_QUANT_LAUNCH1(XT_, false, 1)           \
   }
-  switch (xt) {
-    case XT_F16: SBQ_QUANT_LAUNCH(XT_F16) break;
-    case XT_BF16: SBQ_QUANT_LAUNCH(XT_BF16) break;
-    case XT_F32: SBQ_QUANT_LAUNCH(XT_F32) break;
-    default: return -2;
+  if (qdense) {
+    switch (xt) {
+      case XT_F16: SBQ_QUANT_DENSE(XT_F16) break;
+      case XT_BF16: SBQ_QUANT_DENSE(XT_BF16) break;
+      case XT_F32: SBQ_QUANT_DENSE(XT_F32) break;
+      default: return -2;
+    }
+  } else {
+    switch (xt) {
+      case XT_F16: SBQ_QUANT_LAUNCH(XT_F16) break;
+      case XT_BF16: SBQ_QUANT_LAUNCH(XT_BF16) break;
+      case XT_F32: SBQ_QUANT_LAUNCH(XT_F32) break;
+      default: return -2;
+    }
   }
+#undef SBQ_QUANT_DENSE
+#undef SBQ_QUANT_DENSE1
 #undef SBQ_QUANT_LAUNCH
 #undef SBQ_QUANT_LAUNCH1
   int rc = check_launch();

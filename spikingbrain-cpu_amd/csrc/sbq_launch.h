@@ -71,15 +71,15 @@ int launch_gemv_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
                    bool yvec, GemvArgmaxOut* am = nullptr);
 // ws: device scratch (nullable, 256-byte aligned) of ws_bytes bytes, laid out
 // by w8_ws_layout.  With enough of it the fp16 GEMM takes its per-row sums of x
-// from a pre-pass, and fp32 / bf16 activations are staged as scaled fp16 planes
-// for the same GEMM.
+// from a pre-pass, and fp32 / bf16 activations are staged as a scaled fp16
+// plane for the same GEMM.
 int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const uint8_t* packed,
                    const float* scale, const float* bias, int64_t N, void* y, int yt, int64_t ldy, void* ws,
                    int64_t ws_bytes, hipStream_t st, bool yvec);
 // split: scratch after the workspace's layout (split_area_bytes of the plan;
 // a shorter or null one runs the shape without splitting K).
 // Direct-to-LDS GEMM plan: block configuration id and K splits (1: none);
-// with splits, `tiles` output blocks of 128 x 64 and their partial tiles.
+// with splits, `tiles` output blocks of 64 x 64 and their partial tiles.
 struct DlPlan {
   int id, splits;
   int64_t tiles, part_bytes;
@@ -89,8 +89,8 @@ DlPlan plan_gemm_dl(bool i8, int xt, int64_t M, int64_t Nt, int64_t Kc, bool rsp
 // the partial tiles; the GEMM launchers take it after their other scratch.
 int64_t split_area_bytes(const DlPlan& p);
 
-// W-only prefill scratch: [rowsum: M floats][rscale: M floats][fp16 planes: M x NP x K],
-// each part 256-byte aligned; NP = 1 for fp32 and bf16 x, 0 for fp16.
+// W-only prefill scratch: [rowsum: M floats][rscale: M floats][fp16 plane: M x K for
+// fp32 and bf16 x, none for fp16], each part 256-byte aligned.
 struct W8Ws {
   int64_t rowsum, rscale, planes, bytes;
 };
@@ -105,7 +105,7 @@ int launch_quantize_rows_sym(const void* x, int xt, int64_t ldx, bool xvec, int6
 // Per-row sums in fp32 of fp16 x [M, K] (K % 8 == 0, 16-byte aligned rows).
 int launch_rowsum_f16(const void* x, int64_t ldx, int64_t M, int64_t K, float* out, hipStream_t st,
                       uint32_t* zero = nullptr, int nzero = 0);
-// fp32 / bf16 x [M, K] -> scaled fp16 planes, row sums and row scales.
+// fp32 / bf16 x [M, K] -> a scaled fp16 plane, row sums and row scales.
 int launch_stage_act(const void* x, int xt, int64_t ldx, int64_t M, int64_t K, _Float16* xs, float* rowsum,
                      float* rscale, hipStream_t st, uint32_t* zero = nullptr, int nzero = 0);
 

@@ -84,8 +84,6 @@ __global__ __launch_bounds__(256) void colsum_kernel(const int8_t* __restrict__ 
   if (lane == 0) colsum[n] = s;
 }
 
-// Per-block (min, max) of x [M, K]; block b covers flat rows/columns
-// b, b + gridDim.x, ... in 256-element strides.
 // Zero the split-K tile counters of the GEMM that follows a pre-pass (the
 // pre-pass runs first on the same stream, so the GEMM sees them zeroed).
 __device__ __forceinline__ void zero_counters(uint32_t* c, int n) {
@@ -93,13 +91,78 @@ __device__ __forceinline__ void zero_counters(uint32_t* c, int n) {
     for (int i = threadIdx.x; i < n; i += blockDim.x) c[i] = 0u;
 }
 
+// The block's (min, max) into partials[blockIdx.x]: wave reductions, then
+// thread 0 over the waves.
+__device__ __forceinline__ void store_block_minmax(float mn, float mx, float2* partials) {
+  __shared__ float red[32];
+  mn = wave_min(mn);
+  mx = wave_max(mx);
+  const int wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[2 * wid] = mn;
+    red[2 * wid + 1] = mx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < nw; ++w) {
+      mn = fminf(mn, red[2 * w]);
+      mx = fmaxf(mx, red[2 * w + 1]);
+    }
+    partials[blockIdx.x] = make_float2(mn, mx);
+  }
+}
+
+// Dense x (ldx == K, 16-byte aligned, K % 8 == 0): the M*K values are one flat
+// array of 8-value chunks (16 bytes of fp16 / bf16, 32 of fp32).  Thread t of
+// the grid folds chunks t, t + T, t + 2T, ... (T threads), U loads in flight
+// per round with no branch: indexes past the end are clamped to the last
+// chunk, whose values are already in the range (min and max are idempotent).
+// No division, no per-element guard.
+template <int XT, int U>
+__global__ __launch_bounds__(1024) void minmax_dense_kernel(const void* __restrict__ xv, int64_t nch,
+                                                            float2* __restrict__ partials,
+                                                            uint32_t* __restrict__ zero, int nzero) {
+  typedef typename XElem<XT>::T T;
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  zero_counters(zero, nzero);
+  const int64_t T_ = (int64_t)gridDim.x * blockDim.x;
+  float mn = 0.0f, mx = 0.0f;  // fbgemm's range always holds 0
+  for (int64_t c0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c0 < nch; c0 += U * T_) {
+    float t[U][8];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int64_t c = min(c0 + i * T_, nch - 1);
+      if constexpr (XT == XT_F32) {
+        const f32x4 a0 = *(const f32x4*)((const float*)xv + c * 8), a1 = *(const f32x4*)((const float*)xv + c * 8 + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          t[i][j] = a0[j];
+          t[i][4 + j] = a1[j];
+        }
+      } else {
+        const v8 a = *(const v8*)((const T*)xv + c * 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[i][j] = XElem<XT>::to_f32(a[j]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        mn = fminf(mn, t[i][j]);
+        mx = fmaxf(mx, t[i][j]);
+      }
+  }
+  store_block_minmax(mn, mx, partials);
+}
+
+// Per-block (min, max) of x [M, K] with any row stride: thread t of the grid
+// covers the 8-value chunks t, t + T, ... (T threads; chunks row by row).
 template <int XT>
 __global__ __launch_bounds__(1024) void minmax_partial_kernel(const void* __restrict__ xv, int M, int K, int64_t ldx,
                                                               float2* __restrict__ partials, int vec,
                                                               uint32_t* __restrict__ zero, int nzero) {
-  typedef typename XElem<XT>::T T;
   zero_counters(zero, nzero);
-  // 8-element chunks, row by row; block b covers chunks b, b + nparts, ...
   const int cpr = (K + 7) / 8;
   const int64_t nch = (int64_t)M * cpr;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -132,22 +195,7 @@ __global__ __launch_bounds__(1024) void minmax_partial_kernel(const void* __rest
     load8_f32<XT>(xv, ldx, M, K, m, k0, vec, t);
     fold(t, k0);
   }
-  __shared__ float red[32];
-  mn = wave_min(mn);
-  mx = wave_max(mx);
-  const int wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    red[2 * wid] = mn;
-    red[2 * wid + 1] = mx;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < nw; ++w) {
-      mn = fminf(mn, red[2 * w]);
-      mx = fmaxf(mx, red[2 * w + 1]);
-    }
-    partials[blockIdx.x] = make_float2(mn, mx);
-  }
+  store_block_minmax(mn, mx, partials);
 }
 
 __global__ __launch_bounds__(256) void qparams_kernel(const float2* __restrict__ partials, int nparts,
@@ -201,6 +249,15 @@ __global__ __launch_bounds__(256) void rowsum_f16_kernel(const _Float16* __restr
   const _Float16* p = x + (int64_t)row * ldx;
   float s0 = 0.0f, s1 = 0.0f;
   int k = lane * 8;
+  // eight loads in flight (a whole K = 4096 row in one round), then four, then
+  // one; the chunks are summed in the same order whichever loop takes them
+  for (; k + 7 * 512 < K; k += 8 * 512) {
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = *(const u32x4*)(p + k + j * 512);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) rowsum_acc(v[j], s0, s1);
+  }
   for (; k + 3 * 512 < K; k += 4 * 512) {
     u32x4 v[4];
 #pragma unroll
@@ -251,18 +308,18 @@ __global__ __launch_bounds__(256) void quantize_rows_sym_kernel(const void* __re
   }
 }
 
-// fp32 / bf16 activations -> power-of-two scaled fp16 planes for the fp16
+// fp32 / bf16 activations -> one power-of-two scaled fp16 plane for the fp16
 // prefill GEMM.  Row m is scaled by 2^e (max|x| * 2^e in [2^14, 2^15), an
-// exact scaling); plane 0 is hi = rn16(x * 2^e), plane 1 (NP = 2) is
-// lo = rn16(x * 2^e - hi).  bf16 values (8 significant bits) are exact in
-// plane 0 down to 2^28 below the row maximum; fp32 values keep 11 bits in one
-// plane (the prefill path: relative rounding error <= 2^-11 per value, about
-// 3e-4 relative L2 on the outputs, inside the 1e-3 weight-only tolerance, at
-// half the MFMA work of two planes) and 22 bits in two.
-// Output row m: [hi (K) | lo (K)] fp16 at xs + m * NP * K; rowsum[m] = the fp32
-// sum of every plane's fp16 values; rscale[m] = 2^-e.  One wave per row; rows
-// are 16-byte aligned and K % 64 == 0 on this path.
-template <int XT, int NP>
+// exact scaling) and rounded once: plane row m = rn16(x * 2^e).  bf16 values
+// (8 significant bits) are exact down to 2^28 below the row maximum; fp32
+// values keep 11 bits (relative rounding error <= 2^-11 per value, about 3e-4
+// relative L2 on the outputs, inside the 1e-3 weight-only tolerance).
+// rowsum[m] = the fp32 sum of the plane's fp16 values; rscale[m] = 2^-e.  One
+// wave per row; rows are 16-byte aligned and K % 64 == 0 on this path.  Rows
+// of at most 512 * C values are read once, every 8-value chunk of a lane in
+// flight together and held in registers for the conversion; longer rows are
+// read twice (maximum, then conversion), four chunks in flight.
+template <int XT, int C>
 __global__ __launch_bounds__(256) void stage_act_kernel(const void* __restrict__ xv, int64_t ldx, int M, int K,
                                                         _Float16* __restrict__ xs, float* __restrict__ rowsum,
                                                         float* __restrict__ rscale, uint32_t* __restrict__ zero,
@@ -270,34 +327,55 @@ __global__ __launch_bounds__(256) void stage_act_kernel(const void* __restrict__
   zero_counters(zero, nzero);
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= M) return;
-  float mx = 0.0f;
-  for (int k = lane * 8; k < K; k += 512) {
-    float t[8];
-    load8_f32<XT>(xv, ldx, M, K, row, k, true, t);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(t[j]));
-  }
-  mx = wave_max(mx);
-  const int e = row_scale_exp(mx);
-  const float sc = ldexpf(1.0f, e);
-  _Float16* out = xs + (int64_t)row * NP * K;
-  float s0 = 0.0f, s1 = 0.0f;
-  for (int k = lane * 8; k < K; k += 512) {
-    float t[8];
-    load8_f32<XT>(xv, ldx, M, K, row, k, true, t);
-    f16x8 hi, lo;
+  typedef typename XElem<XT>::T T;
+  const T* xr = (const T*)xv + (int64_t)row * ldx;
+  _Float16* out = xs + (int64_t)row * K;
+  float mx = 0.0f, s = 0.0f;
+  auto convert = [&](const float* t, float sc, int k) {
+    f16x8 h;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float v = t[j] * sc;
-      hi[j] = (_Float16)v;
-      lo[j] = (_Float16)(v - (float)hi[j]);
-      s0 += (float)hi[j];
-      if constexpr (NP == 2) s1 += (float)lo[j];
+      h[j] = (_Float16)(t[j] * sc);
+      s += (float)h[j];
     }
-    *(f16x8*)(out + k) = hi;
-    if constexpr (NP == 2) *(f16x8*)(out + K + k) = lo;
+    *(f16x8*)(out + k) = h;
+  };
+  int e;
+  if (K <= 512 * C) {
+    float t[C][8];
+#pragma unroll
+    for (int c = 0; c < C; ++c)  // clamped: chunks past the row repeat its last chunk, never converted
+      load8_f32_vec<XT>(xr + min(lane * 8 + c * 512, K - 8), t[c]);
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(t[c][j]));
+    e = row_scale_exp(wave_max(mx));
+    const float sc = ldexpf(1.0f, e);
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      if (lane * 8 + c * 512 < K) convert(t[c], sc, lane * 8 + c * 512);
+  } else {
+    for (int k0 = lane * 8; k0 < K; k0 += 4 * 512) {
+      float t[4][8];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) load8_f32_vec<XT>(xr + min(k0 + c * 512, K - 8), t[c]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(t[c][j]));
+    }
+    e = row_scale_exp(wave_max(mx));
+    const float sc = ldexpf(1.0f, e);
+    for (int k0 = lane * 8; k0 < K; k0 += 4 * 512) {
+      float t[4][8];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) load8_f32_vec<XT>(xr + min(k0 + c * 512, K - 8), t[c]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (k0 + c * 512 < K) convert(t[c], sc, k0 + c * 512);
+    }
   }
-  float s = s0 + s1;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
   if (lane == 0) {
@@ -421,6 +499,19 @@ int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t 
   const int64_t total = M * K;
   const int threads = total <= ((int64_t)1 << 19) ? 256 : (total <= ((int64_t)1 << 21) ? 512 : 1024);
   dim3 grid((unsigned)nparts), block(threads);
+  if (vec && ldx == K && K % 8 == 0) {  // one flat array of 8-value chunks
+    const int64_t nch = total / 8;
+#define SBQ_MINMAX_DENSE(XT_)                                                                                    \
+  hipLaunchKernelGGL((minmax_dense_kernel<XT_, 4>), grid, block, 0, st, x, nch, partials, zero, nzero);
+    switch (xt) {
+      case XT_F32: SBQ_MINMAX_DENSE(XT_F32) break;
+      case XT_F16: SBQ_MINMAX_DENSE(XT_F16) break;
+      case XT_BF16: SBQ_MINMAX_DENSE(XT_BF16) break;
+      default: return -2;
+    }
+#undef SBQ_MINMAX_DENSE
+    return check_launch();
+  }
   switch (xt) {
     case XT_F32: hipLaunchKernelGGL(minmax_partial_kernel<XT_F32>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec, zero, nzero); break;
     case XT_F16: hipLaunchKernelGGL(minmax_partial_kernel<XT_F16>, grid, block, 0, st, x, (int)M, (int)K, ldx, partials, vec, zero, nzero); break;
@@ -446,10 +537,10 @@ int launch_stage_act(const void* x, int xt, int64_t ldx, int64_t M, int64_t K, _
                      float* rscale, hipStream_t st, uint32_t* zero, int nzero) {
   const dim3 grid((unsigned)((M + 3) / 4)), block(256);
   if (xt == XT_F32)
-    hipLaunchKernelGGL((stage_act_kernel<XT_F32, 1>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale,
+    hipLaunchKernelGGL((stage_act_kernel<XT_F32, 8>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale,
                        zero, nzero);
   else if (xt == XT_BF16)
-    hipLaunchKernelGGL((stage_act_kernel<XT_BF16, 1>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale,
+    hipLaunchKernelGGL((stage_act_kernel<XT_BF16, 8>), grid, block, 0, st, x, ldx, (int)M, (int)K, xs, rowsum, rscale,
                        zero, nzero);
   else
     return -2;
