@@ -1143,3 +1143,59 @@ def test_w8a8_gemv_row_tiles(dev, M, N, K):
         r_, c_ = torch.from_numpy(rows).to(dev), torch.from_numpy(cols).to(dev)
         np.testing.assert_array_equal(acc[r_][:, c_].cpu().numpy(), acc_ref)
         np.testing.assert_array_equal(pick(y, rows, cols), y_ref)
+
+
+# ---------------------------------------------------------------------------
+# activation pre-passes over every row layout
+# ---------------------------------------------------------------------------
+PREPASS_CASES = [  # (M, N, K): the tiled GEMM (M = 300), its split-K plan (M = 100); K = 8192 takes the staging
+    # pass's two-read path (rows longer than its registers hold), K = 2576 ragged K tiles
+    (300, 1000, 2560), (300, 1000, 8192), (100, 2048, 4096), (300, 520, 2576),
+]
+
+
+def _layout(x, layout, dev):
+    """x [M, K] on the GPU as dense rows, 16-byte aligned rows 64 elements
+    apart beyond K, or rows starting one element past a 16-byte boundary."""
+    M, K = x.shape
+    if layout == "dense":
+        return x.to(dev)
+    wide = torch.zeros((M, K + 64), dtype=x.dtype, device=dev)
+    if layout == "strided":
+        return wide[:, :K].copy_(x.to(dev))
+    return wide[:, 1:1 + K].copy_(x.to(dev))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", PREPASS_CASES)
+@pytest.mark.parametrize("xd", ["f16", "bf16", "f32"])
+def test_prepass_row_layouts_match_oracle(dev, M, N, K, xd):
+    """The pre-passes in front of the GEMMs read dense rows as one flat array
+    (min/max, quantize) and row by row otherwise; the staging pass holds a row
+    in registers up to 4096 values and reads it twice beyond.  Every layout
+    and activation dtype against the oracle on sampled rows and channels:
+    int8-dyn acc and y bit-exact; weight-only within the fp16 GEMM bar for
+    fp16 / bf16 x and 1e-3 for fp32 x (one staged fp16 plane)."""
+    announce(f"pre-pass layouts M={M} N={N} K={K} x={xd}")
+    w = gpu_weight(N, K, 980, dev)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(981))
+    lin = quant.Int8Linear(w, b.to(dev))
+    dyn = quant.DynamicInt8Linear(w, b.to(dev))
+    cols = tile_sample(N, 982, cap=64)
+    q, s = ref_rows(w, cols)
+    del w
+    x = cpu_x(M, K, 983, outliers=True).to(DT[xd])
+    xv = x.float().numpy()
+    rows = tile_sample(M, 984)
+    r_, c_ = torch.from_numpy(rows).to(dev), torch.from_numpy(cols).to(dev)
+    ref = oracle.int8_linear(xv[rows], q, s, b.numpy()[cols])
+    acc_ref, y_ref = ref_w8a8(xv, rows, q, s, b.numpy()[cols])
+    for layout in ("dense", "strided", "offset"):
+        xg = _layout(x, layout, dev)
+        y = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N, workspace=quant.w8_workspace(M, K, dev, DT[xd], N))
+        assert oracle.rel_l2(pick(y, rows, cols), ref) <= (W8_TOL if xd == "f32" else W8_TOL_GEMM_F16), layout
+        acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+        y8 = quant.linear_w8a8(xg, dyn.packed, dyn.scale, dyn.colsum, dyn.bias, N, acc_out=acc,
+                               workspace=quant.w8a8_workspace(M, K, dev, N, DT[xd]))
+        np.testing.assert_array_equal(acc[r_][:, c_].cpu().numpy(), acc_ref, err_msg=layout)
+        np.testing.assert_array_equal(pick(y8, rows, cols), y_ref, err_msg=layout)
