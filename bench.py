@@ -247,6 +247,51 @@ def lm_head_greedy_bench(ctx, V=151936, K=4096, M=1, steps=40, warmup=5):
     return res
 
 
+def sample_bench(ctx, V=151936, M=1, steps=40, warmup=5):
+    """The engine's non-greedy sampling step (engine.py:29-42) over one row of
+    lm_head logits (fp32, N(0, 2.5)), with the logits left on the GPU:
+    sbq_sample_rows (radix selection, no sort) for the engine's default
+    parameters (temperature 0.7, top_p 0.9), with top-k 50 as well, and with
+    neither; beside it the reference's expression run by torch's own GPU ops
+    (division, topk, softmax, sort, cumsum, scatter, multinomial with a GPU
+    generator), timed over the same number of eager calls."""
+    torch, quant = ctx.torch, ctx.quant
+    logits = torch.randn(M, V, generator=torch.Generator().manual_seed(5)).mul_(2.5).to(ctx.dev)
+    u = torch.rand(M, generator=torch.Generator().manual_seed(6)).to(ctx.dev)
+    ws = quant.sample_workspace(M, V, ctx.dev)
+    res = {"V": V, "M": M}
+    for name, (T, k, p) in (("default_T0.7_p0.9", (0.7, 0, 0.9)), ("T0.7_k50_p0.9", (0.7, 50, 0.9)),
+                            ("T1_no_cut", (1.0, 0, 1.0))):
+        res[f"sbq_{name}_us"] = ctx.time_steps(lambda c, T=T, k=k, p=p: quant.sample_tokens(logits, T, p, k, u=u,
+                                                                                              workspace=ws),
+                                               4, steps, warmup) * 1e3
+    gen = torch.Generator(device=ctx.dev).manual_seed(7)
+
+    def torch_sample(T, k, p):
+        z = logits[0] / T
+        if k > 0:
+            z = z.masked_fill(z < torch.topk(z, min(k, z.numel())).values[-1], float("-inf"))
+        pr = torch.softmax(z, -1)
+        if 0 < p < 1:
+            sp, order = pr.sort(descending=True)
+            sp = sp * (sp.cumsum(0) - sp < p)
+            pr = torch.zeros_like(pr).scatter_(0, order, sp)
+        return torch.multinomial(pr / pr.sum(), 1, generator=gen)
+
+    for name, (T, k, p) in (("default_T0.7_p0.9", (0.7, 0, 0.9)), ("T0.7_k50_p0.9", (0.7, 50, 0.9))):
+        for _ in range(warmup):
+            torch_sample(T, k, p)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            torch_sample(T, k, p)
+        e1.record()
+        torch.cuda.synchronize()
+        res[f"torch_ops_{name}_us"] = e0.elapsed_time(e1) / steps * 1e3
+    return res
+
+
 def device_state_bench(ctx, fmt="int8", H=2048, F=5632, blocks=4, V=32000, heads=16, max_len=512, steps=48):
     """Greedy decoding with a toy decoder (tests/toy_decoder.py: our own
     small model of the reference's projection pattern, random weights) in
@@ -897,6 +942,7 @@ def main():
         sm = tuple(args.stack_m)
         fn = {"lm_head_greedy": lm_head_greedy_bench, "device_state": device_state_bench,
               "device_state_hybrid": device_state_hybrid_both,
+              "sample": sample_bench,
               "stack_fused": lambda ctx: stack_bench(ctx, Ms=sm, fused=True),
               "w8a8": lambda ctx: [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)],
               "prefill": lambda ctx: [prefill_bench(ctx, M) for M in (512, 2048, 8192)],
@@ -952,6 +998,8 @@ def main():
                           for N in (4096, 12288)]
         log("lm_head and its greedy token")
         extra["lm_head_greedy"] = lm_head_greedy_bench(ctx)
+        log("sampling step over the lm_head logits (temperature, top-k, top-p)")
+        extra["sample"] = sample_bench(ctx)
         log("device-resident decode (toy decoder)")
         extra["device_state"] = device_state_bench(ctx)
         log("device-resident decode, hybrid layer pattern at the checkpoint's sizes")

@@ -32,6 +32,8 @@
  *                                model.py:447), so the logits need not leave the GPU
  *   sbq_linear_w8_argmax,     <- spikingbrain_cpu/model.py:445-447 (lm_head) and
  *   sbq_linear_w8a8_argmax       engine.py:30-31 (its greedy token) in one launch
+ *   sbq_sample_rows           <- spikingbrain_cpu/engine.py:29-42 sample (temperature,
+ *                                top-k, top-p and the draw) over the lm_head logits
  */
 #ifndef SBQ_H_
 #define SBQ_H_
@@ -312,6 +314,32 @@ int sbq_linear_w8a8_argmax(const void* x, int x_dtype, int64_t M, int64_t K, int
  * stride ldy); NaN ranks above every number (torch.argmax semantics).
  * idx: device int64 [M]. */
 int sbq_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* idx, void* stream);
+
+/* ---- non-greedy sampling (engine.py:29-42, sample) ---- */
+
+/* Workspace bytes of sbq_sample_rows for M rows (about 130 KB per row; any
+ * vocabulary size up to 2^31 - 1).  0 for a bad argument. */
+int64_t sbq_sample_workspace_bytes(int64_t M, int64_t V);
+
+/* tokens[m] = the engine's sample() of row m of fp32 logits [M, V] (row
+ * stride ld), as spikingbrain_cpu/engine.py:29-42 computes it:
+ *   temperature <= 0: the greedy token (sbq_argmax_rows; u and the workspace
+ *     may be NULL);
+ *   z = logits / temperature (fp32 division); top_k > 0: tokens below the
+ *     min(top_k, V)-th largest z are masked; p = softmax(z);
+ *   0 < top_p < 1: a token is kept while the probability mass of the tokens
+ *     above it stays below top_p (ties at that boundary are all kept);
+ *   the draw: the first index (vocabulary order) whose prefix of kept mass
+ *     exceeds u[m] * (kept mass), u: device fp32 [M] uniforms in [0, 1), one
+ *     per row, drawn by the caller (torch.multinomial's distribution; the
+ *     caller's generator supplies the randomness).
+ * Masses are exact sums of the fp32 probabilities truncated to 2^-40, so the
+ * result does not depend on timing.  A row with a NaN, or an infinite
+ * maximum after the division (where the reference raises), gets token -1.
+ * tokens: device int64 [M].  M <= 65535.  Rows are independent. */
+int sbq_sample_rows(const float* logits, int64_t M, int64_t V, int64_t ld, float temperature, int64_t top_k,
+                    float top_p, const float* u, int64_t* tokens, void* workspace, size_t workspace_bytes,
+                    void* stream);
 
 #ifdef __cplusplus
 }

@@ -32,6 +32,14 @@ How each function is pinned (tests/test_oracle.py):
   applied to activation rows (pinned above), the int32 product is checked
   against ``torch._int_mm``, and per-tensor-scale and (acc*s_t)*s_w epilogue
   mutants must fail.
+* ``sample_probs`` / ``sample_token`` (the engine's sample, engine.py:29-42,
+  with the caller's uniform in place of torch.multinomial's generator):
+  against the reference's own expression evaluated with torch CPU ops (topk,
+  masked_fill, softmax, sort, cumsum, scatter); the defining properties (the
+  kept mass reaches top_p and the smallest kept token is needed for it, top_k
+  = 1 keeps the argmax, ties at the k-th value are kept); inverse-CDF draw
+  frequencies over a fine grid of uniforms; mutants (inclusive cumsum, ties
+  dropped at the k-th value, temperature multiplied) must fail.
 """
 from __future__ import annotations
 
@@ -249,3 +257,48 @@ def rel_l2(a, b) -> float:
 
 def cpu_threads() -> int:
     return len(os.sched_getaffinity(0))
+
+
+def sample_probs(logits, temperature: float, top_k: int = 0, top_p: float = 1.0) -> np.ndarray:
+    """engine.py:32-41 for one row of logits: the (unnormalized) probabilities
+    the reference hands to torch.multinomial, float32 [V].  fp32 division by
+    the temperature; top-k masks z below the k-th largest to -inf (ties with
+    it stay); softmax (exp and sum in float64, rounded to fp32); top-p keeps a
+    token in the descending order while cumsum - p < top_p, with torch CPU's
+    cumsum (float64 accumulation, fp32 results) and a stable sort."""
+    x = np.asarray(logits, np.float32)
+    z = (x / np.float32(temperature)).astype(np.float32)
+    if top_k > 0:
+        k = min(int(top_k), z.size)
+        kth = np.sort(z)[-k]
+        z = np.where(z < kth, np.float32(-np.inf), z).astype(np.float32)
+    m = z.max()
+    e = np.exp((z - m).astype(np.float32).astype(np.float64))
+    p = (e / e.sum()).astype(np.float32)
+    if 0 < top_p < 1:
+        order = np.argsort(-p, kind="stable")
+        sp = p[order]
+        csum = np.cumsum(sp.astype(np.float64)).astype(np.float32)
+        keep = (csum - sp) < np.float32(top_p)
+        out = np.zeros_like(p)
+        out[order] = sp * keep
+        p = out
+    return p
+
+
+def sample_token(logits, temperature: float, top_k: int = 0, top_p: float = 1.0, u: float = 0.5) -> int:
+    """engine.py:29-42 with the draw made from the uniform u in [0, 1): the
+    greedy token for temperature <= 0; otherwise the first index whose prefix
+    of sample_probs exceeds u times their sum (the inverse of the distribution
+    torch.multinomial samples).  -1 where the reference raises: a NaN logit,
+    or an infinite maximum after the division."""
+    x = np.asarray(logits, np.float32)
+    if temperature <= 0:
+        nan = np.flatnonzero(np.isnan(x))
+        return int(nan[0]) if nan.size else int(np.argmax(x))
+    z = (x / np.float32(temperature)).astype(np.float32)
+    if np.isnan(z).any() or not np.isfinite(z.max()):
+        return -1
+    c = np.cumsum(sample_probs(x, temperature, top_k, top_p).astype(np.float64))
+    return int(np.searchsorted(c, u * c[-1], side="right"))
+

@@ -456,4 +456,24 @@ int sbq_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* 
   return sbq::launch_argmax_rows(y, M, N, ldy, idx, (hipStream_t)stream);
 }
 
+int64_t sbq_sample_workspace_bytes(int64_t M, int64_t V) {
+  if (M < 0 || V < 1 || M > kIntMax || V > kIntMax) return 0;
+  return sbq::sample_workspace_bytes(M) + 256;  // + alignment slack
+}
+
+int sbq_sample_rows(const float* logits, int64_t M, int64_t V, int64_t ld, float temperature, int64_t top_k,
+                    float top_p, const float* u, int64_t* tokens, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  if (M < 0 || V < 1 || ld < V || V > kIntMax || M > 65535) return SBQ_ERR_ARG;
+  if (temperature != temperature || top_p != top_p) return SBQ_ERR_ARG;
+  if (M == 0) return SBQ_OK;
+  if (!logits || !tokens) return SBQ_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (temperature <= 0.0f) return sbq::launch_argmax_rows(logits, M, V, ld, tokens, st);  // engine.py:30-31
+  if (!u) return SBQ_ERR_ARG;
+  if (!workspace || (int64_t)workspace_bytes < sbq_sample_workspace_bytes(M, V)) return SBQ_ERR_WORKSPACE;
+  void* ws = (void*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  return sbq::launch_sample_rows(logits, M, V, ld, temperature, top_k, top_p, u, tokens, ws, st);
+}
+
 }  // extern "C"

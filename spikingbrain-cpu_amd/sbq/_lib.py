@@ -43,6 +43,8 @@ SIGNATURES = {
     "sbq_argmax_rows": (_I, [_P, _L, _L, _L, _P, _P]),
     "sbq_linear_w8_argmax": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _L, _P, _L, _P, _P, _S, _P, _P]),
     "sbq_linear_w8a8_argmax": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _L, _P, _L, _P, _P, _S, _P, _P]),
+    "sbq_sample_workspace_bytes": (_L, [_L, _L]),
+    "sbq_sample_rows": (_I, [_P, _L, _L, _L, ctypes.c_float, _L, ctypes.c_float, _P, _P, _P, _S, _P]),
 }
 
 _lib = None

@@ -430,6 +430,64 @@ def greedy_tokens(logits: torch.Tensor) -> torch.Tensor:
     return out.reshape(shape[:-1])
 
 
+def sample_workspace(M: int, V: int, device: torch.device) -> torch.Tensor:
+    """Scratch of sample_tokens for M rows of V logits."""
+    return torch.empty((_lib.load().sbq_sample_workspace_bytes(M, V),), dtype=torch.uint8, device=device)
+
+
+def sample_tokens(logits: torch.Tensor, temperature: float, top_p: float = 1.0, top_k: int = 0,
+                  u: torch.Tensor | None = None, generator: torch.Generator | None = None,
+                  workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """engine.py:29-42 (`sample`) on the GPU: int64 [...] of tokens drawn from
+    fp32 GPU logits [..., V] with the engine's temperature, top-k and top-p,
+    one draw per row, without copying the logits to the host.
+
+    temperature <= 0 is the greedy token (greedy_tokens).  Otherwise the draw
+    takes one uniform in [0, 1) per row: `u` (fp32, on the logits' device), or
+    torch.rand from `generator` (a CPU generator, as the engine passes, or one
+    on the logits' device) - the randomness stays the caller's, as with
+    torch.multinomial.  Tokens whose z ties the top-p boundary are all kept.
+    A row with a NaN (or an infinite maximum after the division) gets -1, where
+    the reference raises."""
+    if logits.dtype != torch.float32 or not logits.is_cuda:
+        raise ValueError("sample_tokens expects fp32 GPU logits")
+    if temperature != temperature or top_p != top_p:
+        raise ValueError("temperature and top_p must be numbers")
+    shape = logits.shape
+    y = logits.reshape(-1, shape[-1])
+    if y.stride(-1) != 1:
+        y = y.contiguous()
+    M, V = y.shape
+    out = torch.empty((M,), dtype=torch.int64, device=y.device)
+    if temperature <= 0:
+        return greedy_tokens(logits)
+    if u is None:
+        if generator is not None and generator.device.type == "cuda":
+            u = torch.rand((M,), generator=generator, device=y.device)
+        else:
+            u = torch.rand((M,), generator=generator).to(y.device)
+    if u.dtype != torch.float32 or u.device != y.device or u.numel() != M or not u.is_contiguous():
+        raise ValueError("u must be a contiguous fp32 tensor of one uniform per row on the logits' device")
+    ws = workspace if workspace is not None else sample_workspace(M, V, y.device)
+    if ws.dtype != torch.uint8 or ws.device != y.device:
+        raise ValueError("workspace must be a uint8 tensor on the logits' device")
+    with torch.cuda.device(y.device):
+        _lib.check(_lib.load().sbq_sample_rows(_ptr(y), M, V, y.stride(0), float(temperature), int(top_k),
+                                               float(top_p), _ptr(u), _ptr(out), _ptr(ws), _nbytes(ws),
+                                               _stream(y.device)), "sbq_sample_rows")
+    return out.reshape(shape[:-1])
+
+
+def sample(logits: torch.Tensor, params, generator: torch.Generator | None = None) -> int:
+    """Drop-in for the engine's sample(logits, params, generator)
+    (engine.py:29-42) with the logits on the GPU: the same SamplingParams
+    fields (temperature, top_k, top_p), one uniform drawn from `generator`,
+    and only the token crosses to the host."""
+    tok = sample_tokens(logits.reshape(1, -1), params.temperature, params.top_p, params.top_k,
+                        generator=generator)
+    return int(tok[0])
+
+
 def argmax_state(device: torch.device) -> torch.Tensor:
     """The zeroed state (keys and count) of linear_w8_argmax /
     linear_w8a8_argmax: every call leaves it zero again, so one state serves

@@ -302,3 +302,96 @@ def test_pack_layout_model():
     # padding decodes to q = 0
     off = ((1 * Kc + 1) * 64 + 0 * 16 + 10) * 16 + 0  # row 26 (padded)
     assert p[off] == 0x80
+
+
+# ---------------------------------------------------------------------------
+# the engine's sampling step (engine.py:29-42)
+# ---------------------------------------------------------------------------
+def _torch_kept_probs(x, T, k, p):
+    """engine.py:32-41 evaluated by torch CPU ops: torch.topk for the k-th
+    value, torch.softmax, a descending torch.sort and torch.cumsum."""
+    z = torch.from_numpy(np.asarray(x, np.float32)) / T
+    if k > 0:
+        z = torch.where(z < torch.topk(z, min(k, z.numel())).values[-1], torch.tensor(float("-inf")), z)
+    pr = torch.softmax(z, -1)
+    if 0 < p < 1:
+        vals, idx = torch.sort(pr, descending=True, stable=True)
+        drop = (torch.cumsum(vals, 0) - vals) >= p
+        pr = pr.clone()
+        pr[idx[drop]] = 0.0
+    return pr.numpy()
+
+
+SAMPLE_PARAMS = [(0.7, 0, 0.9), (1.0, 40, 1.0), (0.7, 40, 0.8), (1.3, 0, 1.0), (0.5, 1, 1.0), (1.0, 0, 0.05),
+                 (0.8, 10**6, 0.95)]
+
+
+@pytest.mark.parametrize("T,k,p", SAMPLE_PARAMS)
+def test_sample_probs_match_torch_expression(T, k, p):
+    for seed, scale in ((0, 2.0), (1, 0.5), (2, 6.0)):
+        x = (np.random.default_rng(seed).standard_normal(5003) * scale).astype(np.float32)
+        got = oracle.sample_probs(x, T, k, p)
+        ref = _torch_kept_probs(x, T, k, p)
+        np.testing.assert_array_equal(got > 0, ref > 0)
+        np.testing.assert_allclose(got, ref, rtol=3e-6, atol=1e-30)
+
+
+def test_sample_probs_defining_properties():
+    x = (np.random.default_rng(5).standard_normal(2000) * 3).astype(np.float32)
+    # top-k = 1 keeps the argmax alone
+    p1 = oracle.sample_probs(x, 0.7, 1, 1.0)
+    assert np.flatnonzero(p1).tolist() == [int(np.argmax(x))]
+    # top-p: the kept tokens are the most probable ones, their mass reaches
+    # top_p, and without the least probable kept token it does not
+    full = oracle.sample_probs(x, 0.9, 0, 1.0).astype(np.float64)
+    for top_p in (0.3, 0.6, 0.9, 0.99):
+        kept = oracle.sample_probs(x, 0.9, 0, top_p) > 0
+        assert full[kept].min() >= full[~kept].max()
+        assert full[kept].sum() >= top_p - 1e-6
+        assert full[kept].sum() - full[kept].min() < top_p + 1e-6
+    # ties with the k-th largest value are kept (the mask is z < kth)
+    xt = np.array([1.0, 5.0, 3.0, 5.0, 4.0, 5.0, 2.0], np.float32)
+    assert np.flatnonzero(oracle.sample_probs(xt, 1.0, 2, 1.0)).tolist() == [1, 3, 5]
+    assert np.flatnonzero(oracle.sample_probs(xt, 1.0, 4, 1.0)).tolist() == [1, 3, 4, 5]
+    # the temperature divides the logits: p ~ exp(x / T)
+    pt = oracle.sample_probs(xt, 2.0, 0, 1.0).astype(np.float64)
+    np.testing.assert_allclose(pt, np.exp(xt / 2.0) / np.exp(xt / 2.0).sum(), rtol=1e-6)
+
+
+def test_sample_probs_mutants_fail():
+    # inclusive instead of the reference's exclusive cumsum
+    probs = np.array([0.5, 0.3, 0.2], np.float32)
+    x = np.log(probs)
+    kept = oracle.sample_probs(x, 1.0, 0, 0.5) > 0
+    assert kept.tolist() == [True, False, False]
+    incl = np.cumsum(probs) < 0.5
+    assert incl.tolist() != kept.tolist()
+    # dropping the ties at the k-th value
+    xt = np.array([1.0, 5.0, 3.0, 5.0, 4.0], np.float32)
+    kept = oracle.sample_probs(xt, 1.0, 1, 1.0) > 0
+    assert kept.sum() == 2 and kept.sum() != 1
+    # multiplying by the temperature instead of dividing
+    pt = oracle.sample_probs(xt, 2.0, 0, 1.0).astype(np.float64)
+    assert not np.allclose(pt, np.exp(xt * 2.0) / np.exp(xt * 2.0).sum(), rtol=1e-3)
+
+
+def test_sample_token_draw_and_edge_cases():
+    x = (np.random.default_rng(9).standard_normal(300) * 1.5).astype(np.float32)
+    T, k, p = 0.8, 25, 0.9
+    probs = oracle.sample_probs(x, T, k, p).astype(np.float64)
+    probs /= probs.sum()
+    n = 20000
+    counts = np.bincount([oracle.sample_token(x, T, k, p, (i + 0.5) / n) for i in range(n)], minlength=x.size)
+    # inverse CDF over a uniform grid: each token takes its share of the grid to within one point
+    assert np.abs(counts - n * probs).max() <= 1.0 + 1e-9
+    # greedy branch, NaN and infinite maxima
+    assert oracle.sample_token(x, 0.0) == int(np.argmax(x))
+    xn = x.copy()
+    xn[7] = np.nan
+    assert oracle.sample_token(xn, 0.0) == 7 and oracle.sample_token(xn, 0.7, 0, 0.9, 0.5) == -1
+    xi = x.copy()
+    xi[3] = np.inf
+    assert oracle.sample_token(xi, 0.7, 0, 0.9, 0.5) == -1
+    xm = x.copy()
+    xm[3] = -np.inf
+    assert oracle.sample_token(xm, 0.7, 0, 1.0, 0.5) != 3
