@@ -15,15 +15,18 @@
 //
 // No sort: the k-th largest z and the top-p boundary are found by radix
 // selection over an order-preserving 32-bit key of z, 8 bits per pass, from
-// per-workgroup histograms (token counts for top-k; for top-p the mass
-// exp(z - max), in 2^-40 fixed point, so that every sum is exact and
-// independent of the order the atomics land in; top_p is applied to the
-// kept mass as top_p * sum, which is the normalized condition).  Every launch
-// reads the row again from L2 (608 KB at V = 151936); a workgroup that needs
-// the outcome of the previous pass re-derives it from that pass's histograms
-// (identical in every workgroup), so no workgroup waits for another.  The
-// first pass of each selection rides on the launch before it (the max pass,
-// the softmax-sum pass).  Rows are independent (grid.y).  Differences from
+// histograms of token counts (top-k) or of the mass exp(z - max) (top-p), in
+// 2^-40 fixed point, so that every sum is exact and independent of the order
+// the atomics land in; top_p is applied to the kept mass as top_p * sum,
+// which is the normalized condition.  Each workgroup builds its histogram in
+// LDS and adds it into the pass's row histogram with device-scope atomics
+// (the first launch zeroes those; top-k's first pass, in that launch, keeps
+// one histogram per workgroup instead).  Every launch reads the row again
+// from L2 (608 KB at V = 151936); a workgroup that needs the outcome of the
+// previous pass re-derives it from that pass's histogram (identical in every
+// workgroup), so no workgroup waits for another.  The first pass of each
+// selection rides on the launch before it (the max pass, the softmax-sum
+// pass).  Rows are independent (grid.y).  Differences from
 // the reference's sort-based form: tokens whose z ties the top-p boundary
 // are all kept (the sort keeps some of them, in its own order), and a
 // token's mass is exp(z - max) truncated to 2^-40.
@@ -35,7 +38,7 @@
 namespace sbq {
 
 constexpr int kSampThreads = 1024;
-constexpr int kSampMaxBlocks = 32;   // workgroups per row
+constexpr int kSampMaxBlocks = 64;   // workgroups per row (one wave's lanes sum their per-workgroup values)
 constexpr int kSampCopies = 16;      // LDS copies of each histogram bin (atomics of one wave spread over them)
 constexpr double kSampFix = 1099511627776.0;  // 2^40: exp(z - max) in (0, 1] -> fixed point
 
@@ -43,14 +46,15 @@ constexpr double kSampFix = 1099511627776.0;  // 2^40: exp(z - max) in (0, 1] ->
 struct SampRow {
   static constexpr int64_t kHead = 0;                       // SampHead
   static constexpr int64_t kMax = 256;                      // float [G]
-  static constexpr int64_t kNan = kMax + 256;               // int [G]
-  static constexpr int64_t kEsum = kNan + 256;              // uint64 [G]: mass of the tokens top-k keeps
-  static constexpr int64_t kBsum = kEsum + 256;             // uint64 [G]: mass of the tokens both keep
-  static constexpr int64_t kState = kBsum + 256;            // SampState [2]
-  static constexpr int64_t kHist = kState + 256;            // uint64 [2][G][256]
-  static constexpr int64_t kBytes = kHist + 2 * kSampMaxBlocks * 256 * 8;
+  static constexpr int64_t kNan = kMax + 512;               // int [G]
+  static constexpr int64_t kEsum = kNan + 512;              // uint64 [G]: mass of the tokens top-k keeps
+  static constexpr int64_t kBsum = kEsum + 512;             // uint64 [G]: mass of the tokens both keep
+  static constexpr int64_t kState = kBsum + 512;            // SampState [2]
+  static constexpr int64_t kHist = kState + 256;            // uint64 [G][256]: top-k pass 0, per workgroup
+  static constexpr int64_t kGh = kHist + kSampMaxBlocks * 256 * 8;  // uint64 [7][256]: the later passes' sums
+  static constexpr int64_t kBytes = kGh + 7 * 256 * 8;
 };
-static_assert(kSampMaxBlocks * 8 <= 256, "per-block arrays fit their slots");
+static_assert(kSampMaxBlocks * 8 <= 512 && kSampMaxBlocks <= 64, "per-block arrays fit their slots and one wave");
 
 struct SampHead {
   uint32_t kth;   // key of the k-th largest z (0: no top-k)
@@ -114,6 +118,16 @@ __device__ __forceinline__ void hist_store(const uint64_t* H, uint64_t* out) {
 #pragma unroll
     for (int c = 0; c < kSampCopies; ++c) s += H[b * kSampCopies + c];
     out[b] = s;
+  }
+}
+// add the workgroup's histogram into the row's (zeroed by the first launch)
+__device__ __forceinline__ void hist_accumulate(const uint64_t* H, uint64_t* gh) {
+  for (int b = threadIdx.x; b < 256; b += blockDim.x) {
+    uint64_t s = 0;
+#pragma unroll
+    for (int c = 0; c < kSampCopies; ++c) s += H[b * kSampCopies + c];
+    if (s) __hip_atomic_fetch_add((unsigned long long*)&gh[b], (unsigned long long)s, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -225,6 +239,8 @@ __global__ __launch_bounds__(kSampThreads) void samp_first_kernel(SampArgs a) {
   uint8_t* w = samp_row_ws(a);
   const bool topk = a.k > 0;
   if (topk) hist_clear(H);
+  if (blockIdx.x == 0)  // the row histograms of the later passes
+    for (int b = threadIdx.x; b < 7 * 256; b += blockDim.x) ((uint64_t*)(w + SampRow::kGh))[b] = 0;
   __syncthreads();
   const int i0 = blockIdx.x * a.per, i1 = min(i0 + a.per, a.V);
   float mx = -INFINITY;
@@ -259,15 +275,16 @@ __global__ __launch_bounds__(kSampThreads) void samp_first_kernel(SampArgs a) {
 
 // Radix pass `pass` (1..3) of the top-k selection (MASS false: token counts)
 // or of the top-p boundary (MASS true: fixed-point mass of the tokens top-k
-// keeps).  Reads the previous pass's histograms and state (buffer
-// (pass - 1) & 1), writes its own (buffer pass & 1).
+// keeps).  Row histograms: top-k pass p in gh[p - 1] (its pass 0: the
+// per-workgroup histograms), top-p pass p in gh[3 + p]; the descent state
+// alternates between st[0] and st[1].
 template <bool MASS>
 __global__ __launch_bounds__(kSampThreads) void samp_select_kernel(SampArgs a, int pass) {
   __shared__ uint64_t H[256 * kSampCopies];
   __shared__ SampState bcast;
   const float* row = a.x + (int64_t)blockIdx.y * a.ld;
   uint8_t* w = samp_row_ws(a);
-  uint64_t* hist = (uint64_t*)(w + SampRow::kHist);
+  uint64_t* gh = (uint64_t*)(w + SampRow::kGh);
   SampState* st = (SampState*)(w + SampRow::kState);
   uint32_t kth = 0;
   float m = 0.0f;
@@ -278,8 +295,10 @@ __global__ __launch_bounds__(kSampThreads) void samp_select_kernel(SampArgs a, i
     m = h->m;
     thr = samp_thr(a.top_p, samp_sum_g((const uint64_t*)(w + SampRow::kEsum), a.G));
   }
-  const SampState cur =
-      samp_descend<MASS>(hist + ((pass - 1) & 1) * a.G * 256, a.G, st[(pass - 1) & 1], thr, H, &bcast);
+  const uint64_t* src = MASS ? gh + (3 + pass - 1) * 256
+                             : (pass == 1 ? (const uint64_t*)(w + SampRow::kHist) : gh + (pass - 2) * 256);
+  const int srcG = !MASS && pass == 1 ? a.G : 1;
+  const SampState cur = samp_descend<MASS>(src, srcG, st[(pass - 1) & 1], thr, H, &bcast);
   hist_clear(H);
   __syncthreads();
   const int i0 = blockIdx.x * a.per, i1 = min(i0 + a.per, a.V);
@@ -297,7 +316,7 @@ __global__ __launch_bounds__(kSampThreads) void samp_select_kernel(SampArgs a, i
     }
   }
   __syncthreads();
-  hist_store(H, hist + (pass & 1) * a.G * 256 + blockIdx.x * 256);
+  hist_accumulate(H, gh + (MASS ? 3 + pass : pass - 1) * 256);
   if (blockIdx.x == 0 && threadIdx.x == 0) st[pass & 1] = cur;
 }
 
@@ -312,7 +331,7 @@ __global__ __launch_bounds__(kSampThreads) void samp_soft_kernel(SampArgs a) {
   uint8_t* w = samp_row_ws(a);
   uint32_t kth = 0;
   if (a.k > 0)
-    kth = samp_descend<false>((const uint64_t*)(w + SampRow::kHist) + a.G * 256, a.G,
+    kth = samp_descend<false>((const uint64_t*)(w + SampRow::kGh) + 2 * 256, 1,
                               ((const SampState*)(w + SampRow::kState))[1], 0, H, &bcast)
               .prefix;
   const float* maxp = (const float*)(w + SampRow::kMax);
@@ -345,7 +364,7 @@ __global__ __launch_bounds__(kSampThreads) void samp_soft_kernel(SampArgs a) {
       if (topp) ((SampState*)(w + SampRow::kState))[0] = SampState{0u, 0u, 0u};
     }
   }
-  if (topp) hist_store(H, (uint64_t*)(w + SampRow::kHist) + blockIdx.x * 256);
+  if (topp) hist_accumulate(H, (uint64_t*)(w + SampRow::kGh) + 3 * 256);
 }
 
 // With top-p: the mass of the tokens both cuts keep, per workgroup (the top-p
@@ -358,7 +377,7 @@ __global__ __launch_bounds__(kSampThreads) void samp_bsum_kernel(SampArgs a) {
   uint8_t* w = samp_row_ws(a);
   SampHead* h = (SampHead*)(w + SampRow::kHead);
   const uint64_t S = samp_sum_g((const uint64_t*)(w + SampRow::kEsum), a.G);
-  const uint32_t tkey = samp_descend<true>((const uint64_t*)(w + SampRow::kHist) + a.G * 256, a.G,
+  const uint32_t tkey = samp_descend<true>((const uint64_t*)(w + SampRow::kGh) + 6 * 256, 1,
                                            ((const SampState*)(w + SampRow::kState))[1], samp_thr(a.top_p, S), H,
                                            &bcast)
                             .prefix;
@@ -461,7 +480,7 @@ int launch_sample_rows(const float* x, int64_t M, int64_t V, int64_t ld, float T
   a.x = x;
   a.ld = ld;
   a.V = (int)V;
-  a.G = (int)((V + 4095) / 4096);
+  a.G = (int)((V + 2047) / 2048);
   if (a.G > kSampMaxBlocks) a.G = kSampMaxBlocks;
   a.per = (int)((V + a.G - 1) / a.G);
   a.T = T;

@@ -65,7 +65,7 @@ def test_sample_vocab_rows_match_oracle(dev, T, k, p):
 
 @pytest.mark.parametrize("V", [1, 2, 37, 1000, 4097, 70000])
 def test_sample_small_and_ragged_vocab(dev, V):
-    """Vocabularies from one token up, ragged against the 4096-token
+    """Vocabularies from one token up, ragged against the 2048-token
     workgroup slices; three rows sampled in one call."""
     announce(f"sample small V={V}")
     g = torch.Generator().manual_seed(V)
