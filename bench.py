@@ -186,6 +186,26 @@ def decode_bench(ctx, M, steps, warmup, shapes=DECODE_SHAPES, xdtype=None):
     return out
 
 
+def gemv_grouped4_bench(ctx, N=4096, K=4096, steps=40, warmup=5, xdtype=None):
+    """Four independent N x K projections at M=1 (distinct weights, inputs
+    and outputs) as one grouped launch (sbq_linear_w8_grouped: the launch gap
+    and ramp paid once for the four), weights rotating beyond the Infinity
+    Cache: per-projection time and the group's GB/s."""
+    torch, quant = ctx.torch, ctx.quant
+    shapes = [(N, K)] * 4
+    layers, xs, ys, step_bytes, copies = decode_setup(ctx, 1, shapes, xdtype, seed=900)
+
+    def step(c):
+        L = layers[c]
+        quant.linear_w8_grouped(xs, [l[0] for l in L], [l[1] for l in L], [None] * 4, [N] * 4,
+                                out_dtype=torch.float16, outs=ys)
+
+    ms = ctx.time_steps(step, copies, steps, warmup)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    del layers
+    return {"us_per_launch": ms * 1e3, "us_per_projection": ms * 1e3 / 4, "GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
+
+
 def dominant_kernel(ctx, M=1, launches_per_copy=8, reps=5):
     """Average duration of the gate+up GEMV launch: a graph of back-to-back
     launches (rotating weight copies), HIP events around the replays."""
@@ -943,6 +963,7 @@ def main():
         fn = {"lm_head_greedy": lm_head_greedy_bench, "device_state": device_state_bench,
               "device_state_hybrid": device_state_hybrid_both,
               "sample": sample_bench,
+              "gemv_4096_grouped4": gemv_grouped4_bench,
               "stack_fused": lambda ctx: stack_bench(ctx, Ms=sm, fused=True),
               "w8a8": lambda ctx: [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)],
               "prefill": lambda ctx: [prefill_bench(ctx, M) for M in (512, 2048, 8192)],
@@ -984,6 +1005,7 @@ def main():
         extra["gemv_4096_f16x"] = decode_bench(ctx, 1, args.steps, args.warmup, shapes=[(4096, 4096)])
         extra["gemv_4096_f32x"] = decode_bench(ctx, 1, args.steps, args.warmup, shapes=[(4096, 4096)],
                                                xdtype=torch.float32)
+        extra["gemv_4096_grouped4"] = gemv_grouped4_bench(ctx)
         log("prefill GEMM")
         extra["prefill"] = [prefill_bench(ctx, M) for M in (512, 2048, 8192)]
         # the reference model's own activations are fp32: staged as a scaled fp16 plane
@@ -1054,6 +1076,11 @@ def main():
             "prefill_M2048_mfma_frac": None if pre2048 is None else round(pre2048["mfma_frac"], 4),
             "gemv_4096x4096_M1_f16x": gemv_4096("gemv_4096_f16x"),
             "gemv_4096x4096_M1_f32x": gemv_4096("gemv_4096_f32x"),
+            # four independent 4096x4096 projections in one grouped launch (fp16 x)
+            "gemv_4096x4096_M1_grouped4": None if "gemv_4096_grouped4" not in extra else {
+                "us_per_projection": round(extra["gemv_4096_grouped4"]["us_per_projection"], 3),
+                "GBps": round(extra["gemv_4096_grouped4"]["GBps"], 1),
+                "hbm_frac": round(extra["gemv_4096_grouped4"]["hbm_frac"], 4)},
         },
         "roofline": {
             "bound": "hbm",
