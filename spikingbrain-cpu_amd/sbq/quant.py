@@ -453,14 +453,14 @@ def sample_tokens(logits: torch.Tensor, temperature: float, top_p: float = 1.0, 
         raise ValueError("sample_tokens expects fp32 GPU logits")
     if temperature != temperature or top_p != top_p:
         raise ValueError("temperature and top_p must be numbers")
+    if temperature <= 0:
+        return greedy_tokens(logits)
     shape = logits.shape
     y = logits.reshape(-1, shape[-1])
     if y.stride(-1) != 1:
         y = y.contiguous()
     M, V = y.shape
     out = torch.empty((M,), dtype=torch.int64, device=y.device)
-    if temperature <= 0:
-        return greedy_tokens(logits)
     if u is None:
         if generator is not None and generator.device.type == "cuda":
             u = torch.rand((M,), generator=generator, device=y.device)
