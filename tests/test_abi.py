@@ -214,3 +214,43 @@ def test_gemm_config_reports_the_route(lib):
     for M, N, K, dt, w8a8 in GEMM:
         lib.sbq_gemm_config(M, N, K, dt, w8a8, ctypes.byref(splits))
         assert splits.value >= 1, (M, N, K, dt, w8a8)
+
+
+def test_sample_rows_validation_without_gpu(lib):
+    """sbq_sample_rows (engine.py:29-42) rejects bad arguments before any
+    launch; its workspace size grows with the rows only."""
+    P = ctypes.c_void_p
+    dummy = P(4096)
+    per_row = lib.sbq_sample_workspace_bytes(1, 151936) - lib.sbq_sample_workspace_bytes(0, 151936)
+    assert per_row > 0
+    assert lib.sbq_sample_workspace_bytes(3, 151936) == lib.sbq_sample_workspace_bytes(0, 151936) + 3 * per_row
+    assert lib.sbq_sample_workspace_bytes(3, 10) == lib.sbq_sample_workspace_bytes(3, 151936)
+    assert lib.sbq_sample_workspace_bytes(-1, 10) == 0 and lib.sbq_sample_workspace_bytes(1, 0) == 0
+    ws_ok = lib.sbq_sample_workspace_bytes(1, 1000)
+    nan = float("nan")
+    # M < 0, V < 1, ld < V, too many rows
+    assert lib.sbq_sample_rows(dummy, -1, 1000, 1000, 0.7, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
+    assert lib.sbq_sample_rows(dummy, 1, 0, 1000, 0.7, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
+    assert lib.sbq_sample_rows(dummy, 1, 1000, 999, 0.7, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
+    assert lib.sbq_sample_rows(dummy, 70000, 1000, 1000, 0.7, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
+    # NaN temperature or top_p
+    assert lib.sbq_sample_rows(dummy, 1, 1000, 1000, nan, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
+    assert lib.sbq_sample_rows(dummy, 1, 1000, 1000, 0.7, 0, nan, dummy, dummy, dummy, ws_ok, None) == -1
+    # no rows: nothing to do
+    assert lib.sbq_sample_rows(None, 0, 1000, 1000, 0.7, 0, 0.9, None, None, None, 0, None) == 0
+    # null logits or tokens; a draw without uniforms; a short workspace
+    assert lib.sbq_sample_rows(None, 1, 1000, 1000, 0.7, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
+    assert lib.sbq_sample_rows(dummy, 1, 1000, 1000, 0.7, 0, 0.9, dummy, None, dummy, ws_ok, None) == -1
+    assert lib.sbq_sample_rows(dummy, 1, 1000, 1000, 0.7, 0, 0.9, None, dummy, dummy, ws_ok, None) == -1
+    assert lib.sbq_sample_rows(dummy, 1, 1000, 1000, 0.7, 0, 0.9, dummy, dummy, dummy, ws_ok - 1, None) == -4
+    assert lib.sbq_sample_rows(dummy, 1, 1000, 1000, 0.7, 0, 0.9, dummy, dummy, None, ws_ok, None) == -4
+
+
+def test_sample_tokens_rejects_host_logits():
+    import torch
+    from sbq import quant
+
+    with pytest.raises(ValueError):
+        quant.sample_tokens(torch.zeros(1, 10), 0.7, 0.9)
+    with pytest.raises(ValueError):
+        quant.sample_tokens(torch.zeros(1, 10, dtype=torch.float16), 0.7, 0.9)
