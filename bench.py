@@ -490,6 +490,43 @@ def w8a8_bench(ctx, M, N, K=4096, steps=20, warmup=5, token=False):
     return res
 
 
+def vendor_gemm_bench(ctx, K=4096, steps=20, warmup=5):
+    """The vendor library's own GEMMs at the prefill and mid-sized shapes, as
+    reference points for the kernels above (not part of this library):
+    torch.matmul on fp16 weights [K, N] (hipBLASLt; an fp16 model with no
+    int8 weights at all, twice the weight bytes), and torch._int_mm on s8
+    operands (hipBLASLt's int8 GEMM: the int32 product alone, without the
+    activation quantization, the zero-point correction or the scaled fp16
+    output of an int8-dyn call).  Five steps per graph replay on one weight
+    copy, as prefill_bench and w8a8_bench time theirs."""
+    torch = ctx.torch
+    gen = torch.Generator(device=ctx.dev).manual_seed(970)
+    out = {"fp16_matmul": [], "int8_int_mm": []}
+    for M, N in ((128, 4096), (128, 12288), (512, 12288), (2048, 12288), (8192, 12288)):
+        w = (torch.randn(K, N, generator=gen, device=ctx.dev) * 0.02).half()
+        x = torch.randn(M, K, generator=gen, device=ctx.dev).half()
+        y = torch.empty(M, N, dtype=torch.float16, device=ctx.dev)
+        ms = ctx.time_steps(lambda c: torch.matmul(x, w, out=y), 5, steps, warmup)
+        tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        out["fp16_matmul"].append({"M": M, "N": N, "K": K, "us": ms * 1e3, "TFLOPs": tf,
+                                   "mfma_frac": tf / F16_PEAK_TFLOPS})
+        del w, x, y
+    for M, N in ((128, 4096), (128, 12288), (512, 12288), (2048, 4096), (2048, 12288)):
+        a = torch.randint(-127, 128, (M, K), generator=gen, device=ctx.dev, dtype=torch.int8)
+        b = torch.randint(-127, 128, (K, N), generator=gen, device=ctx.dev, dtype=torch.int8)
+        try:  # eager first: a shape the library refuses is reported, not captured
+            torch._int_mm(a, b)
+            torch.cuda.synchronize()
+        except RuntimeError as e:
+            out["int8_int_mm"].append({"M": M, "N": N, "K": K, "error": str(e).splitlines()[0][:160]})
+            continue
+        ms = ctx.time_steps(lambda c: torch._int_mm(a, b), 5, steps, warmup)
+        tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        out["int8_int_mm"].append({"M": M, "N": N, "K": K, "us": ms * 1e3, "TOPs": tops, "i8_frac": tops / I8_PEAK_TOPS})
+        del a, b
+    return out
+
+
 # ---------------------------------------------------------------------------
 # one decode step through every quantized linear of the 36-layer hybrid model
 # ---------------------------------------------------------------------------
@@ -963,6 +1000,7 @@ def main():
         fn = {"lm_head_greedy": lm_head_greedy_bench, "device_state": device_state_bench,
               "device_state_hybrid": device_state_hybrid_both,
               "sample": sample_bench,
+              "vendor_gemm": vendor_gemm_bench,
               "gemv_4096_grouped4": gemv_grouped4_bench,
               "stack_fused": lambda ctx: stack_bench(ctx, Ms=sm, fused=True),
               "w8a8": lambda ctx: [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)],
@@ -1030,6 +1068,9 @@ def main():
         extra["w8a8"] = [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)]
         log("int8-dyn, per-token symmetric activations (opt-in)")
         extra["w8a8_token"] = [w8a8_bench(ctx, M, N, token=True) for M in (1, 128, 2048) for N in (4096, 12288)]
+        log("vendor GEMMs at the same shapes (reference points)")
+        extra["vendor_gemm"] = vendor_gemm_bench(ctx)
+        torch.cuda.empty_cache()
         log("36-layer linear stack")
         extra["stack"] = stack_bench(ctx)
         log("36-layer linear stack, layers reading the same input fused")
