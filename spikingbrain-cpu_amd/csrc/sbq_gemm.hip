@@ -1347,7 +1347,15 @@ int launch_gemm_w8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, boo
       uint8_t* w = (uint8_t*)ws;
       float* rowsum = (float*)(w + l.rowsum);
       a.rsum = rowsum;
-      if (xt == XT_F16) {
+      if (xt == XT_F16 && !zero && (id == 3 || id == 5 || id == 16)) {
+        // fp16 x, no split: these three configurations sum the rows in their
+        // K loop for less than the row-sum launch costs (measured over
+        // M = 192 ... 1024, N = 2048 ... 24576, K = 2560 ... 12288: 128 x 64
+        // blocks with K over 4 wave groups 6-7% faster, 128 x 64 and 192 x 64
+        // blocks 0-4%; the larger blocks and the 64 x 64 split ran 2-30% slower
+        // that way, and keep the pre-pass)
+        a.rsum = nullptr;
+      } else if (xt == XT_F16) {
         const int rc = launch_rowsum_f16(x, ldx, M, K, rowsum, st, zero, ncount);
         if (rc) return rc;
       } else {
