@@ -206,6 +206,37 @@ def gemv_grouped4_bench(ctx, N=4096, K=4096, steps=40, warmup=5, xdtype=None):
     return {"us_per_launch": ms * 1e3, "us_per_projection": ms * 1e3 / 4, "GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
 
 
+def stream_floor_bench(ctx, steps=40, warmup=5):
+    """What one dependent launch of other kernels takes to read the same bytes
+    as a 4096x4096 (16.8 MB) and a 24576x4096 (100.7 MB) int8 GEMV at M=1,
+    rotating beyond the Infinity Cache as the GEMV benches' weights do:
+    torch's copy_ moving as many HBM bytes (half read, half written; a plain
+    elementwise kernel, safe to capture in a graph), and the vendor library's
+    GEMV on fp16 weights of the same shape (torch.matmul, hipBLASLt: twice
+    the weight bytes).  Reference points for the per-launch floor of the
+    GEMV; not part of this library."""
+    torch = ctx.torch
+    out = {}
+    for N, K in ((4096, 4096), (24576, 4096)):
+        nbytes = N * K
+        copies = math.ceil(ROTATE_BYTES / nbytes) + 1
+        src = [torch.empty(nbytes // 2, dtype=torch.uint8, device=ctx.dev).fill_(c) for c in range(copies)]
+        dst = [torch.empty(nbytes // 2, dtype=torch.uint8, device=ctx.dev) for _ in range(copies)]
+        ms = ctx.time_steps(lambda c: dst[c].copy_(src[c]), copies, steps, warmup)
+        r = {"copy_us": ms * 1e3, "copy_GBps": nbytes / (ms * 1e-3) / 1e9}
+        del src, dst
+        copies16 = math.ceil(ROTATE_BYTES / (2 * nbytes)) + 1
+        ws = [(torch.randn(K, N, device=ctx.dev) * 0.02).half() for _ in range(copies16)]
+        x = torch.randn(1, K, device=ctx.dev).half()
+        y = torch.empty((1, N), dtype=torch.float16, device=ctx.dev)
+        ms = ctx.time_steps(lambda c: torch.matmul(x, ws[c], out=y), copies16, steps, warmup)
+        r["fp16_matmul_us"] = ms * 1e3
+        r["fp16_matmul_GBps"] = 2 * nbytes / (ms * 1e-3) / 1e9
+        del ws
+        out[f"{N}x{K}"] = r
+    return out
+
+
 def dominant_kernel(ctx, M=1, launches_per_copy=8, reps=5):
     """Average duration of the gate+up GEMV launch: a graph of back-to-back
     launches (rotating weight copies), HIP events around the replays."""
@@ -1001,6 +1032,7 @@ def main():
               "device_state_hybrid": device_state_hybrid_both,
               "sample": sample_bench,
               "vendor_gemm": vendor_gemm_bench,
+              "stream_floor": stream_floor_bench,
               "gemv_4096_grouped4": gemv_grouped4_bench,
               "stack_fused": lambda ctx: stack_bench(ctx, Ms=sm, fused=True),
               "w8a8": lambda ctx: [w8a8_bench(ctx, M, N) for M in (1, 128, 512, 2048) for N in (4096, 12288)],
@@ -1044,6 +1076,8 @@ def main():
         extra["gemv_4096_f32x"] = decode_bench(ctx, 1, args.steps, args.warmup, shapes=[(4096, 4096)],
                                                xdtype=torch.float32)
         extra["gemv_4096_grouped4"] = gemv_grouped4_bench(ctx)
+        log("other kernels reading the GEMV's bytes (reference points)")
+        extra["stream_floor"] = stream_floor_bench(ctx)
         log("prefill GEMM")
         extra["prefill"] = [prefill_bench(ctx, M) for M in (512, 2048, 8192)]
         # the reference model's own activations are fp32: staged as a scaled fp16 plane
