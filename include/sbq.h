@@ -317,8 +317,8 @@ int sbq_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* 
 
 /* ---- non-greedy sampling (engine.py:29-42, sample) ---- */
 
-/* Workspace bytes of sbq_sample_rows for M rows (about 130 KB per row; any
- * vocabulary size up to 2^31 - 1).  0 for a bad argument. */
+/* Workspace bytes of sbq_sample_rows for M rows (about 130 KB per row, for
+ * any vocabulary size up to 2^23).  0 for a bad argument. */
 int64_t sbq_sample_workspace_bytes(int64_t M, int64_t V);
 
 /* tokens[m] = the engine's sample() of row m of fp32 logits [M, V] (row
@@ -336,7 +336,8 @@ int64_t sbq_sample_workspace_bytes(int64_t M, int64_t V);
  * Masses are exact sums of the fp32 probabilities truncated to 2^-40, so the
  * result does not depend on timing.  A row with a NaN, or an infinite
  * maximum after the division (where the reference raises), gets token -1.
- * tokens: device int64 [M].  M <= 65535.  Rows are independent. */
+ * tokens: device int64 [M].  M <= 65535, V <= 2^23 (a row's mass, at most
+ * V * 2^40, fits 64 bits).  Rows are independent. */
 int sbq_sample_rows(const float* logits, int64_t M, int64_t V, int64_t ld, float temperature, int64_t top_k,
                     float top_p, const float* u, int64_t* tokens, void* workspace, size_t workspace_bytes,
                     void* stream);

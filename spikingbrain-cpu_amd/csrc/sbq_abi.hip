@@ -457,14 +457,14 @@ int sbq_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* 
 }
 
 int64_t sbq_sample_workspace_bytes(int64_t M, int64_t V) {
-  if (M < 0 || V < 1 || M > kIntMax || V > kIntMax) return 0;
+  if (M < 0 || V < 1 || M > 65535 || V > sbq::kSampMaxVocab) return 0;
   return sbq::sample_workspace_bytes(M) + 256;  // + alignment slack
 }
 
 int sbq_sample_rows(const float* logits, int64_t M, int64_t V, int64_t ld, float temperature, int64_t top_k,
                     float top_p, const float* u, int64_t* tokens, void* workspace, size_t workspace_bytes,
                     void* stream) {
-  if (M < 0 || V < 1 || ld < V || V > kIntMax || M > 65535) return SBQ_ERR_ARG;
+  if (M < 0 || V < 1 || ld < V || V > sbq::kSampMaxVocab || M > 65535) return SBQ_ERR_ARG;
   if (temperature != temperature || top_p != top_p) return SBQ_ERR_ARG;
   if (M == 0) return SBQ_OK;
   if (!logits || !tokens) return SBQ_ERR_ARG;

@@ -26,7 +26,10 @@ int launch_minmax_partials(const void* x, int xt, int64_t M, int64_t K, int64_t 
 int launch_qparams(const float2* partials, int nparts, float* scale_out, int32_t* zp_out, hipStream_t st);
 int launch_argmax_rows(const float* y, int64_t M, int64_t N, int64_t ldy, int64_t* out, hipStream_t st);
 // The engine's non-greedy sampling step (sbq_sample.hip) over rows of fp32
-// logits; ws: sample_workspace_bytes(M), 256-byte aligned.
+// logits; ws: sample_workspace_bytes(M), 256-byte aligned.  Vocabularies up
+// to kSampMaxVocab: a row's fixed-point mass (each token at most 2^40) then
+// stays below 2^63.
+constexpr int64_t kSampMaxVocab = (int64_t)1 << 23;
 int64_t sample_workspace_bytes(int64_t M);
 int launch_sample_rows(const float* x, int64_t M, int64_t V, int64_t ld, float T, int64_t top_k, float top_p,
                        const float* u, int64_t* tokens, void* ws, hipStream_t st);

@@ -226,6 +226,9 @@ def test_sample_rows_validation_without_gpu(lib):
     assert lib.sbq_sample_workspace_bytes(3, 151936) == lib.sbq_sample_workspace_bytes(0, 151936) + 3 * per_row
     assert lib.sbq_sample_workspace_bytes(3, 10) == lib.sbq_sample_workspace_bytes(3, 151936)
     assert lib.sbq_sample_workspace_bytes(-1, 10) == 0 and lib.sbq_sample_workspace_bytes(1, 0) == 0
+    # at most 65535 rows and 2^23 tokens (a row's 2^-40 fixed-point mass fits 64 bits)
+    assert lib.sbq_sample_workspace_bytes(1, 1 << 23) > 0 and lib.sbq_sample_workspace_bytes(1, (1 << 23) + 1) == 0
+    assert lib.sbq_sample_workspace_bytes(65536, 10) == 0
     ws_ok = lib.sbq_sample_workspace_bytes(1, 1000)
     nan = float("nan")
     # M < 0, V < 1, ld < V, too many rows
@@ -233,6 +236,8 @@ def test_sample_rows_validation_without_gpu(lib):
     assert lib.sbq_sample_rows(dummy, 1, 0, 1000, 0.7, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
     assert lib.sbq_sample_rows(dummy, 1, 1000, 999, 0.7, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
     assert lib.sbq_sample_rows(dummy, 70000, 1000, 1000, 0.7, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
+    big = (1 << 23) + 1
+    assert lib.sbq_sample_rows(dummy, 1, big, big, 0.7, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
     # NaN temperature or top_p
     assert lib.sbq_sample_rows(dummy, 1, 1000, 1000, nan, 0, 0.9, dummy, dummy, dummy, ws_ok, None) == -1
     assert lib.sbq_sample_rows(dummy, 1, 1000, 1000, 0.7, 0, nan, dummy, dummy, dummy, ws_ok, None) == -1
