@@ -848,7 +848,8 @@ namespace {
   X(4, 4, 2, false)         \
   X(5, 8, 2, false)         \
   X(6, 4, 2, true)          \
-  X(7, 2, 5, true)
+  X(7, 2, 5, true)          \
+  X(8, 2, 6, false)
 
 struct FastCfg {
   int id, D, G;
@@ -1025,7 +1026,8 @@ int launch_gemv_mt(const GemvArgs& a, int xt, hipStream_t st, bool gemm_alt) {
 // 151936): 4-tile steps over two row tiles per wave for wide K = 4096 layers,
 // 8-tile steps over one row tile for long K or narrow N, two waves per row tile
 // once M > 8 (the activation fragments then dominate the registers), five row
-// tiles per workgroup with x in LDS at M = 4 .. 8 on wide short-K layers.  bf16
+// tiles per workgroup with x in LDS at M = 4 .. 8 on wide short-K layers, six
+// with x loaded directly where five do not fit one round at M > 8.  bf16
 // activations follow the fp16 rules; fp32 activations are copied to LDS and
 // split once into bf16 high / remainder planes when x fits (M <= 8), and
 // otherwise take direct steps with two row tiles per wave on wide layers (M =
@@ -1110,6 +1112,13 @@ bool pick_gemv_fast(int64_t M, int64_t K, int64_t N, int xt, bool w8a8, bool xve
     // five row tiles per workgroup with x in LDS, as at M = 4 .. 8
     if (!w8a8 && Kc < 128 && Nt > 1024 && (Nt + 4) / 5 <= 256 && M * K * 2 <= kFastXLdsWideBytes) {
       *id = 7;  // D=2, G=5, x in LDS
+      *ks = 8;
+    } else if (!w8a8 && Kc < 128 && Nt > 1024 && (Nt + 5) / 6 <= 256) {
+      // six row tiles per workgroup, x fragments loaded directly: each wave
+      // reads its K range of x once per six row tiles instead of two, and the
+      // grid still fits one round of the CUs (M = 16, N = 24576, K = 4096:
+      // 19.8 -> 18.2 us; M = 16 x is 128 KiB there, beyond the LDS copy)
+      *id = 8;  // D=2, G=6
       *ks = 8;
     }
   }

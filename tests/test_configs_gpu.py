@@ -96,6 +96,8 @@ W8_FULL = [
     # (M, N, K, x dtype, y dtype)
     (1, 24576, 4096, "f16", "f16"),    # gate+up, the dominant decode launch
     (1, 24576, 4096, "f32", "f32"),
+    (16, 24576, 4096, "f16", "f16"),   # six row tiles per workgroup (M > 8, wide, short K)
+    (9, 21999, 2560, "bf16", "f32"),   # the same, ragged N and a last workgroup of one row tile
     (1, 4096, 4096, "f16", "f32"),     # single 4096x4096 GEMV
     (1, 4096, 4096, "f32", "f32"),
     (1, 151936, 4096, "f32", "f32"),   # lm_head, 36-layer benchmark model
