@@ -26,6 +26,8 @@
  *   sbq_act_qparams           <- spikingbrain_cpu/quant.py:65 (the per-tensor activation
  *                                quantization parameters chosen inside
  *                                torch.ops.quantized.linear_dynamic)
+ *   sbq_act_quant_per_tensor  <- spikingbrain_cpu/quant.py:65 (those parameters and the
+ *                                uint8 activations linear_dynamic multiplies)
  *   sbq_linear_w8a8           <- spikingbrain_cpu/quant.py:63-66 DynamicInt8Linear.forward
  *   sbq_argmax_rows           <- spikingbrain_cpu/engine.py:30-31 (greedy sampling,
  *                                int(logits.argmax()) over the lm_head output of
@@ -202,6 +204,19 @@ int64_t sbq_w8a8_workspace_bytes(int64_t M, int64_t K);
 int sbq_act_qparams(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                     float* scale_out, int32_t* zp_out,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* The activation quantization itself, the step inside
+ * quantized::linear_dynamic (spikingbrain_cpu/quant.py:65) that the int8-dyn
+ * entry points below fuse into their kernels: the (scale, zero_point) of
+ * sbq_act_qparams, then
+ *   xq[m,k] = clamp(rint(fma(x[m,k], 1/scale, zero_point)), 0, 255)
+ * (one rounding, half to even) into device uint8 xq [M, K] with row stride
+ * ldq >= K; sbq_linear_w8a8's acc equals sum_k (xq[m,k] - zp) * q[n,k].
+ * Results: *scale_out (device fp32[1]), *zp_out (device int32[1]).
+ * workspace: >= sbq_w8a8_workspace_bytes(M, K) bytes. */
+int sbq_act_quant_per_tensor(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                             uint8_t* xq, int64_t ldq, float* scale_out, int32_t* zp_out,
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* y[m,n] = fp32(acc[m,n]) * fp32(s_x * scale[n]) (+ bias[n]) where
  *   xq[m,k]  = clamp(rint(fma(x[m,k], 1/s_x, zp)), 0, 255)   (one rounding)

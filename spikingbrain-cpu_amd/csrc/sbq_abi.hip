@@ -319,6 +319,24 @@ int sbq_act_qparams(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ld
   return sbq::launch_qparams(parts, np, scale_out, zp_out, st);
 }
 
+int sbq_act_quant_per_tensor(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, uint8_t* xq, int64_t ldq,
+                             float* scale_out, int32_t* zp_out, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  if (!valid_dtype(x_dtype)) return SBQ_ERR_DTYPE;
+  if (M < 1 || K < 1 || ldx < K || ldq < K || M > kIntMax || K > kIntMax) return SBQ_ERR_ARG;
+  if (M * ((K + 7) / 8) > (int64_t)0x7fffffff * 256) return SBQ_ERR_ARG;  // one thread per 8 values
+  if (!x || !xq || !scale_out || !zp_out) return SBQ_ERR_ARG;
+  if (!workspace || (int64_t)workspace_bytes < sbq_w8a8_workspace_bytes(M, K)) return SBQ_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  float2* parts = ws_partials(workspace);
+  const int np = sbq::minmax_nparts(M, K);
+  int rc = sbq::launch_minmax_partials(x, x_dtype, M, K, ldx, parts, np, st);
+  if (rc) return rc;
+  rc = sbq::launch_qparams(parts, np, scale_out, zp_out, st);
+  if (rc) return rc;
+  return sbq::launch_act_quant_u8(x, x_dtype, M, K, ldx, x_vec_ok(x, x_dtype, ldx), parts, np, xq, ldq, st);
+}
+
 int sbq_linear_w8a8_token(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* packed,
                           const float* scale, const float* bias, int64_t N, void* y, int y_dtype, int64_t ldy,
                           int32_t* acc_out, void* workspace, size_t workspace_bytes, void* stream) {

@@ -108,6 +108,10 @@ W8Ws w8_ws_layout(int64_t M, int64_t K, int xt);
 int launch_gemm_w8a8_token(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec,
                            const uint8_t* packed, const float* scale, const float* bias, int64_t N, void* y, int yt,
                            int64_t ldy, int32_t* acc_out, int8_t* xq, float* s_t, hipStream_t st, bool yvec);
+// uint8 xq [M][ldq] of fbgemm's per-tensor activation quantization from the
+// min/max partials (sbq_act_quant_per_tensor).
+int launch_act_quant_u8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const float2* partials,
+                        int nparts, uint8_t* xq, int64_t ldq, hipStream_t st);
 int launch_quantize_rows_sym(const void* x, int xt, int64_t ldx, bool xvec, int64_t M, int64_t K, int64_t Kp,
                              int8_t* xq, float* s_out, hipStream_t st);
 // Per-row sums in fp32 of fp16 x [M, K] (K % 8 == 0, 16-byte aligned rows).

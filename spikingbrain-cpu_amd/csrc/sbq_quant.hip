@@ -272,6 +272,45 @@ __global__ __launch_bounds__(256) void rowsum_f16_kernel(const _Float16* __restr
   if (lane == 0) out[row] = s;
 }
 
+// fbgemm's per-tensor activation quantization on its own (the step inside
+// quantized::linear_dynamic, quant.py:65, that the int8-dyn GEMMs fuse into
+// their pre-pass): the (s_x, zp) of the min/max partials, then
+// xq[m,k] = clamp(rint(fma(x[m,k], 1/s_x, zp)), 0, 255) as uint8 [M][ldq],
+// the arithmetic of the GEMM path's quantize pass (without its s8 shift).
+// One thread per 8 consecutive values of a row; loads clamped to the row,
+// stores guarded.
+template <int XT>
+__global__ __launch_bounds__(256) void act_quant_u8_kernel(const void* __restrict__ x, int64_t ldx, int M, int K,
+                                                           bool vec, const float2* __restrict__ partials,
+                                                           int nparts, uint8_t* __restrict__ xq, int64_t ldq,
+                                                           bool qvec) {
+  const int cpr = (K + 7) / 8;
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t cl = min(c, (int64_t)M * cpr - 1);
+  const int m = (int)(cl / cpr), k0 = (int)(cl - (int64_t)m * cpr) * 8;
+  float t[8];
+  load8_f32<XT>(x, ldx, M, K, m, k0, vec, t);
+  __shared__ float red[8];
+  const ActQParams qp = block_qparams_from_partials(partials, nparts, red);
+  if (c >= (int64_t)M * cpr) return;
+  uint32_t d[2];
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    uint32_t v = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(t[4 * w], qp.inv, qp.zpf), 0, 0u);
+    v = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(t[4 * w + 1], qp.inv, qp.zpf), 1, v);
+    v = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(t[4 * w + 2], qp.inv, qp.zpf), 2, v);
+    d[w] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(t[4 * w + 3], qp.inv, qp.zpf), 3, v);
+  }
+  uint8_t* dst = xq + (int64_t)m * ldq + k0;
+  if (qvec && k0 + 8 <= K) {
+    *(u32x2*)dst = (u32x2){d[0], d[1]};
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (k0 + j < K) dst[j] = (uint8_t)(d[j >> 2] >> (8 * (j & 3)));
+  }
+}
+
 // Per-token symmetric activation quantization (the opt-in int8-dyn
 // granularity): each activation row is quantized exactly as
 // quantize_per_channel (spikingbrain_cpu/quant.py:25-29) quantizes a weight
@@ -544,6 +583,20 @@ int launch_stage_act(const void* x, int xt, int64_t ldx, int64_t M, int64_t K, _
                        zero, nzero);
   else
     return -2;
+  return check_launch();
+}
+
+int launch_act_quant_u8(const void* x, int xt, int64_t M, int64_t K, int64_t ldx, bool xvec, const float2* partials,
+                        int nparts, uint8_t* xq, int64_t ldq, hipStream_t st) {
+  const int64_t chunks = M * ((K + 7) / 8);
+  const dim3 grid((unsigned)((chunks + 255) / 256)), block(256);
+  const bool qvec = (uintptr_t)xq % 8 == 0 && ldq % 8 == 0;
+  switch (xt) {
+    case XT_F32: hipLaunchKernelGGL(act_quant_u8_kernel<XT_F32>, grid, block, 0, st, x, ldx, (int)M, (int)K, xvec, partials, nparts, xq, ldq, qvec); break;
+    case XT_F16: hipLaunchKernelGGL(act_quant_u8_kernel<XT_F16>, grid, block, 0, st, x, ldx, (int)M, (int)K, xvec, partials, nparts, xq, ldq, qvec); break;
+    case XT_BF16: hipLaunchKernelGGL(act_quant_u8_kernel<XT_BF16>, grid, block, 0, st, x, ldx, (int)M, (int)K, xvec, partials, nparts, xq, ldq, qvec); break;
+    default: return -2;
+  }
   return check_launch();
 }
 

@@ -7,8 +7,9 @@ formats run on hand-written gfx950 kernels through libsbq.so:
 ``int8``      symmetric per-output-channel int8 weights with fp32 scales,
               weight-only (quant.py:32-53).  Decode shapes stream the packed
               weights from HBM through MFMA; prefill shapes use an LDS-tiled
-              MFMA GEMM.  fp16/bf16 activations are used exactly, fp32
-              activations as bf16 hi + lo.
+              MFMA GEMM.  fp16/bf16 activations are used exactly; fp32
+              activations as bf16 high + remainder planes at decode sizes
+              and as one power-of-two scaled fp16 plane in the GEMM.
 ``int8-dyn``  int8 weights with activations quantized per tensor at run time
               (quant.py:56-66): the fbgemm dynamic-linear arithmetic,
               reproduced bit for bit (uint8 activations, exact int32
@@ -571,7 +572,10 @@ def _greedy_state(module: nn.Module, device: torch.device) -> torch.Tensor:
 
 
 def act_qparams(x2: torch.Tensor) -> tuple[float, int]:
-    """The per-tensor (scale, zero_point) the int8-dyn path uses for x2 [M, K]."""
+    """The per-tensor (scale, zero_point) the int8-dyn path uses for x2 [M, K]
+    (a GPU tensor)."""
+    if not x2.is_cuda or x2.dim() != 2:
+        raise ValueError("act_qparams: x must be a 2-D GPU tensor")
     x2 = _as_activation(x2)
     M, K = x2.shape
     s = torch.empty((1,), dtype=torch.float32, device=x2.device)
@@ -582,6 +586,32 @@ def act_qparams(x2: torch.Tensor) -> tuple[float, int]:
                                                _ptr(ws), _nbytes(ws), _stream(x2.device)),
                    "sbq_act_qparams")
     return float(s.item()), int(z.item())
+
+
+def act_quant_per_tensor(x2: torch.Tensor, out: torch.Tensor | None = None
+                         ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The activation quantization inside linear_dynamic (quant.py:65) on its
+    own: (xq uint8 [M, K], scale fp32 [1], zero_point int32 [1]) on x2's GPU,
+    xq = clamp(rint(fma(x, 1/scale, zero_point)), 0, 255).  `out`: a uint8
+    [M, >= K] GPU tensor with unit column stride to write xq into."""
+    if not x2.is_cuda or x2.dim() != 2:
+        raise ValueError("act_quant_per_tensor: x must be a 2-D GPU tensor")
+    x2 = _as_activation(x2)
+    M, K = x2.shape
+    if out is None:
+        out = torch.empty((M, K), dtype=torch.uint8, device=x2.device)
+    if (out.dtype != torch.uint8 or out.dim() != 2 or out.shape[0] != M or out.shape[1] < K or out.stride(1) != 1
+            or out.device != x2.device):
+        raise ValueError("out must be a uint8 [M, >= K] tensor on x's device with unit column stride")
+    s = torch.empty((1,), dtype=torch.float32, device=x2.device)
+    z = torch.empty((1,), dtype=torch.int32, device=x2.device)
+    ws = w8a8_workspace(M, K, x2.device)
+    with torch.cuda.device(x2.device):
+        _lib.check(_lib.load().sbq_act_quant_per_tensor(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(out),
+                                                        out.stride(0), _ptr(s), _ptr(z), _ptr(ws), _nbytes(ws),
+                                                        _stream(x2.device)),
+                   "sbq_act_quant_per_tensor")
+    return out[:, :K], s, z
 
 
 # ---------------------------------------------------------------------------

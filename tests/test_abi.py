@@ -84,6 +84,12 @@ def test_argument_validation_without_gpu(lib):
     assert lib.sbq_quantize_per_channel(dummy, 5, 4, 4, 4, dummy, 4, dummy, None) == -2
     assert lib.sbq_repack_w8(dummy, 4, 64, 32, dummy, None, None) == -1
     assert lib.sbq_act_qparams(dummy, 0, 1, 64, 64, dummy, dummy, None, 0, None) == -4
+    # activation quantization on its own: ldq < K, null xq, bad dtype, short workspace
+    wsq = lib.sbq_w8a8_workspace_bytes(2, 64)
+    assert lib.sbq_act_quant_per_tensor(dummy, 0, 2, 64, 64, dummy, 63, dummy, dummy, dummy, wsq, None) == -1
+    assert lib.sbq_act_quant_per_tensor(dummy, 0, 2, 64, 64, None, 64, dummy, dummy, dummy, wsq, None) == -1
+    assert lib.sbq_act_quant_per_tensor(dummy, 7, 2, 64, 64, dummy, 64, dummy, dummy, dummy, wsq, None) == -2
+    assert lib.sbq_act_quant_per_tensor(dummy, 0, 2, 64, 64, dummy, 64, dummy, dummy, dummy, wsq - 1, None) == -4
     # the no-allocation W8A8 entry point: colsum required; quantized activations
     # beyond its static scratch (M * ceil(K/64)*64 > SBQ_NOALLOC_XQ_BYTES) rejected
     from sbq import _lib

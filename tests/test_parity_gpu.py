@@ -556,6 +556,51 @@ def test_w8a8_qparams_edge_cases(dev, kind):
     np.testing.assert_array_equal(lin(x.to(dev)).cpu().numpy(), oracle.dyn_linear(x.numpy(), q, s))
 
 
+ACT_QUANT_CASES = [  # (M, K, x dtype, row stride pad, xq row stride pad, kind)
+    (1, 4096, "f32", 0, 0, "outliers"), (7, 700, "f16", 0, 3, "normal"), (33, 4096, "bf16", 64, 0, "outliers"),
+    (128, 2560, "f32", 8, 16, "normal"), (5, 13, "f32", 3, 1, "normal"), (300, 1000, "f16", 0, 0, "tiny"),
+    (2, 64, "f32", 0, 0, "zeros"), (64, 12288, "f16", 0, 0, "positive"),
+]
+
+
+@pytest.mark.parametrize("M,K,xd,xpad,qpad,kind", ACT_QUANT_CASES)
+def test_act_quant_per_tensor_matches_oracle(dev, M, K, xd, xpad, qpad, kind):
+    """sbq_act_quant_per_tensor (the quantization step of linear_dynamic,
+    quant.py:65): scale, zero point and every uint8 value bit-exact against
+    the oracle, strided rows in and out (ragged K, unaligned strides); and
+    sbq_linear_w8a8's int32 accumulators equal sum_k (xq - zp) * q."""
+    announce(f"act quant M={M} K={K} x={xd} pads={xpad},{qpad} {kind}")
+    g = torch.Generator().manual_seed(M * 7 + K)
+    x = torch.randn(M, K, generator=g)
+    if kind == "outliers":
+        x[:, torch.randperm(K, generator=g)[: max(1, K // 100)]] *= 20
+    elif kind == "tiny":
+        x *= 1e-6
+    elif kind == "zeros":
+        x *= 0
+    elif kind == "positive":
+        x = x.abs() + 0.5
+    x = x.to(DT[xd])
+    xs = torch.zeros((M, K + xpad), dtype=x.dtype)
+    xs[:, :K] = x
+    xd_dev = xs.to(dev)[:, :K]
+    buf = torch.full((M, K + qpad), 77, dtype=torch.uint8, device=dev)
+    xq, s, z = quant.act_quant_per_tensor(xd_dev, out=buf)
+    so, zo = oracle.act_qparams(x.float().numpy())
+    assert (np.float32(s.item()), int(z.item())) == (np.float32(so), zo)
+    np.testing.assert_array_equal(xq.cpu().numpy(), oracle.quantize_act(x.float().numpy(), so, zo))
+    if qpad:
+        assert bool((buf[:, K:] == 77).all())  # the padding columns are left alone
+    N = 48
+    w = make_weights(N, K, 9)
+    q, _ = oracle.quantize_per_channel(w.numpy())
+    lin = quant.DynamicInt8Linear(w, None)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    quant.linear_w8a8(xd_dev, lin.packed, lin.scale, lin.colsum, None, N, acc_out=acc)
+    ref = (xq.cpu().numpy().astype(np.int64) - zo) @ q.astype(np.int64).T
+    np.testing.assert_array_equal(acc.cpu().numpy(), ref.astype(np.int32))
+
+
 def test_w8a8_bias_fused(dev):
     announce("w8a8 bias")
     N, K = 72, 512
