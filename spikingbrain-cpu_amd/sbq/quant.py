@@ -422,11 +422,12 @@ def greedy_tokens(logits: torch.Tensor) -> torch.Tensor:
         raise ValueError("greedy_tokens expects fp32 GPU logits")
     shape = logits.shape
     y = logits.reshape(-1, shape[-1])
-    if y.stride(-1) != 1:
+    if y.stride(-1) != 1 or (y.shape[0] > 1 and y.stride(0) < y.shape[1]):
         y = y.contiguous()
+    ld = y.shape[1] if y.shape[0] <= 1 else y.stride(0)  # one row is contiguous whatever its stride(0) says
     out = torch.empty((y.shape[0],), dtype=torch.int64, device=y.device)
     with torch.cuda.device(y.device):
-        _lib.check(_lib.load().sbq_argmax_rows(_ptr(y), y.shape[0], y.shape[1], y.stride(0), _ptr(out),
+        _lib.check(_lib.load().sbq_argmax_rows(_ptr(y), y.shape[0], y.shape[1], ld, _ptr(out),
                                                _stream(y.device)), "sbq_argmax_rows")
     return out.reshape(shape[:-1])
 
@@ -458,9 +459,10 @@ def sample_tokens(logits: torch.Tensor, temperature: float, top_p: float = 1.0, 
         return greedy_tokens(logits)
     shape = logits.shape
     y = logits.reshape(-1, shape[-1])
-    if y.stride(-1) != 1:
+    if y.stride(-1) != 1 or (y.shape[0] > 1 and y.stride(0) < y.shape[1]):
         y = y.contiguous()
     M, V = y.shape
+    ld = V if M <= 1 else y.stride(0)  # one row is contiguous whatever its stride(0) says
     out = torch.empty((M,), dtype=torch.int64, device=y.device)
     if u is None:
         if generator is not None and generator.device.type == "cuda":
@@ -470,10 +472,10 @@ def sample_tokens(logits: torch.Tensor, temperature: float, top_p: float = 1.0, 
     if u.dtype != torch.float32 or u.device != y.device or u.numel() != M or not u.is_contiguous():
         raise ValueError("u must be a contiguous fp32 tensor of one uniform per row on the logits' device")
     ws = workspace if workspace is not None else sample_workspace(M, V, y.device)
-    if ws.dtype != torch.uint8 or ws.device != y.device:
-        raise ValueError("workspace must be a uint8 tensor on the logits' device")
+    if ws.dtype != torch.uint8 or ws.device != y.device or not ws.is_contiguous():
+        raise ValueError("workspace must be a contiguous uint8 tensor on the logits' device")
     with torch.cuda.device(y.device):
-        _lib.check(_lib.load().sbq_sample_rows(_ptr(y), M, V, y.stride(0), float(temperature), int(top_k),
+        _lib.check(_lib.load().sbq_sample_rows(_ptr(y), M, V, ld, float(temperature), int(top_k),
                                                float(top_p), _ptr(u), _ptr(out), _ptr(ws), _nbytes(ws),
                                                _stream(y.device)), "sbq_sample_rows")
     return out.reshape(shape[:-1])

@@ -106,6 +106,22 @@ def test_sample_ties_greedy_and_invalid_rows(dev):
     assert int(greedy[0]) == 10 and int(greedy[1]) == 123 and int(greedy[3]) == int(torch.argmax(x[3]))
 
 
+def test_sample_strided_rows(dev):
+    """Rows of a wider buffer (row stride above V) and one row viewed from a
+    column (stride(0) below V): the same tokens as the contiguous copies."""
+    announce("sample strided rows")
+    V = 5000
+    big = torch.randn(3, V + 37, generator=torch.Generator().manual_seed(12)).to(dev) * 2
+    rows = big[:, :V]
+    u = torch.tensor([0.2, 0.6, 0.9], dtype=torch.float32, device=dev)
+    assert torch.equal(quant.sample_tokens(rows, 0.8, 0.9, 30, u=u), quant.sample_tokens(rows.contiguous(), 0.8, 0.9, 30, u=u))
+    assert torch.equal(quant.greedy_tokens(rows), quant.greedy_tokens(rows.contiguous()))
+    col = torch.randn(V, 1, generator=torch.Generator().manual_seed(13)).to(dev)
+    one = col.t()  # [1, V], stride (1, 1)
+    assert torch.equal(quant.sample_tokens(one, 1.0, 0.95, 0, u=u[:1]), quant.sample_tokens(one.contiguous(), 1.0, 0.95, 0, u=u[:1]))
+    assert torch.equal(quant.greedy_tokens(one), quant.greedy_tokens(one.contiguous()))
+
+
 def test_sample_drop_in_and_graph_replay(dev):
     """sbq.quant.sample(logits, params, generator) draws its uniform from the
     caller's CPU generator, as the engine passes one; sample_tokens captured
