@@ -79,8 +79,9 @@ def _as_activation(x2: torch.Tensor) -> torch.Tensor:
 
 
 def _ldx(x2: torch.Tensor) -> int:
-    """Row stride to pass for an activation from _as_activation: a single row
-    is contiguous whatever its stride(0) says (e.g. a transposed [K, 1])."""
+    """Row stride to pass for a 2-D operand with unit column stride (an
+    activation from _as_activation, an output, a weight): a single row is
+    contiguous whatever its stride(0) says (e.g. a transposed [K, 1])."""
     return x2.shape[1] if x2.shape[0] <= 1 else x2.stride(0)
 
 
@@ -138,8 +139,8 @@ def quantize_per_channel_gpu(weight: torch.Tensor) -> tuple[torch.Tensor, torch.
     q = torch.empty((N, K), dtype=torch.int8, device=w.device)
     scale = torch.empty((N,), dtype=torch.float32, device=w.device)
     with torch.cuda.device(w.device):
-        _lib.check(_lib.load().sbq_quantize_per_channel(_ptr(w), _code(w.dtype), N, K, w.stride(0), _ptr(q),
-                                                        q.stride(0), _ptr(scale), _stream(w.device)),
+        _lib.check(_lib.load().sbq_quantize_per_channel(_ptr(w), _code(w.dtype), N, K, _ldx(w), _ptr(q),
+                                                        _ldx(q), _ptr(scale), _stream(w.device)),
                    "sbq_quantize_per_channel")
     return q, scale
 
@@ -155,7 +156,7 @@ def repack(q: torch.Tensor, with_colsum: bool = True) -> tuple[torch.Tensor, tor
     packed = torch.empty((L.sbq_packed_bytes(N, K),), dtype=torch.uint8, device=q.device)
     colsum = torch.empty((N,), dtype=torch.int32, device=q.device) if with_colsum else None
     with torch.cuda.device(q.device):
-        _lib.check(L.sbq_repack_w8(_ptr(q), N, K, q.stride(0), _ptr(packed), _ptr(colsum), _stream(q.device)),
+        _lib.check(L.sbq_repack_w8(_ptr(q), N, K, _ldx(q), _ptr(packed), _ptr(colsum), _stream(q.device)),
                    "sbq_repack_w8")
     return packed, colsum
 
@@ -200,7 +201,7 @@ def linear_w8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, bias:
                     ws)
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
-                                             _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype), y.stride(0),
+                                             _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype), _ldx(y),
                                              _ptr(ws), _nbytes(ws), _stream(x2.device)),
                    "sbq_linear_w8")
     return y
@@ -269,7 +270,7 @@ def _run_grouped(name, xs, packeds, scales, colsums, biases, Ns, out_dtype, outs
                 arr(ctypes.c_void_p, [scales[i].data_ptr() for i in idx]))
         tail = (arr(ctypes.c_void_p, [0 if biases[i] is None else biases[i].data_ptr() for i in idx]),
                 arr(ctypes.c_int64, [Ns[i] for i in idx]), arr(ctypes.c_void_p, [ys[i].data_ptr() for i in idx]),
-                arr(ctypes.c_int64, [ys[i].stride(0) for i in idx]), _code(ydt))
+                arr(ctypes.c_int64, [_ldx(ys[i]) for i in idx]), _code(ydt))
         with torch.cuda.device(dev):
             if w8a8:
                 rc = L.sbq_linear_w8a8_grouped(*head, arr(ctypes.c_void_p, [colsums[i].data_ptr() for i in idx]),
@@ -357,7 +358,7 @@ def linear_w8a8(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, col
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8a8(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
                                                _ptr(scale), _ptr(colsum), _ptr(bias), N, _ptr(y), _code(y.dtype),
-                                               y.stride(0), _ptr(acc_out), _ptr(ws), _nbytes(ws),
+                                               _ldx(y), _ptr(acc_out), _ptr(ws), _nbytes(ws),
                                                _stream(x2.device)),
                    "sbq_linear_w8a8")
     return y
@@ -385,7 +386,7 @@ def linear_w8a8_noalloc(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Ten
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8a8_noalloc(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
                                                        _ptr(scale), _ptr(colsum), _ptr(bias), N, _ptr(out),
-                                                       _code(out.dtype), out.stride(0), _ptr(acc_out),
+                                                       _code(out.dtype), _ldx(out), _ptr(acc_out),
                                                        _stream(x2.device)),
                    "sbq_linear_w8a8_noalloc")
     return out
@@ -409,7 +410,7 @@ def linear_w8a8_token(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tenso
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8a8_token(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
                                                      _ptr(scale), _ptr(bias), N, _ptr(y), _code(y.dtype),
-                                                     y.stride(0), _ptr(acc_out), _ptr(ws), _nbytes(ws),
+                                                     _ldx(y), _ptr(acc_out), _ptr(ws), _nbytes(ws),
                                                      _stream(x2.device)),
                    "sbq_linear_w8a8_token")
     return y
@@ -424,7 +425,7 @@ def greedy_tokens(logits: torch.Tensor) -> torch.Tensor:
     y = logits.reshape(-1, shape[-1])
     if y.stride(-1) != 1 or (y.shape[0] > 1 and y.stride(0) < y.shape[1]):
         y = y.contiguous()
-    ld = y.shape[1] if y.shape[0] <= 1 else y.stride(0)  # one row is contiguous whatever its stride(0) says
+    ld = _ldx(y)
     out = torch.empty((y.shape[0],), dtype=torch.int64, device=y.device)
     with torch.cuda.device(y.device):
         _lib.check(_lib.load().sbq_argmax_rows(_ptr(y), y.shape[0], y.shape[1], ld, _ptr(out),
@@ -462,7 +463,7 @@ def sample_tokens(logits: torch.Tensor, temperature: float, top_p: float = 1.0, 
     if y.stride(-1) != 1 or (y.shape[0] > 1 and y.stride(0) < y.shape[1]):
         y = y.contiguous()
     M, V = y.shape
-    ld = V if M <= 1 else y.stride(0)  # one row is contiguous whatever its stride(0) says
+    ld = _ldx(y)
     out = torch.empty((M,), dtype=torch.int64, device=y.device)
     if u is None:
         if generator is not None and generator.device.type == "cuda":
@@ -531,7 +532,7 @@ def linear_w8_argmax(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor
     idx = _check_argmax("linear_w8_argmax", x2, state, idx)
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8_argmax(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
-                                                    _ptr(scale), _ptr(bias), N, _ptr(y), y.stride(0), _ptr(idx),
+                                                    _ptr(scale), _ptr(bias), N, _ptr(y), _ldx(y), _ptr(idx),
                                                     _ptr(ws), _nbytes(ws), _ptr(state), _stream(x2.device)),
                    "sbq_linear_w8_argmax")
     return y, idx
@@ -555,7 +556,7 @@ def linear_w8a8_argmax(x2: torch.Tensor, packed: torch.Tensor, scale: torch.Tens
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_linear_w8a8_argmax(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(packed),
                                                       _ptr(scale), _ptr(colsum), _ptr(bias), N, _ptr(y),
-                                                      y.stride(0), _ptr(idx), _ptr(ws), _nbytes(ws), _ptr(state),
+                                                      _ldx(y), _ptr(idx), _ptr(ws), _nbytes(ws), _ptr(state),
                                                       _stream(x2.device)),
                    "sbq_linear_w8a8_argmax")
     return y, idx
@@ -610,7 +611,7 @@ def act_quant_per_tensor(x2: torch.Tensor, out: torch.Tensor | None = None
     ws = w8a8_workspace(M, K, x2.device)
     with torch.cuda.device(x2.device):
         _lib.check(_lib.load().sbq_act_quant_per_tensor(_ptr(x2), _code(x2.dtype), M, K, _ldx(x2), _ptr(out),
-                                                        out.stride(0), _ptr(s), _ptr(z), _ptr(ws), _nbytes(ws),
+                                                        _ldx(out), _ptr(s), _ptr(z), _ptr(ws), _nbytes(ws),
                                                         _stream(x2.device)),
                    "sbq_act_quant_per_tensor")
     return out[:, :K], s, z

@@ -707,6 +707,28 @@ def test_mismatched_operands_raise_before_launch(dev):
     np.testing.assert_array_equal(quant.linear_w8(x, lin.packed, lin.scale, None, N).cpu().numpy(), ok.cpu().numpy())
 
 
+def test_single_row_views_with_small_row_stride(dev):
+    """One-row operands viewed from a column ([1, n] with stride(0) = 1, as
+    t() of an [n, 1] tensor gives): a weight row, an activation row and the
+    output row, in both formats; equal to the contiguous copies."""
+    announce("single-row views")
+    N, K = 96, 512
+    w1 = torch.randn(K, 1, generator=torch.Generator().manual_seed(61)).to(dev).t()  # [1, K], stride (1, 1)
+    q1, s1 = quant.quantize_per_channel_gpu(w1)
+    q2, s2 = quant.quantize_per_channel_gpu(w1.contiguous())
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+    w = make_weights(N, K, 62)
+    x1 = make_x(K, 1, 63).to(dev).t()  # [1, K], stride (1, 1)
+    for fmt in ("int8", "int8-dyn"):
+        lin = quant.make_linear(fmt, w, None)
+        out = torch.empty((N, 1), dtype=torch.float32, device=dev).t()  # [1, N], stride (1, 1)
+        if fmt == "int8":
+            quant.linear_w8(x1, lin.packed, lin.scale, None, N, out=out)
+        else:
+            quant.linear_w8a8(x1, lin.packed, lin.scale, lin.colsum, None, N, out=out)
+        np.testing.assert_array_equal(out.cpu().numpy(), lin(x1.contiguous()).cpu().numpy(), err_msg=fmt)
+
+
 def test_cpu_tensors_in_and_out(dev):
     """The reference model feeds CPU fp32 [T, B, K] tensors and views the
     fp32 contiguous result (model.py:262-264): same contract here."""
