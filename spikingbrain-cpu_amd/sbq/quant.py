@@ -317,7 +317,7 @@ def grouped_forward(pairs):
         ys = linear_w8a8_grouped(x2s, *args, [m.colsum for m in layers], *rest)
     else:
         ys = linear_w8_grouped(x2s, *args, *rest)
-    return [y.reshape(*shape0[:-1], -1) for y in ys]
+    return [y.reshape(*shape0[:-1], y.shape[-1]) for y in ys]
 
 
 def gemm_config(M: int, N: int, K: int, dtype: torch.dtype = torch.float16, w8a8: bool = False) -> tuple[int, int]:
@@ -708,7 +708,7 @@ class Int8Linear(nn.Module):
             return linear_w8(x2, self.packed, scale, bias, N, self.out_dtype)
 
         out = _run_on_device(x, self.qweight.device, run)
-        return out.reshape(*shape[:-1], -1)
+        return out.reshape(*shape[:-1], out.shape[-1])
 
     def forward_greedy(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """forward(x) and the greedy token of each row in one pass, for the
@@ -722,7 +722,7 @@ class Int8Linear(nn.Module):
         bias = None if self.bias is None else self.bias.float()
         y, idx = linear_w8_argmax(x.reshape(-1, shape[-1]), self.packed, self.scale.float(), bias, self.out_features,
                                   _greedy_state(self, x.device))
-        return y.reshape(*shape[:-1], -1), idx.reshape(shape[:-1])
+        return y.reshape(*shape[:-1], y.shape[-1]), idx.reshape(shape[:-1])
 
 
 class _Fp32Buffers:
@@ -788,7 +788,7 @@ class DynamicInt8Linear(_Fp32Buffers, nn.Module):
             return linear_w8a8(x2, self.packed, scale, self.colsum, bias, self.out_features, self.out_dtype)
 
         out = _run_on_device(x, self.packed.device, run)
-        return out.reshape(*shape[:-1], -1)
+        return out.reshape(*shape[:-1], out.shape[-1])
 
     def forward_greedy(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """forward(x) and the greedy token of each row in one pass (see
@@ -802,7 +802,7 @@ class DynamicInt8Linear(_Fp32Buffers, nn.Module):
         bias = None if self.bias is None else self.bias.float()
         y, idx = linear_w8a8_argmax(x.reshape(-1, shape[-1]), self.packed, self.scale.float(), self.colsum, bias,
                                     self.out_features, _greedy_state(self, x.device))
-        return y.reshape(*shape[:-1], -1), idx.reshape(shape[:-1])
+        return y.reshape(*shape[:-1], y.shape[-1]), idx.reshape(shape[:-1])
 
 
 def _dyn_from_quantized(qweight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None) -> "DynamicInt8Linear":
@@ -978,7 +978,7 @@ class FusedLinear(_Fp32Buffers, nn.Module):
 
         y = _run_on_device(x, self.packed.device, run)
         outs = torch.split(y, self.sizes, dim=-1)
-        return tuple(o.contiguous().reshape(*shape[:-1], -1) for o in outs)
+        return tuple(o.contiguous().reshape(*shape[:-1], o.shape[-1]) for o in outs)
 
     def _shared(self, x: torch.Tensor, i: int) -> torch.Tensor:
         """Part i's output for x from the launch of the current call

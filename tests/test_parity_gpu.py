@@ -729,6 +729,24 @@ def test_single_row_views_with_small_row_stride(dev):
         np.testing.assert_array_equal(out.cpu().numpy(), lin(x1.contiguous()).cpu().numpy(), err_msg=fmt)
 
 
+def test_empty_inputs(dev):
+    """No tokens: [0, K] and [2, 0, K] inputs give [0, N] and [2, 0, N] fp32
+    outputs as the reference's matmul does, on GPU and CPU tensors, in both
+    formats; no logits rows give no tokens."""
+    announce("empty inputs")
+    N, K = 48, 256
+    w = make_weights(N, K, 71)
+    for fmt in ("int8", "int8-dyn"):
+        mod = quant.make_linear(fmt, w, None)
+        for shape in ((0, K), (2, 0, K)):
+            for x in (torch.empty(shape, device=dev), torch.empty(shape)):
+                y = mod(x)
+                assert y.shape == shape[:-1] + (N,) and y.dtype == torch.float32 and y.device == x.device, (fmt, shape)
+    none = torch.empty((0, 1000), device=dev)
+    assert quant.greedy_tokens(none).shape == (0,)
+    assert quant.sample_tokens(none, 0.7, 0.9).shape == (0,)
+
+
 def test_cpu_tensors_in_and_out(dev):
     """The reference model feeds CPU fp32 [T, B, K] tensors and views the
     fp32 contiguous result (model.py:262-264): same contract here."""
