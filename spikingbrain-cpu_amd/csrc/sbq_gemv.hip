@@ -428,6 +428,10 @@ static GemvCfg pick_gemv(int64_t M, int64_t Nt, int64_t Kc, bool w8a8, int xt) {
   }
   if (c.p <= reg_p) {
     c.xm = XM_REG;
+    // the epilogue takes one thread per output pair (G * MT * 64 threads):
+    // two row tiles of x need two waves even when one wave covers K (the
+    // second wave's K range is empty and adds zeros)
+    if (c.waves < c.mt) c.waves = c.mt;
   } else if (c.mt == 1) {
     c.xm = XM_CHUNK;
   } else {

@@ -1274,6 +1274,35 @@ def test_graph_replays_lds_epilogue(dev):
 # block configuration, the register-staged GEMM) against the oracle, with
 # random activation and output dtypes and aligned or misaligned row strides
 # ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K,xd,yd,pad", [
+    (31, 51, 15, "f16", "f16", 1), (17, 942, 64, "f32", "f16", 8), (32, 100, 256, "bf16", "f32", 1),
+    (20, 33, 128, "f16", "bf16", 3), (17, 64, 64, "f32", "f32", 1), (24, 300, 200, "f32", "f32", 0),
+])
+def test_general_gemv_two_row_tiles_short_k(dev, M, N, K, xd, yd, pad):
+    """17..32 tokens at short K on the general GEMV (ragged K or misaligned
+    rows keep them off the fast paths): one wave covers K, and the second row
+    tile of x still gets its outputs (a workgroup of one wave once left rows
+    16..M-1 unwritten).  Both formats against the oracle."""
+    announce(f"general gemv two row tiles M={M} N={N} K={K} x={xd} y={yd} pad={pad}")
+    w = make_weights(N, K, 7100 + M)
+    big = torch.zeros((M, K + pad), dtype=DT[xd])
+    big[:, pad:] = make_x(M, K, 7200 + M, outliers=True).to(DT[xd])
+    x = big.to(dev)[:, pad:]
+    xv = x.float().cpu().numpy()
+    q, s = oracle.quantize_per_channel(w.numpy())
+    lin = quant.Int8Linear(w, None)
+    dyn = quant.DynamicInt8Linear(w, None)
+    y = torch.full((M, N), float("nan"), dtype=DT[yd], device=dev)
+    quant.linear_w8(x, lin.packed, lin.scale, None, N, out=y)
+    err = oracle.rel_l2(y.float().cpu().numpy(), oracle.int8_linear(xv, q, s))
+    assert err <= {"f32": W8_TOL, "f16": W8_TOL, "bf16": 5e-3}[yd], err
+    acc = torch.full((M, N), -7, dtype=torch.int32, device=dev)
+    yd8 = quant.linear_w8a8(x, dyn.packed, dyn.scale, dyn.colsum, None, N, acc_out=acc)
+    refd, info = oracle.dyn_linear(xv, q, s, return_intermediates=True)
+    np.testing.assert_array_equal(acc.cpu().numpy(), info["acc"])
+    np.testing.assert_array_equal(yd8.cpu().numpy(), refd)
+
+
 def _random_cases(n, seed):
     g = np.random.default_rng(seed)
     cases = []
