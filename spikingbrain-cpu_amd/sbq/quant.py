@@ -250,6 +250,14 @@ def _run_grouped(name, xs, packeds, scales, colsums, biases, Ns, out_dtype, outs
             raise ValueError(f"{name}: every x must have the shape, dtype and device of xs[0]")
     ys = list(outs) if outs is not None else [torch.empty((M, N), dtype=out_dtype, device=dev) for N in Ns]
     ydt = ys[0].dtype
+    if not w8a8 and M > 16:
+        # no grouped launch past decode sizes: each linear runs as linear_w8
+        # does on its own, with the prefill workspace it allocates (the C
+        # entry point's one-by-one fallback has none, which for fp32 x is a
+        # different, slower path)
+        if any(y.dtype != ydt for y in ys):
+            raise ValueError(f"{name}: every output must have one dtype")
+        return [linear_w8(xs[i], packeds[i], scales[i], biases[i], Ns[i], out=ys[i]) for i in range(n)]
     ws = None
     if w8a8:
         ws = workspace if workspace is not None else w8a8_workspace(M, K, dev)

@@ -941,14 +941,15 @@ def test_split_k_graph_replays(dev):
 GROUP_CASES = [
     # (M, K, Ns, x dtype): the hybrid layer's pairs (lora up-projections,
     # SSE / SWA output projections), mixed and ragged widths, fp32 / bf16 x,
-    # and M > 16 (no grouped kernel: the linears run one by one)
+    # and M > 16 (no grouped kernel: each linear runs as linear_w8 alone, with
+    # fp32 x the staged prefill path of its own workspace)
     (1, 128, (4096, 4096), "f16"),
     (1, 4096, (4096, 4096), "f16"),
     (4, 4096, (1000, 64, 4096, 4), "f16"),
     (16, 4096, (2048, 6144), "bf16"),
     (1, 4096, (4096, 4096, 4096), "f32"),
     (1, 12288, (4096, 10), "f16"),
-    (24, 4096, (4096, 1000), "f16"),
+    (24, 4096, (4096, 1000), "f16"), (20, 2560, (4096, 4096), "f32"), (40, 3008, (3888, 7472), "f32"),
     # M = 4 .. 8 over more than 1024 row tiles in all at K = 2560: five row
     # tiles per workgroup with x in LDS (fp32: split from registers), ragged
     # segments
