@@ -433,7 +433,10 @@ int sbq_linear_w8_argmax(const void* x, int x_dtype, int64_t M, int64_t K, int64
   if (!aligned(argmax_ws, 8)) return SBQ_ERR_ALIGN;
   hipStream_t st = (hipStream_t)stream;
   sbq::GemvArgmaxOut am{(uint8_t*)argmax_ws, idx, false};
-  if (sbq::gemv_supports(M, K, false, x_dtype)) {
+  // decode sizes: the GEMV with the token fused; larger M: the logits exactly
+  // as sbq_linear_w8 computes them (its row-tile and split-K routes), then
+  // the row argmax
+  if (M <= 16 && sbq::gemv_supports(M, K, false, x_dtype)) {
     const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, SBQ_F32, ldy, N);
     rc = sbq::launch_gemv_w8(x, x_dtype, M, K, ldx, xv, packed, scale, bias, N, y, SBQ_F32, ldy, st, yv, &am);
   } else {
@@ -456,13 +459,14 @@ int sbq_linear_w8a8_argmax(const void* x, int x_dtype, int64_t M, int64_t K, int
   const bool xv = x_vec_ok(x, x_dtype, ldx), yv = y_vec_ok(y, SBQ_F32, ldy, N);
   hipStream_t st = (hipStream_t)stream;
   sbq::GemvArgmaxOut am{(uint8_t*)argmax_ws, idx, false};
-  if (sbq::gemv_supports(M, K, true, x_dtype))
+  // decode sizes: the GEMV with the token fused; larger M: sbq_linear_w8a8's
+  // own routes (bit-identical logits either way), then the row argmax
+  if (M <= 16 && sbq::gemv_supports(M, K, true, x_dtype))
     rc = sbq::launch_gemv_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, SBQ_F32, ldy, nullptr,
                                ws_partials(workspace), st, yv, &am);
   else
-    rc = sbq::launch_gemm_w8a8(x, x_dtype, M, K, ldx, xv, packed, scale, colsum, bias, N, y, SBQ_F32, ldy, nullptr,
-                               ws_partials(workspace), ws_xq(workspace), ws_qp(workspace), st, yv,
-                               ws_split(workspace, M, K), ws_split_bytes(workspace, workspace_bytes, M, K));
+    rc = sbq_linear_w8a8(x, x_dtype, M, K, ldx, packed, scale, colsum, bias, N, y, SBQ_F32, ldy, nullptr, workspace,
+                         workspace_bytes, stream);
   if (rc || am.fused) return rc;
   return sbq::launch_argmax_rows(y, M, N, ldy, idx, st);
 }

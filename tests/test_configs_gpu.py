@@ -688,14 +688,18 @@ def test_lm_head_greedy_ties_nan_zeros(dev, fmt):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,N,K", [(20, 5000, 1024), (40, 3000, 512), (2, 1000, 200)])
-def test_greedy_one_pass_other_shapes(dev, M, N, K):
+@pytest.mark.parametrize("xd", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("M,N,K", [(20, 5000, 1024), (40, 3000, 512), (2, 1000, 200), (20, 845, 2560),
+                                   (24, 3520, 2560)])
+def test_greedy_one_pass_other_shapes(dev, M, N, K, xd):
     """Shapes the fused GEMV does not take (M > 16, ragged K): the logits
-    kernel and then the row argmax; same tokens."""
-    announce(f"greedy other shapes M={M} N={N} K={K}")
+    exactly as forward computes them (for fp16 / bf16 x at 16 < M <= 64 the
+    row-tile GEMV or the split GEMM, not the general GEMV), then the row
+    argmax; same tokens."""
+    announce(f"greedy other shapes M={M} N={N} K={K} x={xd}")
     for fmt in ("int8", "int8-dyn"):
         lm = quant.make_linear(fmt, gpu_weight(N, K, 66, dev))
-        x = cpu_x(M, K, 67).to(dev)
+        x = cpu_x(M, K, 67).to(DT[xd]).to(dev)
         y, tok = lm.forward_greedy(x)
         np.testing.assert_array_equal(y.cpu().numpy(), lm(x).cpu().numpy())
         _check_greedy(y, tok, lm)
