@@ -39,8 +39,15 @@ W8_TOL_EXACT_X = 2e-6
 # subnormals) and removes 128 * rowsum(x) in the epilogue: at K = 4096 with
 # N(0, 1) activations that offset is about 3x the result, so its fp32 rounding
 # reaches about 2e-6 relative (a numpy model of the scheme gives 1e-6, plain
-# fp32 accumulation 2e-7).
+# fp32 accumulation 2e-7).  The rounding grows like sqrt(K): at K = 12288 with
+# 1% of the channels x20, 3.4-4.05e-6 measured, the same with the row sums
+# from the pre-pass or from the K loop (gemm_f16_tol).
 W8_TOL_GEMM_F16 = 4e-6
+
+
+def gemm_f16_tol(K):
+    """The fp16 prefill GEMM's bar for fp16 / bf16 inputs at reduction length K."""
+    return W8_TOL_GEMM_F16 * max(1.0, (K / 4096) ** 0.5)
 DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
 
 
@@ -130,7 +137,7 @@ def test_w8_full_size(dev, M, N, K, xd, yd):
     quant.linear_w8(x.to(dev), lin.packed, lin.scale, None, N, out=out)
     rows = tile_sample(M, 3)
     ref = oracle.int8_linear(x.float().numpy()[rows], q, s)
-    tol = (W8_TOL_GEMM_F16 if M > 64 else W8_TOL_EXACT_X) if (xd != "f32" and yd == "f32") else W8_TOL
+    tol = (gemm_f16_tol(K) if M > 64 else W8_TOL_EXACT_X) if (xd != "f32" and yd == "f32") else W8_TOL
     assert oracle.rel_l2(pick(out, rows, cols), ref) <= tol
 
 
@@ -259,7 +266,7 @@ def test_random_prefill_picks_match_oracle(dev, i, M, N, K, xd, has_bias):
     bc = None if b is None else b.numpy()[cols]
     y = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N)
     ref = oracle.int8_linear(xv[rows], q, s, bc)
-    assert oracle.rel_l2(pick(y, rows, cols), ref) <= (W8_TOL if xd == "f32" else W8_TOL_GEMM_F16)
+    assert oracle.rel_l2(pick(y, rows, cols), ref) <= (W8_TOL if xd == "f32" else gemm_f16_tol(K))
     acc = torch.empty((M, N), dtype=torch.int32, device=dev)
     y8 = quant.linear_w8a8(xg, dyn.packed, dyn.scale, dyn.colsum, dyn.bias, N, acc_out=acc)
     acc_ref, y_ref = ref_w8a8(xv, rows, q, s, bc)
@@ -1202,7 +1209,7 @@ def test_prepass_row_layouts_match_oracle(dev, M, N, K, xd):
     for layout in ("dense", "strided", "offset"):
         xg = _layout(x, layout, dev)
         y = quant.linear_w8(xg, lin.packed, lin.scale, lin.bias, N, workspace=quant.w8_workspace(M, K, dev, DT[xd], N))
-        assert oracle.rel_l2(pick(y, rows, cols), ref) <= (W8_TOL if xd == "f32" else W8_TOL_GEMM_F16), layout
+        assert oracle.rel_l2(pick(y, rows, cols), ref) <= (W8_TOL if xd == "f32" else gemm_f16_tol(K)), layout
         acc = torch.empty((M, N), dtype=torch.int32, device=dev)
         y8 = quant.linear_w8a8(xg, dyn.packed, dyn.scale, dyn.colsum, dyn.bias, N, acc_out=acc,
                                workspace=quant.w8a8_workspace(M, K, dev, N, DT[xd]))
