@@ -185,6 +185,17 @@ int64_t sbq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype,
  * reference (diagnostics and tests of the configuration choice). */
 int sbq_gemm_config(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8, int* splits);
 
+/* The general decode GEMV's configuration for an [M, K] input of x_dtype
+ * (the kernel that runs ragged K, misaligned rows and 17..32 tokens on the
+ * layers the row-tile GEMV leaves): info[0..8] = supported (0 / 1), row
+ * tiles of x, weight tiles per group, K tiles per wave, waves per
+ * workgroup, activation mode (0 registers, 1 LDS, 2 chunks), staging
+ * chunks per thread, LDS bytes, and whether a kernel instance exists for
+ * it.  Host-only: needs no GPU.  SBQ_ERR_ARG / SBQ_ERR_DTYPE for a bad
+ * argument.  No counterpart in the reference (diagnostics and tests of the
+ * configuration choice). */
+int sbq_gemv_config(int64_t M, int64_t K, int x_dtype, int w8a8, int32_t* info);
+
 /* ---- int8-dyn W8A8 linear (DynamicInt8Linear.forward, quant.py:63-66) ---- */
 
 /* Workspace bytes sbq_linear_w8a8 / sbq_act_qparams need for an [M, K] input:

@@ -294,6 +294,12 @@ int64_t sbq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int x_dtype,
   return base + sbq::split_area_bytes(sbq::plan_gemm_dl(w8a8 != 0, 1, M, Nt, Kc, true));
 }
 
+int sbq_gemv_config(int64_t M, int64_t K, int x_dtype, int w8a8, int32_t* info) {
+  if (!valid_dtype(x_dtype)) return SBQ_ERR_DTYPE;
+  if (M < 1 || K < 1 || M > kIntMax || K > kIntMax || (w8a8 != 0 && w8a8 != 1) || !info) return SBQ_ERR_ARG;
+  return sbq::gemv_config_info(M, K, w8a8 != 0, x_dtype, info);
+}
+
 int sbq_gemm_config(int64_t M, int64_t N, int64_t K, int x_dtype, int w8a8, int* splits) {
   if (!valid_dtype(x_dtype)) return SBQ_ERR_DTYPE;
   if (M < 1 || N < 1 || K < 1 || M > kIntMax || N > kIntMax || K > kIntMax || (w8a8 != 0 && w8a8 != 1))

@@ -445,6 +445,27 @@ bool gemv_supports(int64_t M, int64_t K, bool w8a8, int xt) {
   return pick_gemv(M, 1, (K + 63) / 64, w8a8, xt).ok;
 }
 
+// Forward declaration: the instance table below decides whether a picked
+// configuration has a kernel.
+static bool gemv_instance_exists(const GemvCfg& c, int xt, bool w8a8);
+
+int gemv_config_info(int64_t M, int64_t K, bool w8a8, int xt, int32_t* info) {
+  const int64_t Kc = (K + 63) / 64;
+  const GemvCfg c = pick_gemv(M, 1, Kc, w8a8, xt);
+  const int64_t xb = xt == XT_F32 ? 4 : 2;
+  const int64_t lds = (int64_t)c.waves * c.g * c.mt * 64 * 16 + (c.xm == XM_LDS ? M * Kc * 64 * xb : 0);
+  info[0] = c.ok ? 1 : 0;
+  info[1] = c.mt;
+  info[2] = c.g;
+  info[3] = c.p;
+  info[4] = c.waves;
+  info[5] = c.xm;
+  info[6] = c.sc;
+  info[7] = (int32_t)std::min<int64_t>(lds, 0x7fffffff);
+  info[8] = c.ok && gemv_instance_exists(c, xt, w8a8) ? 1 : 0;
+  return 0;
+}
+
 // (MT, P, XM, SC).  Covers every configuration pick_gemv returns: P is one of
 // {1, 2, 4, 8, 12}, SC one of {1, 2, 4}; XM_REG only with P <= 4 (MT 1 or 2);
 // XM_CHUNK only with P in {8, 12} (K > 16 register-held tiles per wave).
@@ -497,6 +518,26 @@ static int launch_gemv_xt(const GemvCfg& c, GemvArgs a, hipStream_t st) {
   SBQ_GEMV_CONFIGS(SBQ_GEMV_CASE)
 #undef SBQ_GEMV_CASE
   return -1;
+}
+
+template <int XT, bool W8A8>
+static bool gemv_instance_exists_xt(const GemvCfg& c) {
+#define SBQ_GEMV_HAS(MT_, P_, XM_, SC_)                                                   \
+  if constexpr (gemv_instance_used<XT, W8A8, MT_, P_, XM_>()) {                         \
+    if (c.mt == MT_ && c.p == P_ && c.xm == XM_ && c.sc == SC_ && c.g == 1) return true; \
+  }
+  SBQ_GEMV_CONFIGS(SBQ_GEMV_HAS)
+#undef SBQ_GEMV_HAS
+  return false;
+}
+
+static bool gemv_instance_exists(const GemvCfg& c, int xt, bool w8a8) {
+  switch (xt) {
+    case XT_F16: return w8a8 ? gemv_instance_exists_xt<XT_F16, true>(c) : gemv_instance_exists_xt<XT_F16, false>(c);
+    case XT_BF16: return w8a8 ? gemv_instance_exists_xt<XT_BF16, true>(c) : gemv_instance_exists_xt<XT_BF16, false>(c);
+    case XT_F32: return w8a8 ? gemv_instance_exists_xt<XT_F32, true>(c) : gemv_instance_exists_xt<XT_F32, false>(c);
+  }
+  return false;
 }
 
 // The fast-path arguments with the fused greedy token attached when it is

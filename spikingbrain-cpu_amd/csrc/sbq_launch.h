@@ -36,6 +36,11 @@ int launch_sample_rows(const float* x, int64_t M, int64_t V, int64_t ld, float T
 
 // True when the streaming GEMV kernels take this M and K (otherwise the GEMM).
 bool gemv_supports(int64_t M, int64_t K, bool w8a8, int xt);
+// The general GEMV's configuration for an [M, K] input (sbq_gemv_config):
+// info[0..8] = ok, row tiles of x, weight tiles per group, K tiles per wave,
+// waves, activation mode, staging chunks per thread, LDS bytes, and whether a
+// kernel instance exists for it.
+int gemv_config_info(int64_t M, int64_t K, bool w8a8, int xt, int32_t* info);
 
 // Decode fast path (sbq_gemv_fast.hip): M <= 16, K % 64 == 0, aligned x rows.
 // pick_gemv_fast chooses a configuration id and the waves per workgroup;

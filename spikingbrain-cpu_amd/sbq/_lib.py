@@ -35,6 +35,7 @@ SIGNATURES = {
     "sbq_w8a8_workspace_bytes": (_L, [_L, _L]),
     "sbq_linear_workspace_bytes": (_L, [_L, _L, _L, _I, _I]),
     "sbq_gemm_config": (_I, [_L, _L, _L, _I, _I, _P]),
+    "sbq_gemv_config": (_I, [_L, _L, _I, _I, _P]),
     "sbq_act_qparams": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _S, _P]),
     "sbq_act_quant_per_tensor": (_I, [_P, _I, _L, _L, _L, _P, _L, _P, _P, _P, _S, _P]),
     "sbq_linear_w8a8": (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _L, _P, _I, _L, _P, _P, _S, _P]),

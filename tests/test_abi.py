@@ -265,3 +265,40 @@ def test_sample_tokens_rejects_host_logits():
         quant.sample_tokens(torch.zeros(1, 10), 0.7, 0.9)
     with pytest.raises(ValueError):
         quant.sample_tokens(torch.zeros(1, 10, dtype=torch.float16), 0.7, 0.9)
+
+
+def test_general_gemv_configurations_are_launchable(lib):
+    """Every configuration the general GEMV picks (M = 1..32, K = 1..12288,
+    both formats, every activation dtype) has a kernel instance and satisfies
+    the launch invariants its kernel relies on: at most 16 waves; the waves'
+    K ranges cover every K tile; one epilogue thread per output pair
+    (waves >= row tiles x weight tiles; too few once left rows 16..M-1
+    unwritten); LDS-staged activations fully staged by the threads' chunks;
+    LDS within the 160 KiB of a CU."""
+    info = (ctypes.c_int32 * 9)()
+    Ks = sorted(set(list(range(1, 300)) + list(range(300, 12289, 37)) + [64 * i for i in range(1, 193)]))
+    checked = 0
+    for w8a8 in (0, 1):
+        for dt in (0, 1, 2):
+            xb = 4 if dt == 0 else 2
+            for M in range(1, 33):
+                for K in Ks:
+                    assert lib.sbq_gemv_config(M, K, dt, w8a8, info) == 0
+                    ok, mt, g, p, waves, xm, sc, lds, inst = list(info)
+                    if not ok:
+                        continue
+                    Kc = (K + 63) // 64
+                    where = (M, K, dt, w8a8, list(info))
+                    assert inst == 1, where
+                    assert 1 <= waves <= 16, where
+                    assert p * waves >= Kc, where
+                    assert waves >= mt * g, where
+                    assert mt == (1 if M <= 16 else 2), where
+                    if xm == 1:  # staged in LDS: sc 16-byte chunks per thread cover x[M][Kc*64]
+                        assert sc * 64 * waves * 16 >= M * Kc * 64 * xb, where
+                    assert lds <= 160 * 1024, where
+                    checked += 1
+    assert checked > 50000
+    assert lib.sbq_gemv_config(0, 64, 1, 0, info) == -1
+    assert lib.sbq_gemv_config(1, 64, 9, 0, info) == -2
+    assert lib.sbq_gemv_config(1, 64, 1, 0, None) == -1
