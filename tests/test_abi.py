@@ -302,3 +302,20 @@ def test_general_gemv_configurations_are_launchable(lib):
     assert lib.sbq_gemv_config(0, 64, 1, 0, info) == -1
     assert lib.sbq_gemv_config(1, 64, 9, 0, info) == -2
     assert lib.sbq_gemv_config(1, 64, 1, 0, None) == -1
+
+
+@pytest.mark.parametrize("lang,std", [("c", "c99"), ("c++", "c++17")])
+def test_header_compiles_standalone(tmp_path, lang, std):
+    """include/sbq.h is a plain C interface: it compiles on its own as C99 and
+    as C++ with every warning an error (what a cgo / FFI binding includes)."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc" if lang == "c" else "g++")
+    if cc is None:
+        pytest.skip("no host compiler")
+    src = tmp_path / ("use.c" if lang == "c" else "use.cpp")
+    src.write_text('#include "sbq.h"\nint sbq_use(void) { return SBQ_OK + SBQ_F16 + SBQ_MAX_GROUP; }\n')
+    r = subprocess.run([cc, f"-std={std}", "-Wall", "-Wextra", "-pedantic", "-Werror", "-fsyntax-only",
+                        f"-I{HEADER.parent}", str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
