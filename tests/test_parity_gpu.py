@@ -729,6 +729,24 @@ def test_single_row_views_with_small_row_stride(dev):
         np.testing.assert_array_equal(out.cpu().numpy(), lin(x1.contiguous()).cpu().numpy(), err_msg=fmt)
 
 
+@pytest.mark.parametrize("M,K,xd", [(1, 16384, "f16"), (4, 24576, "f32"), (1, 40000, "bf16"), (3, 65536, "f16"),
+                                    (20, 20000, "f32")])
+def test_long_k_beyond_the_gemv(dev, M, K, xd):
+    """K beyond the decode GEMVs' 12288 (no model layer has it; a caller
+    might): the tiled GEMM serves even one token; both formats against the
+    oracle."""
+    announce(f"long K M={M} K={K} x={xd}")
+    N = 200
+    w = make_weights(N, K, 81)
+    q, s = oracle.quantize_per_channel(w.numpy())
+    x = make_x(M, K, 82, outliers=True).to(DT[xd])
+    xv = x.float().numpy()
+    y = quant.Int8Linear(w, None)(x.to(dev))
+    assert oracle.rel_l2(y.cpu().numpy(), oracle.int8_linear(xv, q, s)) <= W8_TOL
+    yd = quant.DynamicInt8Linear(w, None)(x.to(dev))
+    np.testing.assert_array_equal(yd.cpu().numpy(), oracle.dyn_linear(xv, q, s))
+
+
 def test_empty_inputs(dev):
     """No tokens: [0, K] and [2, 0, K] inputs give [0, N] and [2, 0, N] fp32
     outputs as the reference's matmul does, on GPU and CPU tensors, in both
