@@ -747,6 +747,30 @@ def test_long_k_beyond_the_gemv(dev, M, K, xd):
     np.testing.assert_array_equal(yd.cpu().numpy(), oracle.dyn_linear(xv, q, s))
 
 
+@pytest.mark.parametrize("M,N,K,xd", [(65536, 16, 4096, "f16"), (100003, 8, 512, "f32"), (40000, 3, 1000, "bf16")])
+def test_many_tokens_few_outputs(dev, M, N, K, xd):
+    """Very tall, narrow calls (a router over a long prompt): grids of many
+    row blocks and one column block; sampled rows against the oracle, int8-dyn
+    with the parameters of the whole tensor."""
+    announce(f"many tokens M={M} N={N} K={K} x={xd}")
+    w = make_weights(N, K, 83)
+    q, s = oracle.quantize_per_channel(w.numpy())
+    x = make_x(M, K, 84, outliers=True).to(DT[xd])
+    xg = x.to(dev)
+    rows = np.unique(np.concatenate([np.arange(0, M, max(1, M // 97)), [M - 1]]))
+    xv = x.float().numpy()
+    y = quant.Int8Linear(w, None)(xg)
+    assert oracle.rel_l2(y.cpu().numpy()[rows], oracle.int8_linear(xv[rows], q, s)) <= W8_TOL
+    dyn = quant.DynamicInt8Linear(w, None)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    yd = quant.linear_w8a8(xg, dyn.packed, dyn.scale, dyn.colsum, None, N, acc_out=acc)
+    sx, zp = oracle.act_qparams(xv)
+    xq = oracle.quantize_act(xv[rows], sx, zp)
+    acc_ref = ((xq.astype(np.int64) - zp) @ q.astype(np.int64).T).astype(np.int32)
+    np.testing.assert_array_equal(acc.cpu().numpy()[rows], acc_ref)
+    np.testing.assert_array_equal(yd.cpu().numpy()[rows], oracle.dyn_epilogue(acc_ref, sx, s))
+
+
 def test_empty_inputs(dev):
     """No tokens: [0, K] and [2, 0, K] inputs give [0, N] and [2, 0, N] fp32
     outputs as the reference's matmul does, on GPU and CPU tensors, in both
