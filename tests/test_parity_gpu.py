@@ -1158,6 +1158,63 @@ def test_concurrent_streams_match_sequential(dev):
                 np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy(), err_msg=f"stream {i} M={x.shape[0]}")
 
 
+def test_concurrent_host_threads_match_sequential(dev):
+    """Host threads calling the library at once, each on its own stream with
+    its own workspaces (ctypes releases the GIL for every call, so the calls
+    overlap on the host as well as on the GPU): module calls, the greedy
+    token (separate and fused with lm_head) and the sampler give the results
+    of the same calls made one after the other."""
+    import threading
+
+    announce("four host threads")
+    K, V = 2560, 20000
+    lins = [quant.Int8Linear(make_weights(N, K, 190 + i), None) for i, N in enumerate((9728, 1024))]
+    dyns = [quant.DynamicInt8Linear(make_weights(N, K, 195 + i), None) for i, N in enumerate((4096, 640))]
+    head = quant.Int8Linear(make_weights(V, K, 199), None)
+    xs = [make_x(M, K, 200 + M).to(dev).half() for M in (1, 4, 24, 160)]
+    uni = torch.rand(4, generator=torch.Generator().manual_seed(205)).to(dev)
+    torch.cuda.synchronize()  # inputs and packed weights made on the default stream
+
+    def work(t, reps):
+        s = torch.cuda.Stream()  # default priority
+        out = []
+        with torch.cuda.stream(s):
+            for _ in range(reps):
+                res = []
+                for j, x in enumerate(xs):
+                    lin, dyn = lins[(t + j) % 2], dyns[(t + j) % 2]
+                    res.append(lin(x))
+                    res.append(dyn(x))
+                logits = head(xs[1])
+                res.append(quant.greedy_tokens(logits))
+                res.append(quant.sample_tokens(logits, 0.7, top_p=0.9, u=uni))
+                res.extend(head.forward_greedy(xs[1]))  # a fused-argmax state per stream
+                out = res
+        s.synchronize()
+        return out
+
+    ref = [work(t, 1) for t in range(4)]
+    got = [None] * 4
+    errs = []
+
+    def run(t):
+        try:
+            got[t] = work(t, 3)
+        except Exception as e:  # reported below, not lost in the thread
+            errs.append(repr(e))
+
+    threads = [threading.Thread(target=run, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errs, errs
+    for t in range(4):
+        assert len(got[t]) == len(ref[t])
+        for k, (a, b) in enumerate(zip(got[t], ref[t])):
+            np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy(), err_msg=f"thread {t} result {k}")
+
+
 # ---------------------------------------------------------------------------
 # model-level fidelity, as the reference's loader test checks its formats
 # (tests/test_model.py:180-192: logits of a tiny random model in each format
