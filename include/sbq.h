@@ -354,7 +354,10 @@ int64_t sbq_sample_workspace_bytes(int64_t M, int64_t V);
  *   z = logits / temperature (fp32 division); top_k > 0: tokens below the
  *     min(top_k, V)-th largest z are masked; p = softmax(z);
  *   0 < top_p < 1: a token is kept while the probability mass of the tokens
- *     above it stays below top_p (ties at that boundary are all kept);
+ *     above it stays below top_p, the tokens taken in the order of z (of
+ *     two tokens of equal fp32 probability the larger z first; the
+ *     reference's sort leaves their order open), ties of z at that boundary
+ *     all kept;
  *   the draw: the first index (vocabulary order) whose prefix of kept mass
  *     exceeds u[m] * (kept mass), u: device fp32 [M] uniforms in [0, 1), one
  *     per row, drawn by the caller (torch.multinomial's distribution; the

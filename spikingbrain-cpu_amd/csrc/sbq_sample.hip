@@ -27,9 +27,12 @@
 // workgroup), so no workgroup waits for another.  The first pass of each
 // selection rides on the launch before it (the max pass, the softmax-sum
 // pass).  Rows are independent (grid.y).  Differences from
-// the reference's sort-based form: tokens whose z ties the top-p boundary
-// are all kept (the sort keeps some of them, in its own order), and a
-// token's mass is exp(z - max) truncated to 2^-40.
+// the reference's sort-based form: the top-p rule walks the tokens in the
+// order of z, where the sort walks the fp32 probabilities, so of two tokens
+// whose probabilities round to the same fp32 value the larger z comes first
+// (the sort leaves the order of equal values open); tokens whose z ties the
+// top-p boundary are all kept (the sort keeps some of them, in its own
+// order); and a token's mass is exp(z - max) truncated to 2^-40.
 #include <stdint.h>
 
 #include "sbq_common.h"

@@ -457,7 +457,10 @@ def sample_tokens(logits: torch.Tensor, temperature: float, top_p: float = 1.0, 
     takes one uniform in [0, 1) per row: `u` (fp32, on the logits' device), or
     torch.rand from `generator` (a CPU generator, as the engine passes, or one
     on the logits' device) - the randomness stays the caller's, as with
-    torch.multinomial.  Tokens whose z ties the top-p boundary are all kept.
+    torch.multinomial.  The top-p rule takes the tokens in the order of z
+    (of two tokens of equal fp32 probability, whose order the reference's
+    sort leaves open, the larger z first); tokens whose z ties the top-p
+    boundary are all kept.
     A row with a NaN (or an infinite maximum after the division) gets -1, where
     the reference raises."""
     if logits.dtype != torch.float32 or not logits.is_cuda:

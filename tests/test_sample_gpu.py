@@ -6,8 +6,12 @@ The kernel finds the top-k value and the top-p boundary by radix selection
 and sums probabilities in 2^-40 fixed point; the oracle sorts and sums in
 float64.  So a token may differ only where the oracle itself changes its
 answer under a perturbation of 2e-6 of the uniform or of top_p (a draw or a
-kept-set boundary that close); every other token must be equal, and the
-count of boundary cases is checked to stay small.
+kept-set boundary that close), or where tokens of equal fp32 probability
+meet the top-p boundary: engine.py:38 sorts with probs.sort(descending=True),
+which leaves the order of equal values open; the oracle takes them in index
+order, the kernel in the order of z (larger first), and both are the
+reference's rule.  Every other token must be equal, and the count of
+boundary cases is checked to stay small.
 """
 import numpy as np
 import pytest
@@ -26,14 +30,32 @@ PARAMS = [  # (temperature, top_k, top_p): the engine's defaults first (engine.p
 DELTA = 2e-6
 
 
+def _token_ties_by_z(x, T, k, p, u):
+    """The oracle's draw with tokens of equal fp32 probability taken in the
+    order of z (larger first, then index) instead of index order when the
+    top-p rule walks the sorted probabilities (engine.py:38-40)."""
+    pf = oracle.sample_probs(x, T, k, 1.0)
+    z = (np.asarray(x, np.float32) / np.float32(T)).astype(np.float32)
+    order = np.lexsort((np.arange(z.size), -z, -pf))
+    sp = pf[order]
+    keep = (np.cumsum(sp.astype(np.float64)).astype(np.float32) - sp) < np.float32(p)
+    kept = np.zeros_like(pf)
+    kept[order] = sp * keep
+    c = np.cumsum(kept.astype(np.float64))
+    return int(np.searchsorted(c, u * c[-1], side="right"))
+
+
 def _accept(x, T, k, p, u, tok):
-    """The oracle's token, and whether `tok` is acceptable: equal to it, or to
-    the oracle's answer under a 2e-6 perturbation of u or top_p."""
+    """The oracle's token, and whether `tok` is acceptable: equal to it, to
+    the oracle's answer under a 2e-6 perturbation of u or top_p, or to the
+    draw with equal probabilities at the top-p boundary taken in z order."""
     want = oracle.sample_token(x, T, k, p, u)
     if tok == want:
         return want, True, False
     alts = {oracle.sample_token(x, T, k, pp, uu) for uu in (max(u - DELTA, 0.0), u, min(u + DELTA, 1 - 1e-9))
             for pp in ((p - DELTA, p, p + DELTA) if 0 < p < 1 else (p,))}
+    if want >= 0 and T > 0 and 0 < p < 1:
+        alts.add(_token_ties_by_z(x, T, k, p, u))
     return want, tok in alts, True
 
 
@@ -104,6 +126,36 @@ def test_sample_ties_greedy_and_invalid_rows(dev):
     assert seen == {10, 20, 30, 40}
     greedy = quant.sample_tokens(xd, 0.0).cpu()
     assert int(greedy[0]) == 10 and int(greedy[1]) == 123 and int(greedy[3]) == int(torch.argmax(x[3]))
+
+
+def test_sample_top_p_boundary_probability_ties(dev):
+    """Two tokens whose z differ by one ulp (0.2 at index 0, 0.20000002 at
+    index 2) have the same fp32 probability, and top_p cuts between them.
+    The reference's sort leaves their order open (engine.py:38); the kernel
+    keeps the larger z (index 2), the oracle's index order keeps index 0, and
+    the draws from the two kept sets differ.  A regression case from a
+    randomized run (V = 131183, T = 1, top_p 0.3)."""
+    announce("sample top-p boundary probability ties")
+    x = np.array([0.2, -1.0, 0.20000002, -0.7, -2.0, 1.5], np.float32)
+    pf = oracle.sample_probs(x, 1.0, 0, 1.0)
+    assert pf[0] == pf[2] and x[0] != x[2]  # equal fp32 probabilities of different z
+    top_p = float(pf[5] + pf[0] / 2)  # keeps index 5 and one of the pair
+    xd = torch.from_numpy(np.stack([x, x])).to(dev)
+    for u0 in (0.01, 0.05, 0.15):
+        assert oracle.sample_token(x, 1.0, 0, top_p, u0) == 0
+        assert _token_ties_by_z(x, 1.0, 0, top_p, u0) == 2
+        toks = _run(xd, 1.0, 0, top_p, torch.full((2,), u0, dtype=torch.float32, device=dev))
+        assert toks.tolist() == [2, 2], toks
+        assert _accept(x, 1.0, 0, top_p, u0, 2)[1]
+    # the randomized run's rows (row 0 met such a pair at the boundary)
+    big = torch.randn(5, 131183, generator=torch.Generator().manual_seed(160384264)) * 0.3
+    us = torch.tensor([0.4574942, 0.953343, 0.942172, 0.29724792, 0.47127655], dtype=torch.float32)
+    toks = _run(big.to(dev), 1.0, 0, 0.3, us.to(dev))
+    xn = big.numpy()
+    assert oracle.sample_token(xn[0], 1.0, 0, 0.3, float(us[0])) != _token_ties_by_z(xn[0], 1.0, 0, 0.3, float(us[0]))
+    assert int(toks[0]) == _token_ties_by_z(xn[0], 1.0, 0, 0.3, float(us[0]))
+    for r in range(5):
+        assert _accept(xn[r], 1.0, 0, 0.3, float(us[r]), int(toks[r]))[1], r
 
 
 def test_sample_strided_rows(dev):
