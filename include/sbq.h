@@ -356,8 +356,9 @@ int64_t sbq_sample_workspace_bytes(int64_t M, int64_t V);
  *   0 < top_p < 1: a token is kept while the probability mass of the tokens
  *     above it stays below top_p, the tokens taken in the order of z (of
  *     two tokens of equal fp32 probability the larger z first; the
- *     reference's sort leaves their order open), ties of z at that boundary
- *     all kept;
+ *     reference's sort leaves their order open); of tokens of equal z at
+ *     that boundary, as many as the rule admits, first in vocabulary order
+ *     (a stable sort's order);
  *   the draw: the first index (vocabulary order) whose prefix of kept mass
  *     exceeds u[m] * (kept mass), u: device fp32 [M] uniforms in [0, 1), one
  *     per row, drawn by the caller (torch.multinomial's distribution; the

@@ -30,9 +30,10 @@
 // the reference's sort-based form: the top-p rule walks the tokens in the
 // order of z, where the sort walks the fp32 probabilities, so of two tokens
 // whose probabilities round to the same fp32 value the larger z comes first
-// (the sort leaves the order of equal values open); tokens whose z ties the
-// top-p boundary are all kept (the sort keeps some of them, in its own
-// order); and a token's mass is exp(z - max) truncated to 2^-40.
+// (the sort leaves the order of equal values open); and a token's mass is
+// exp(z - max) truncated to 2^-40.  Tokens whose z ties at the top-p boundary
+// are kept as the sort keeps them: as many as its rule admits, the first ones
+// in vocabulary order (the order a stable sort gives them).
 #include <stdint.h>
 
 #include "sbq_common.h"
@@ -51,19 +52,24 @@ struct SampRow {
   static constexpr int64_t kMax = 256;                      // float [G]
   static constexpr int64_t kNan = kMax + 512;               // int [G]
   static constexpr int64_t kEsum = kNan + 512;              // uint64 [G]: mass of the tokens top-k keeps
-  static constexpr int64_t kBsum = kEsum + 512;             // uint64 [G]: mass of the tokens both keep
-  static constexpr int64_t kState = kBsum + 512;            // SampState [2]
+  static constexpr int64_t kBsum = kEsum + 512;             // uint64 [G]: mass of the tokens both keep (boundary ties aside)
+  static constexpr int64_t kTie = kBsum + 512;              // int [G]: tokens of the top-p boundary key
+  static constexpr int64_t kState = kTie + 256;             // SampState [2]
   static constexpr int64_t kHist = kState + 256;            // uint64 [G][256]: top-k pass 0, per workgroup
   static constexpr int64_t kGh = kHist + kSampMaxBlocks * 256 * 8;  // uint64 [7][256]: the later passes' sums
   static constexpr int64_t kBytes = kGh + 7 * 256 * 8;
 };
-static_assert(kSampMaxBlocks * 8 <= 512 && kSampMaxBlocks <= 64, "per-block arrays fit their slots and one wave");
+static_assert(kSampMaxBlocks * 8 <= 512 && kSampMaxBlocks * 4 <= 256 && kSampMaxBlocks <= 64,
+              "per-block arrays fit their slots and one wave");
 
 struct SampHead {
-  uint32_t kth;   // key of the k-th largest z (0: no top-k)
-  uint32_t tkey;  // key of the top-p boundary (0: no top-p)
-  float m;        // max z
-  int valid;      // 0: a NaN or an infinite max (the reference raises)
+  uint32_t kth;    // key of the k-th largest z (0: no top-k)
+  uint32_t tkey;   // key of the top-p boundary (0: no top-p)
+  float m;         // max z
+  int valid;       // 0: a NaN or an infinite max (the reference raises)
+  int tie_n;       // top-p keeps the first tie_n tokens of key tkey (vocabulary order) ...
+  int pad;
+  uint64_t tie_f;  // ... each of mass tie_f (0: no such tokens)
 };
 
 // Radix descent state before a pass: the key bits found so far and the
@@ -91,6 +97,11 @@ struct SampArgs {
 __device__ __forceinline__ uint32_t samp_key(float z) {
   const uint32_t b = __float_as_uint(z == 0.0f ? 0.0f : z);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// z of a key (the inverse of samp_key; +0 for the key of zeros)
+__device__ __forceinline__ float samp_unkey(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
 __device__ __forceinline__ float samp_z(const SampArgs& a, const float* row, int i) { return row[i] / a.T; }
@@ -364,6 +375,8 @@ __global__ __launch_bounds__(kSampThreads) void samp_soft_kernel(SampArgs a) {
       h->tkey = 0;
       h->m = m;
       h->valid = valid ? 1 : 0;
+      h->tie_n = 0;
+      h->tie_f = 0;
       if (topp) ((SampState*)(w + SampRow::kState))[0] = SampState{0u, 0u, 0u};
     }
   }
@@ -372,6 +385,12 @@ __global__ __launch_bounds__(kSampThreads) void samp_soft_kernel(SampArgs a) {
 
 // With top-p: the mass of the tokens both cuts keep, per workgroup (the top-p
 // boundary's last digit is derived here); workgroup 0 records the boundary.
+// The tokens of the boundary key share one z, so one mass f.  The reference's
+// sort puts them together (in vocabulary order: a stable sort) and its rule
+// keeps the j-th of them while the mass above it, A + j f, stays below
+// top_p: the first n = ceil((thr - A) / f) of them (A: the mass of the keys
+// above, the descent's rest).  They are counted per workgroup here and left
+// out of its mass; the draw adds f for each of the first n.
 __global__ __launch_bounds__(kSampThreads) void samp_bsum_kernel(SampArgs a) {
   __shared__ uint64_t H[1024];
   __shared__ SampState bcast;
@@ -380,33 +399,57 @@ __global__ __launch_bounds__(kSampThreads) void samp_bsum_kernel(SampArgs a) {
   uint8_t* w = samp_row_ws(a);
   SampHead* h = (SampHead*)(w + SampRow::kHead);
   const uint64_t S = samp_sum_g((const uint64_t*)(w + SampRow::kEsum), a.G);
-  const uint32_t tkey = samp_descend<true>((const uint64_t*)(w + SampRow::kGh) + 6 * 256, 1,
-                                           ((const SampState*)(w + SampRow::kState))[1], samp_thr(a.top_p, S), H,
-                                           &bcast)
-                            .prefix;
+  const uint64_t thr = samp_thr(a.top_p, S);
+  const uint64_t* last = (const uint64_t*)(w + SampRow::kGh) + 6 * 256;  // pass 3: masses by the key's low byte
+  const SampState fin = samp_descend<true>(last, 1, ((const SampState*)(w + SampRow::kState))[1], thr, H, &bcast);
+  const uint32_t tkey = fin.prefix;
   const uint32_t kth = h->kth;
   const float m = h->m;
   const bool valid = h->valid != 0;
   const uint32_t lim = kth > tkey ? kth : tkey;
+  // the boundary key's tokens: mass f each, tmass in all (0: none kept by top-k)
+  const uint64_t tmass = last[tkey & 255u];
+  const uint64_t f = valid && tmass ? samp_efix(samp_unkey(tkey), kth, m) : 0;
   const int i0 = blockIdx.x * a.per, i1 = min(i0 + a.per, a.V);
-  uint64_t part = 0;
+  uint64_t part = 0, ties = 0;
   if (valid)
     for (int i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
       const float z = samp_z(a, row, i);
-      if (samp_key(z) >= lim) part += samp_efix(z, kth, m);
+      const uint32_t key = samp_key(z);
+      if (f && key == tkey)
+        ++ties;
+      else if (key >= lim)
+        part += samp_efix(z, kth, m);
     }
   const uint64_t b = samp_block_sum_u64(part, red);
+  const uint64_t tc = samp_block_sum_u64(ties, red);
   if (threadIdx.x == 0) {
     ((uint64_t*)(w + SampRow::kBsum))[blockIdx.x] = b;
-    if (blockIdx.x == 0) h->tkey = tkey;
+    ((int*)(w + SampRow::kTie))[blockIdx.x] = (int)tc;
+    if (blockIdx.x == 0) {
+      uint64_t n = 0;
+      if (f) {
+        const uint64_t cnt = tmass / f;  // every token of the key adds the same f
+        n = thr > fin.rest ? (thr - fin.rest + f - 1) / f : 0;  // >= 1: the boundary key qualifies
+        if (n > cnt) n = cnt;
+      }
+      h->tkey = tkey;
+      h->tie_f = f;
+      h->tie_n = (int)n;
+    }
   }
 }
 
 // The draw: the first index whose prefix of kept mass exceeds u * total.
 // One workgroup per row; thread t owns a contiguous run of the chosen
-// workgroup slice; wave scans, then the wave totals in order.
+// workgroup slice; wave scans, then the wave totals in order.  With top-p,
+// of the tokens of the boundary key only the first tie_n (vocabulary order)
+// count, tie_f each: a slice keeps those of them that the slices before it
+// leave, and a token's rank among them is the slice's start plus the ties
+// of the threads before it and of its own run before it.
 __global__ __launch_bounds__(kSampThreads) void samp_pick_kernel(SampArgs a, int use_bsum) {
   __shared__ uint64_t wtot[16];
+  __shared__ int wtie[16];
   __shared__ int found;
   const int row_i = blockIdx.y;
   const float* row = a.x + (int64_t)row_i * a.ld;
@@ -418,8 +461,20 @@ __global__ __launch_bounds__(kSampThreads) void samp_pick_kernel(SampArgs a, int
   }
   const uint64_t* bsum = (const uint64_t*)(w + (use_bsum ? SampRow::kBsum : SampRow::kEsum));
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  // every wave: the slice sums in lanes, their inclusive prefix, the total
-  const uint64_t mine_g = lane < a.G ? bsum[lane] : 0;
+  const uint64_t tf = use_bsum ? h->tie_f : 0;
+  const int tn = use_bsum ? h->tie_n : 0;
+  // every wave: the boundary ties of the slices in lanes and their prefix ...
+  const int tc_g = tf && lane < a.G ? ((const int*)(w + SampRow::kTie))[lane] : 0;
+  int tpre_g = tc_g;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(tpre_g, o);
+    if (lane >= o) tpre_g += v;
+  }
+  const int tbefore_g = tpre_g - tc_g;  // ties in the slices before
+  const int tkeep_g = min(max(tn - tbefore_g, 0), tc_g);
+  // ... the slice masses, their inclusive prefix, the total
+  const uint64_t mine_g = lane < a.G ? bsum[lane] + tf * (uint64_t)tkeep_g : 0;
   uint64_t pre_g = mine_g;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -435,17 +490,38 @@ __global__ __launch_bounds__(kSampThreads) void samp_pick_kernel(SampArgs a, int
   const uint64_t over = __ballot(lane < a.G && pre_g > target);
   const int g = over ? __ffsll((long long)over) - 1 : a.G - 1;
   target -= __shfl(pre_g - mine_g, g);  // within workgroup slice g
+  const int trank0 = __shfl(tbefore_g, g);
   const uint32_t kth = h->kth, tkey = h->tkey;
   const uint32_t lim = kth > tkey ? kth : tkey;
   const float m = h->m;
   const int i0 = g * a.per, i1 = min(i0 + a.per, a.V);
   const int e = (i1 - i0 + (int)blockDim.x - 1) / (int)blockDim.x;  // elements per thread
   const int t0 = i0 + threadIdx.x * e, t1 = min(t0 + e, i1);
-  uint64_t mine = 0;
-  for (int i = t0; i < t1; ++i) {
-    const float z = samp_z(a, row, i);
-    if (samp_key(z) >= lim) mine += samp_efix(z, kth, m);
+  // boundary ties of this thread's run, then their exclusive prefix over the threads
+  int myt = 0;
+  if (tf)
+    for (int i = t0; i < t1; ++i) myt += samp_key(samp_z(a, row, i)) == tkey;
+  int tincl = myt;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(tincl, o);
+    if (lane >= o) tincl += v;
   }
+  if (lane == 63) wtie[wv] = tincl;
+  __syncthreads();
+  int tbase = trank0;
+  for (int i = 0; i < wv; ++i) tbase += wtie[i];
+  const int rank0 = tbase + tincl - myt;  // rank of this run's first boundary tie
+  // the kept mass of token i (rank: the boundary ties met so far)
+  auto kept = [&](int i, int& rank) -> uint64_t {
+    const float z = samp_z(a, row, i);
+    const uint32_t key = samp_key(z);
+    if (tf && key == tkey) return rank++ < tn ? tf : 0;
+    return key >= lim ? samp_efix(z, kth, m) : 0;
+  };
+  uint64_t mine = 0;
+  int rank = rank0;
+  for (int i = t0; i < t1; ++i) mine += kept(i, rank);
   // inclusive scan within the wave, then the wave totals in wave order
   uint64_t incl = mine;
 #pragma unroll
@@ -462,9 +538,9 @@ __global__ __launch_bounds__(kSampThreads) void samp_pick_kernel(SampArgs a, int
   const uint64_t excl = incl - mine;
   if (excl <= target && target < incl) {
     uint64_t c = excl;
+    rank = rank0;
     for (int i = t0; i < t1; ++i) {
-      const float z = samp_z(a, row, i);
-      if (samp_key(z) >= lim) c += samp_efix(z, kth, m);
+      c += kept(i, rank);
       if (c > target) {
         found = i;
         break;

@@ -459,8 +459,9 @@ def sample_tokens(logits: torch.Tensor, temperature: float, top_p: float = 1.0, 
     on the logits' device) - the randomness stays the caller's, as with
     torch.multinomial.  The top-p rule takes the tokens in the order of z
     (of two tokens of equal fp32 probability, whose order the reference's
-    sort leaves open, the larger z first); tokens whose z ties the top-p
-    boundary are all kept.
+    sort leaves open, the larger z first); of tokens whose z ties at the
+    top-p boundary, as many as the rule admits are kept, the first ones in
+    vocabulary order (a stable sort's order).
     A row with a NaN (or an infinite maximum after the division) gets -1, where
     the reference raises."""
     if logits.dtype != torch.float32 or not logits.is_cuda:

@@ -158,6 +158,59 @@ def test_sample_top_p_boundary_probability_ties(dev):
         assert _accept(xn[r], 1.0, 0, 0.3, float(us[r]), int(toks[r]))[1], r
 
 
+def _mid_uniforms(x, T, k, p, idx):
+    """For each token i in idx, the uniform at the middle of its interval of
+    the oracle's kept distribution (None where the token is not kept)."""
+    c = np.cumsum(oracle.sample_probs(x, T, k, p).astype(np.float64))
+    out = []
+    for i in idx:
+        lo = c[i - 1] if i > 0 else 0.0
+        out.append(None if c[i] == lo else float((lo + c[i]) / 2 / c[-1]))
+    return out
+
+
+@pytest.mark.parametrize("case", ["small", "topk", "slices"])
+def test_sample_top_p_boundary_z_ties(dev, case):
+    """Tokens of equal z at the top-p boundary: the reference's sort puts them
+    together and its rule (cumsum - p < top_p, engine.py:38-40) keeps only
+    the first of them that fit, in vocabulary order for a stable sort; the
+    kernel keeps the same first n.  Cases: four ties in six tokens with top_p
+    keeping two of them; the same with top-k's k-th value at the ties (top-k
+    keeps all four, top-p two); twenty ties spread over the workgroup slices
+    of a 50000-token row with top_p keeping seven.  Every tie top_p keeps is
+    drawn by a uniform at the middle of its interval, the dropped ones never,
+    and the tokens after them keep their intervals."""
+    announce(f"sample top-p boundary z ties {case}")
+    T = 1.0
+    if case in ("small", "topk"):
+        x = np.array([1.0, 0.3, 0.3, 2.0, 0.3, -1.0, 0.3], np.float32)
+        ties, keep_n, k = [1, 2, 4, 6], 2, (3 if case == "topk" else 0)
+    else:
+        rng = np.random.default_rng(21)
+        x = rng.standard_normal(50000).astype(np.float32)
+        ties = [i * 2400 + 7 for i in range(20)]
+        x[ties] = np.float32(1.25)
+        keep_n, k = 7, 0
+    full = oracle.sample_probs(x, T, k, 1.0)
+    pt = float(full[ties[0]])
+    above = float(full[full > pt].astype(np.float64).sum())
+    top_p = above + (keep_n - 0.5) * pt
+    kept = oracle.sample_probs(x, T, k, top_p)
+    assert [i for i in ties if kept[i] > 0] == ties[:keep_n]
+    others = [i for i in range(x.size) if kept[i] > 0 and i not in ties][:40]
+    probe = ties + others
+    us = _mid_uniforms(x, T, k, top_p, probe)
+    xd = torch.from_numpy(x).reshape(1, -1).to(dev)
+    for i, u0 in zip(probe, us):
+        if u0 is None:
+            continue
+        tok = int(_run(xd, T, k, top_p, torch.tensor([u0], dtype=torch.float32, device=dev))[0])
+        assert tok == i == oracle.sample_token(x, T, k, top_p, u0), (i, tok)
+    drawn = {int(_run(xd, T, k, top_p, torch.tensor([u0], dtype=torch.float32, device=dev))[0])
+             for u0 in np.linspace(0.0, 0.999, 97)}
+    assert not drawn & set(ties[keep_n:]), drawn & set(ties[keep_n:])
+
+
 def test_sample_strided_rows(dev):
     """Rows of a wider buffer (row stride above V) and one row viewed from a
     column (stride(0) below V): the same tokens as the contiguous copies."""
