@@ -157,6 +157,29 @@ __device__ __forceinline__ uint64_t samp_block_sum_u64(uint64_t v, uint64_t* red
   return s;
 }
 
+// Two block sums at once (one pair of barriers); red: 32 words.
+__device__ __forceinline__ void samp_block_sum2_u64(uint64_t& v0, uint64_t& v1, uint64_t* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    v0 += __shfl_xor(v0, o);
+    v1 += __shfl_xor(v1, o);
+  }
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[w] = v0;
+    red[16 + w] = v1;
+  }
+  __syncthreads();
+  uint64_t s0 = 0, s1 = 0;
+  for (int i = 0; i < nw; ++i) {
+    s0 += red[i];
+    s1 += red[16 + i];
+  }
+  __syncthreads();
+  v0 = s0;
+  v1 = s1;
+}
+
 // Sum of v over the G <= 64 lanes of one wave (exact), every lane the result.
 __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 #pragma unroll
@@ -389,12 +412,13 @@ __global__ __launch_bounds__(kSampThreads) void samp_soft_kernel(SampArgs a) {
 // sort puts them together (in vocabulary order: a stable sort) and its rule
 // keeps the j-th of them while the mass above it, A + j f, stays below
 // top_p: the first n = ceil((thr - A) / f) of them (A: the mass of the keys
-// above, the descent's rest).  They are counted per workgroup here and left
-// out of its mass; the draw adds f for each of the first n.
+// above, the descent's rest).  When n is below their count, they are counted
+// per workgroup here and left out of its mass, and the draw adds f for each
+// of the first n; otherwise all of them are kept, as every key above.
 __global__ __launch_bounds__(kSampThreads) void samp_bsum_kernel(SampArgs a) {
   __shared__ uint64_t H[1024];
   __shared__ SampState bcast;
-  __shared__ uint64_t red[16];
+  __shared__ uint64_t red[32];
   const float* row = a.x + (int64_t)blockIdx.y * a.ld;
   uint8_t* w = samp_row_ws(a);
   SampHead* h = (SampHead*)(w + SampRow::kHead);
@@ -407,32 +431,48 @@ __global__ __launch_bounds__(kSampThreads) void samp_bsum_kernel(SampArgs a) {
   const float m = h->m;
   const bool valid = h->valid != 0;
   const uint32_t lim = kth > tkey ? kth : tkey;
-  // the boundary key's tokens: mass f each, tmass in all (0: none kept by top-k)
-  const uint64_t tmass = last[tkey & 255u];
-  const uint64_t f = valid && tmass ? samp_efix(samp_unkey(tkey), kth, m) : 0;
   const int i0 = blockIdx.x * a.per, i1 = min(i0 + a.per, a.V);
-  uint64_t part = 0, ties = 0;
+  uint64_t part = 0, ties = 0;  // the mass of every kept key, the tokens of the boundary key
   if (valid)
     for (int i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
       const float z = samp_z(a, row, i);
       const uint32_t key = samp_key(z);
-      if (f && key == tkey)
-        ++ties;
-      else if (key >= lim)
-        part += samp_efix(z, kth, m);
+      ties += key == tkey;
+      if (key >= lim) part += samp_efix(z, kth, m);
     }
-  const uint64_t b = samp_block_sum_u64(part, red);
-  const uint64_t tc = samp_block_sum_u64(ties, red);
+  samp_block_sum2_u64(part, ties, red);
   if (threadIdx.x == 0) {
-    ((uint64_t*)(w + SampRow::kBsum))[blockIdx.x] = b;
-    ((int*)(w + SampRow::kTie))[blockIdx.x] = (int)tc;
-    if (blockIdx.x == 0) {
-      uint64_t n = 0;
-      if (f) {
-        const uint64_t cnt = tmass / f;  // every token of the key adds the same f
-        n = thr > fin.rest ? (thr - fin.rest + f - 1) / f : 0;  // >= 1: the boundary key qualifies
-        if (n > cnt) n = cnt;
+    // the boundary key's tokens: mass f0 each, tmass in all (0: none kept by
+    // top-k), from the pass-3 histogram the descent left in LDS (four
+    // partial sums per bin); the same decision in every workgroup
+    const uint32_t tb = tkey & 255u;
+    const uint64_t tmass = H[tb] + H[256 + tb] + H[512 + tb] + H[768 + tb];
+    const uint64_t f0 = valid && tmass ? samp_efix(samp_unkey(tkey), kth, m) : 0;
+    uint64_t n = 0, cnt = 0;
+    // one token (tmass == f0, the usual case) is kept whole; the quotients
+    // below are for a key of several tokens (thr > rest: the key qualifies)
+    if (f0 && tmass > f0 && thr > fin.rest) {
+      // cnt = tmass / f0 (every token of the key adds the same f0; an
+      // integer <= V, so the rounded double quotient is exact) and n =
+      // min(cnt, ceil(need / f0)): below tmass the quotient is < cnt, and
+      // its double estimate is corrected by at most one either way
+      cnt = (uint64_t)((double)tmass / (double)f0 + 0.5);
+      const uint64_t need = thr - fin.rest;
+      if (need >= tmass) {
+        n = cnt;
+      } else {
+        n = (uint64_t)ceil((double)need / (double)f0);
+        if (n > 0 && (n - 1) * f0 >= need) --n;
+        if (n * f0 < need) ++n;
       }
+    }
+    // only a boundary key that keeps part of its tokens is split off (usually
+    // it holds one token, which is kept): its tokens leave the slice's mass
+    // (each added f0 to it) and are counted instead
+    const uint64_t f = n < cnt ? f0 : 0;
+    ((uint64_t*)(w + SampRow::kBsum))[blockIdx.x] = f ? part - ties * f0 : part;
+    ((int*)(w + SampRow::kTie))[blockIdx.x] = f ? (int)ties : 0;
+    if (blockIdx.x == 0) {
       h->tkey = tkey;
       h->tie_f = f;
       h->tie_n = (int)n;
@@ -454,17 +494,18 @@ __global__ __launch_bounds__(kSampThreads) void samp_pick_kernel(SampArgs a, int
   const int row_i = blockIdx.y;
   const float* row = a.x + (int64_t)row_i * a.ld;
   const uint8_t* w = samp_row_ws(a);
-  const SampHead* h = (const SampHead*)(w + SampRow::kHead);
-  if (!h->valid) {
+  const SampHead hd = *(const SampHead*)(w + SampRow::kHead);  // the whole head in one load
+  if (!hd.valid) {
     if (threadIdx.x == 0) a.tokens[row_i] = -1;
     return;
   }
   const uint64_t* bsum = (const uint64_t*)(w + (use_bsum ? SampRow::kBsum : SampRow::kEsum));
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint64_t tf = use_bsum ? h->tie_f : 0;
-  const int tn = use_bsum ? h->tie_n : 0;
+  const uint64_t tf = use_bsum ? hd.tie_f : 0;
+  const int tn = use_bsum ? hd.tie_n : 0;
   // every wave: the boundary ties of the slices in lanes and their prefix ...
-  const int tc_g = tf && lane < a.G ? ((const int*)(w + SampRow::kTie))[lane] : 0;
+  const int tc_all = use_bsum && lane < a.G ? ((const int*)(w + SampRow::kTie))[lane] : 0;
+  const int tc_g = tf ? tc_all : 0;
   int tpre_g = tc_g;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -491,27 +532,12 @@ __global__ __launch_bounds__(kSampThreads) void samp_pick_kernel(SampArgs a, int
   const int g = over ? __ffsll((long long)over) - 1 : a.G - 1;
   target -= __shfl(pre_g - mine_g, g);  // within workgroup slice g
   const int trank0 = __shfl(tbefore_g, g);
-  const uint32_t kth = h->kth, tkey = h->tkey;
+  const uint32_t kth = hd.kth, tkey = hd.tkey;
   const uint32_t lim = kth > tkey ? kth : tkey;
-  const float m = h->m;
+  const float m = hd.m;
   const int i0 = g * a.per, i1 = min(i0 + a.per, a.V);
   const int e = (i1 - i0 + (int)blockDim.x - 1) / (int)blockDim.x;  // elements per thread
   const int t0 = i0 + threadIdx.x * e, t1 = min(t0 + e, i1);
-  // boundary ties of this thread's run, then their exclusive prefix over the threads
-  int myt = 0;
-  if (tf)
-    for (int i = t0; i < t1; ++i) myt += samp_key(samp_z(a, row, i)) == tkey;
-  int tincl = myt;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int v = __shfl_up(tincl, o);
-    if (lane >= o) tincl += v;
-  }
-  if (lane == 63) wtie[wv] = tincl;
-  __syncthreads();
-  int tbase = trank0;
-  for (int i = 0; i < wv; ++i) tbase += wtie[i];
-  const int rank0 = tbase + tincl - myt;  // rank of this run's first boundary tie
   // the kept mass of token i (rank: the boundary ties met so far)
   auto kept = [&](int i, int& rank) -> uint64_t {
     const float z = samp_z(a, row, i);
@@ -519,9 +545,32 @@ __global__ __launch_bounds__(kSampThreads) void samp_pick_kernel(SampArgs a, int
     if (tf && key == tkey) return rank++ < tn ? tf : 0;
     return key >= lim ? samp_efix(z, kth, m) : 0;
   };
+  // this thread's run: the mass of its other tokens and its boundary ties
   uint64_t mine = 0;
-  int rank = rank0;
-  for (int i = t0; i < t1; ++i) mine += kept(i, rank);
+  int myt = 0;
+  for (int i = t0; i < t1; ++i) {
+    const float z = samp_z(a, row, i);
+    const uint32_t key = samp_key(z);
+    if (tf && key == tkey)
+      ++myt;
+    else if (key >= lim)
+      mine += samp_efix(z, kth, m);
+  }
+  int rank0 = 0;  // rank of this run's first boundary tie
+  if (tf) {  // uniform: the row's head
+    int tincl = myt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(tincl, o);
+      if (lane >= o) tincl += v;
+    }
+    if (lane == 63) wtie[wv] = tincl;
+    __syncthreads();
+    int tbase = trank0;
+    for (int i = 0; i < wv; ++i) tbase += wtie[i];
+    rank0 = tbase + tincl - myt;
+    mine += tf * (uint64_t)min(max(tn - rank0, 0), myt);  // its ties below rank tn
+  }
   // inclusive scan within the wave, then the wave totals in wave order
   uint64_t incl = mine;
 #pragma unroll
@@ -538,7 +587,7 @@ __global__ __launch_bounds__(kSampThreads) void samp_pick_kernel(SampArgs a, int
   const uint64_t excl = incl - mine;
   if (excl <= target && target < incl) {
     uint64_t c = excl;
-    rank = rank0;
+    int rank = rank0;
     for (int i = t0; i < t1; ++i) {
       c += kept(i, rank);
       if (c > target) {
