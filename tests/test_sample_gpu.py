@@ -4,9 +4,9 @@ reference repository), with the same uniform for the draw.
 
 The kernel finds the top-k value and the top-p boundary by radix selection
 and sums probabilities in 2^-40 fixed point; the oracle sorts and sums in
-float64.  So a token may differ only where the oracle itself changes its
-answer under a perturbation of 2e-6 of the uniform or of top_p (a draw or a
-kept-set boundary that close), or where tokens of equal fp32 probability
+float64.  So a token may differ only where its interval of the kept mass
+comes within 2e-6 of the uniform's point, for top_p or 2e-6 beside it (a
+draw or a kept-set boundary that close), or where tokens of equal fp32 probability
 meet the top-p boundary: engine.py:38 sorts with probs.sort(descending=True),
 which leaves the order of equal values open; the oracle takes them in index
 order, the kernel in the order of z (larger first), and both are the
@@ -30,33 +30,53 @@ PARAMS = [  # (temperature, top_k, top_p): the engine's defaults first (engine.p
 DELTA = 2e-6
 
 
-def _token_ties_by_z(x, T, k, p, u):
-    """The oracle's draw with tokens of equal fp32 probability taken in the
-    order of z (larger first, then index) instead of index order when the
-    top-p rule walks the sorted probabilities (engine.py:38-40)."""
+def _probs_ties_by_z(x, T, k, p):
+    """The oracle's kept probabilities with tokens of equal fp32 probability
+    taken in the order of z (larger first, then index) instead of index order
+    when the top-p rule walks the sorted probabilities (engine.py:38-40)."""
     pf = oracle.sample_probs(x, T, k, 1.0)
+    if not 0 < p < 1:
+        return pf
     z = (np.asarray(x, np.float32) / np.float32(T)).astype(np.float32)
     order = np.lexsort((np.arange(z.size), -z, -pf))
     sp = pf[order]
     keep = (np.cumsum(sp.astype(np.float64)).astype(np.float32) - sp) < np.float32(p)
     kept = np.zeros_like(pf)
     kept[order] = sp * keep
-    c = np.cumsum(kept.astype(np.float64))
+    return kept
+
+
+def _token_ties_by_z(x, T, k, p, u):
+    """The draw from _probs_ties_by_z, as oracle.sample_token draws."""
+    c = np.cumsum(_probs_ties_by_z(x, T, k, p).astype(np.float64))
     return int(np.searchsorted(c, u * c[-1], side="right"))
 
 
+def _near_draw(probs, u, tok):
+    """tok is kept and its interval of the cumulative kept mass comes within
+    DELTA (of the kept mass) of the uniform's point u."""
+    if not 0 <= tok < probs.size or probs[tok] <= 0:
+        return False
+    c = np.cumsum(probs.astype(np.float64))
+    lo = c[tok - 1] if tok else 0.0
+    return lo <= (u + DELTA) * c[-1] and c[tok] > (u - DELTA) * c[-1]
+
+
 def _accept(x, T, k, p, u, tok):
-    """The oracle's token, and whether `tok` is acceptable: equal to it, to
-    the oracle's answer under a 2e-6 perturbation of u or top_p, or to the
-    draw with equal probabilities at the top-p boundary taken in z order."""
+    """The oracle's token, and whether `tok` is acceptable: equal to it, or a
+    kept token whose interval comes within 2e-6 of the uniform's point, for
+    top_p itself or 2e-6 beside it, with equal probabilities at the top-p
+    boundary in index or in z order."""
     want = oracle.sample_token(x, T, k, p, u)
     if tok == want:
         return want, True, False
-    alts = {oracle.sample_token(x, T, k, pp, uu) for uu in (max(u - DELTA, 0.0), u, min(u + DELTA, 1 - 1e-9))
-            for pp in ((p - DELTA, p, p + DELTA) if 0 < p < 1 else (p,))}
-    if want >= 0 and T > 0 and 0 < p < 1:
-        alts.add(_token_ties_by_z(x, T, k, p, u))
-    return want, tok in alts, True
+    if want < 0 or T <= 0:
+        return want, False, True
+    for pp in ((p - DELTA, p, p + DELTA) if 0 < p < 1 else (p,)):
+        for probs in (oracle.sample_probs(x, T, k, pp), _probs_ties_by_z(x, T, k, pp)):
+            if _near_draw(probs, u, tok):
+                return want, True, True
+    return want, False, True
 
 
 def _run(logits, T, k, p, u):
