@@ -503,17 +503,20 @@ __global__ __launch_bounds__(kSampThreads) void samp_pick_kernel(SampArgs a, int
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const uint64_t tf = use_bsum ? hd.tie_f : 0;
   const int tn = use_bsum ? hd.tie_n : 0;
-  // every wave: the boundary ties of the slices in lanes and their prefix ...
-  const int tc_all = use_bsum && lane < a.G ? ((const int*)(w + SampRow::kTie))[lane] : 0;
-  const int tc_g = tf ? tc_all : 0;
-  int tpre_g = tc_g;
+  // every wave, when the boundary key is split off (tf: uniform, the row's
+  // head): the boundary ties of the slices in lanes and their prefix ...
+  int tbefore_g = 0, tkeep_g = 0;  // ties in the slices before, ties the slice keeps
+  if (tf) {
+    const int tc_g = lane < a.G ? ((const int*)(w + SampRow::kTie))[lane] : 0;
+    int tpre_g = tc_g;
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int v = __shfl_up(tpre_g, o);
-    if (lane >= o) tpre_g += v;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(tpre_g, o);
+      if (lane >= o) tpre_g += v;
+    }
+    tbefore_g = tpre_g - tc_g;
+    tkeep_g = min(max(tn - tbefore_g, 0), tc_g);
   }
-  const int tbefore_g = tpre_g - tc_g;  // ties in the slices before
-  const int tkeep_g = min(max(tn - tbefore_g, 0), tc_g);
   // ... the slice masses, their inclusive prefix, the total
   const uint64_t mine_g = lane < a.G ? bsum[lane] + tf * (uint64_t)tkeep_g : 0;
   uint64_t pre_g = mine_g;
